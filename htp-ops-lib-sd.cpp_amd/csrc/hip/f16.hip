@@ -1,0 +1,250 @@
+// Packed-F16 GEMM with fused epilogue (opcodes 1 and 16) on gfx950.
+//
+// Contract (reference src/dsp/ops/mat_mul.c:937-1049):
+//   a = fp16(x) (RNE)                                       :114-148
+//   acc = sum_k a*W, FP32 accumulation on v_mfma_f32_16x16x32_f16
+//   v = (float)fp16(acc) -- the HMX readout is an fp16 tile  :724-778
+//   mode 0: v + bias; 1: GELU(v + bias); 2: QuickGELU(v + bias);
+//   mode 3: v + bias stored channel-major y[c][m], c < channels  :788-882
+// The fp32->fp16 activation conversion is fused into the A-tile staging.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "hb_internal.h"
+
+namespace {
+
+constexpr int kFragBytes = 1024;  // 16 x 32 fp16 operand tile, lane-ordered
+constexpr int kStageK = 64;       // k per LDS stage (two MFMA k-steps)
+
+// ---------------------------------------------------------------------------
+// Permuted reference layout -> MFMA tile image.
+// ---------------------------------------------------------------------------
+
+__global__ __launch_bounds__(256) void f16_prepack(uint4 *__restrict__ packed, const uint16_t *__restrict__ perm,
+                                                  int k, int n) {
+  const size_t slots = (size_t)n * (size_t)k / 8u;
+  const int kblocks = k / 32;
+  for (size_t slot = (size_t)blockIdx.x * blockDim.x + threadIdx.x; slot < slots;
+       slot += (size_t)gridDim.x * blockDim.x) {
+    const size_t blk = slot / 64u;
+    const int lane = (int)(slot % 64u);
+    const int nb = (int)(blk / (size_t)kblocks), kb = (int)(blk % (size_t)kblocks);
+    const int col = nb * 16 + lane % 16;
+    const int k0 = kb * 32 + (lane / 16) * 8;
+    uint32_t w[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int kk = k0 + 2 * g;  // even: (kk, kk+1) are adjacent in the permuted layout
+      const size_t idx = ((size_t)(col / 32) * (size_t)kblocks + (size_t)(kk / 32)) * 1024u +
+                         (size_t)((kk % 32) / 2) * 64u + (size_t)(col % 32) * 2u;
+      w[g] = *(const uint32_t *)(perm + idx);
+    }
+    packed[slot] = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Epilogue activations (reference src/dsp/ops/mat_mul.c:788-826): stable
+// sigmoid with e = 2^max(-|a|*log2(e), -126).
+// ---------------------------------------------------------------------------
+
+__device__ inline float stable_sigmoid(float a) {
+  const float neg = fmaxf(__fmul_rn(fabsf(a), -1.4426950408889634f), -126.0f);
+  const float e = exp2f(neg);
+  const float inv = __fdiv_rn(1.0f, __fadd_rn(e, 1.0f));
+  return a < 0.0f ? __fmul_rn(e, inv) : inv;
+}
+
+__device__ inline float apply_mode(float z, int mode) {
+  if (mode == 1) {
+    const float cubic = __fmul_rn(__fmul_rn(z, z), z);
+    const float inner = __fadd_rn(z, __fmul_rn(cubic, 0.044715f));
+    return __fmul_rn(z, stable_sigmoid(__fmul_rn(inner, 1.5957691216057308f)));
+  }
+  if (mode == 2) return __fmul_rn(z, stable_sigmoid(__fmul_rn(z, 1.702f)));
+  return z;
+}
+
+// ---------------------------------------------------------------------------
+// Tiled GEMM: BM x BN tile per workgroup of WM x WN waves; LDS double buffer
+// of 64-k stages; A converted fp32 -> fp16 while staging.
+// ---------------------------------------------------------------------------
+
+template <int BM, int BN, int WM, int WN>
+__global__ __launch_bounds__(64 * WM *WN) void f16_gemm_tiles(float *__restrict__ y, const float *__restrict__ x,
+                                                              const uint16_t *__restrict__ packed,
+                                                              const float *__restrict__ bias, int m, int k, int n,
+                                                              int channels, int mode) {
+  constexpr int NT = 64 * WM * WN;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int FM = WTM / 16, FN = WTN / 16;
+  constexpr int A_BYTES = BM * kStageK * 2, B_BYTES = BN * kStageK * 2;
+  constexpr int A_CH = BM * 8 / NT;  // 8 fp16 (one 16-byte slot) per chunk
+  constexpr int B_CH = B_BYTES / 16 / NT;
+  static_assert(A_CH * NT == BM * 8 && B_CH * 16 * NT == B_BYTES, "tile/thread mismatch");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2][A_BYTES + B_BYTES];
+
+  const int tiles_n = (n + BN - 1) / BN;
+  const int tm = blockIdx.x / tiles_n, tn = blockIdx.x % tiles_n;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int kblocks = k / 32;
+  const int stages = (k + kStageK - 1) / kStageK;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int wm = wave / WN, wn = wave % WN;
+
+  const float *a_src[A_CH];
+  int a_dst[A_CH], a_k[A_CH];
+#pragma unroll
+  for (int i = 0; i < A_CH; ++i) {
+    const int c = tid + NT * i;
+    const int row = c >> 3, kc = c & 7;  // kc: 8-element chunk within the 64-k stage
+    const int grow = min(m0 + row, m - 1);
+    a_src[i] = x + (size_t)grow * k + kc * 8;
+    a_k[i] = kc * 8;
+    a_dst[i] = ((row >> 4) * 2 + (kc >> 2)) * kFragBytes + ((row & 15) + 16 * (kc & 3)) * 16;
+  }
+  const uint16_t *b_src[B_CH];
+  int b_dst[B_CH], b_kb[B_CH];
+  const int nblocks = n / 16;
+#pragma unroll
+  for (int i = 0; i < B_CH; ++i) {
+    const int c = tid + NT * i;
+    const int blk = c >> 7, rem = c & 127;
+    const int kb2 = rem >> 6, slot = rem & 63;
+    const int gnb = min(n0 / 16 + blk, nblocks - 1);
+    b_src[i] = packed + ((size_t)gnb * kblocks + kb2) * 512u + slot * 8;
+    b_kb[i] = kb2;
+    b_dst[i] = A_BYTES + (blk * 2 + kb2) * kFragBytes + slot * 16;
+  }
+
+  uint4 ra[A_CH], rb[B_CH];
+  auto load = [&](int st) {
+    const int kbase = st * kStageK;
+#pragma unroll
+    for (int i = 0; i < A_CH; ++i) {
+      if (kbase + a_k[i] < k) {
+        const float4 lo = *(const float4 *)(a_src[i] + kbase);
+        const float4 hi = *(const float4 *)(a_src[i] + kbase + 4);
+        hb_f16x8 h = {(_Float16)lo.x, (_Float16)lo.y, (_Float16)lo.z, (_Float16)lo.w,
+                      (_Float16)hi.x, (_Float16)hi.y, (_Float16)hi.z, (_Float16)hi.w};
+        ra[i] = *(const uint4 *)&h;
+      } else {
+        ra[i] = make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < B_CH; ++i) {
+      const int kb = st * 2 + b_kb[i];
+      rb[i] = kb < kblocks ? *(const uint4 *)(b_src[i] + (size_t)st * 2u * 512u) : make_uint4(0u, 0u, 0u, 0u);
+    }
+  };
+  auto stash = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < A_CH; ++i) *(uint4 *)(&lds[buf][a_dst[i]]) = ra[i];
+#pragma unroll
+    for (int i = 0; i < B_CH; ++i) *(uint4 *)(&lds[buf][b_dst[i]]) = rb[i];
+  };
+
+  hb_f32x4 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = hb_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  load(0);
+  stash(0);
+  __syncthreads();
+  for (int st = 0; st < stages; ++st) {
+    const int cur = st & 1;
+    if (st + 1 < stages) load(st + 1);
+#pragma unroll
+    for (int kb2 = 0; kb2 < 2; ++kb2) {
+      hb_f16x8 bf[FN];
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        bf[j] = *(const hb_f16x8 *)(&lds[cur][A_BYTES + ((wn * FN + j) * 2 + kb2) * kFragBytes + lane * 16]);
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const hb_f16x8 af = *(const hb_f16x8 *)(&lds[cur][((wm * FM + i) * 2 + kb2) * kFragBytes + lane * 16]);
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[j], acc[i][j], 0, 0, 0);
+      }
+    }
+    if (st + 1 < stages) stash(cur ^ 1);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int col = n0 + wn * WTN + j * 16 + (lane & 15);
+    const int limit = mode == 3 ? channels : n;
+    if (col >= limit) continue;
+    const float b = bias ? bias[col] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = m0 + wm * WTM + i * 16 + (lane >> 4) * 4 + r;
+        if (row >= m) continue;
+        const float v = (float)(_Float16)acc[i][j][r];
+        const float z = bias ? __fadd_rn(v, b) : v;
+        if (mode == 3) {
+          y[(size_t)col * m + row] = z;
+        } else {
+          y[(size_t)row * n + col] = apply_mode(z, mode);
+        }
+      }
+    }
+  }
+}
+
+bool aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+size_t hb_f16_packed_bytes(int k, int n) {
+  if (k <= 0 || n <= 0) return 0;
+  return (size_t)k * (size_t)n * 2u;
+}
+
+int hb_f16_prepack(uint16_t *d_packed, const uint16_t *d_permuted, int k, int n, hb_stream s) {
+  if (!d_packed || !d_permuted) return hb_invalid("hb_f16_prepack null pointer");
+  if (k < 32 || k % 32 || n < 32 || n % 32) return hb_invalid("hb_f16_prepack shape");
+  if (!aligned(d_permuted, 4) || !aligned(d_packed, 16)) return hb_invalid("hb_f16_prepack alignment");
+  const size_t slots = (size_t)n * k / 8u;
+  const int grid = (int)((slots + 255) / 256 < 65536 ? (slots + 255) / 256 : 65536);
+  hipLaunchKernelGGL(f16_prepack, dim3(grid), dim3(256), 0, hb_resolve_stream(s), (uint4 *)d_packed, d_permuted, k,
+                     n);
+  return hb_check_launch("f16_prepack");
+}
+
+int hb_f16_gemm(float *d_y, const float *d_x, const uint16_t *d_packed, const float *d_bias, int m, int k, int n,
+                int channels, int mode, hb_stream s) {
+  if (!d_y || !d_x || !d_packed) return hb_invalid("hb_f16_gemm null pointer");
+  if (m < 1 || k < 32 || k % 32 || n < 32 || n % 32 || channels < 1 || channels > n || mode < 0 || mode > 3 ||
+      (mode != 3 && channels != n))
+    return hb_invalid("hb_f16_gemm shape/mode");
+  if (!aligned(d_x, 16) || !aligned(d_packed, 16) || !aligned(d_y, 4) || (d_bias && !aligned(d_bias, 4)))
+    return hb_invalid("hb_f16_gemm alignment");
+  hipStream_t st = hb_resolve_stream(s);
+  const long long big = ((m + 127) / 128) * (long long)((n + 127) / 128);
+  const long long mid = ((m + 63) / 64) * (long long)((n + 63) / 64);
+  if (big >= 256) {
+    hipLaunchKernelGGL((f16_gemm_tiles<128, 128, 2, 2>), dim3((int)big), dim3(256), 0, st, d_y, d_x, d_packed, d_bias,
+                       m, k, n, channels, mode);
+  } else if (mid >= 128) {
+    hipLaunchKernelGGL((f16_gemm_tiles<64, 64, 2, 2>), dim3((int)mid), dim3(256), 0, st, d_y, d_x, d_packed, d_bias,
+                       m, k, n, channels, mode);
+  } else {
+    const int grid = ((m + 31) / 32) * ((n + 31) / 32);
+    hipLaunchKernelGGL((f16_gemm_tiles<32, 32, 2, 2>), dim3(grid), dim3(256), 0, st, d_y, d_x, d_packed, d_bias, m,
+                       k, n, channels, mode);
+  }
+  return hb_check_launch("f16_gemm_tiles");
+}
+
+}  // extern "C"

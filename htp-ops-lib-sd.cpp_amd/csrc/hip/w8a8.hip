@@ -1,0 +1,567 @@
+// W8A8 linear (opcode 15) on gfx950: weight prepack, per-token activation
+// quantization and the INT8 MFMA GEMM with its fused output epilogue.
+//
+// Arithmetic contract (reference src/dsp/ops/linear_w8a8.c):
+//   t = x*inv; s = max(max|t|/127, 1e-12); r = 1/s;                 :34-40, :83-109
+//   u = rne(clamp(t*r + 128, 1, 255))  (clamp on IEEE bits)          :42-59
+//   acc = sum_k u*W(n,k) (int32);  c = acc - (sums[n] << 7) (wrap)   :478-502, :159-171
+//   y = ((float)c * sw[n]) * s[m]                                    :172-179
+// Every float step is one IEEE RNE operation (no contraction).  The GEMM
+// multiplies signed q = u - 128 by W and adds delta[n] = 128*(sum_k W - sums[n]),
+// which equals acc - (sums << 7) modulo 2^32 for every input.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "hb_internal.h"
+
+namespace {
+
+constexpr int kKStep = 64;        // k per v_mfma_i32_16x16x64_i8
+constexpr int kFragBytes = 1024;  // one 16 x 64 int8 operand tile, lane-ordered
+
+size_t kp_of(int k) { return hb_round_up((size_t)k, 64); }
+size_t mp_of(int m) { return hb_round_up((size_t)m, 16); }
+
+// ---------------------------------------------------------------------------
+// Prepack: constants blob -> MFMA tile image.
+// ---------------------------------------------------------------------------
+
+__device__ inline size_t blob_weight_offset(int k, int col, int kk) {
+  // W(n,k) address in the blob (reference linear_w8a8.c:453,482,486-488;
+  // tests/hmx-probe/study_dsp.c:82-84); kk is a multiple of 4.
+  return 128u + (size_t)(col / 64) * 64u * (size_t)k + (size_t)(kk / 32) * 2048u +
+         (size_t)((col % 64) / 32) * 1024u + (size_t)((kk % 32) / 4) * 128u + (size_t)(col % 32) * 4u;
+}
+
+__global__ __launch_bounds__(256) void w8a8_prepack_weights(uint4 *__restrict__ wpack,
+                                                           const uint8_t *__restrict__ blob, int k, int n,
+                                                           int kp) {
+  const size_t slots = (size_t)n * (size_t)kp / 16u;
+  const int kblocks = kp / kKStep;
+  for (size_t slot = (size_t)blockIdx.x * blockDim.x + threadIdx.x; slot < slots;
+       slot += (size_t)gridDim.x * blockDim.x) {
+    const size_t blk = slot / 64u;
+    const int lane = (int)(slot % 64u);
+    const int nb = (int)(blk / (size_t)kblocks), kb = (int)(blk % (size_t)kblocks);
+    const int col = nb * 16 + lane % 16;
+    const int k0 = kb * kKStep + (lane / 16) * 16;
+    uint32_t w[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int kk = k0 + g * 4;
+      w[g] = kk < k ? *(const uint32_t *)(blob + blob_weight_offset(k, col, kk)) : 0u;
+    }
+    wpack[slot] = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+__global__ __launch_bounds__(256) void w8a8_prepack_columns(float *__restrict__ sw_out, int32_t *__restrict__ delta,
+                                                           int32_t *__restrict__ wsum128,
+                                                           float *__restrict__ inv_out,
+                                                           const uint8_t *__restrict__ blob, int k, int n,
+                                                           int kp) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t kn = (size_t)k * (size_t)n;
+  if (t < n) {
+    int32_t sum = 0;
+    for (int kk = 0; kk < k; kk += 4) {
+      const uint32_t w = *(const uint32_t *)(blob + blob_weight_offset(k, t, kk));
+      sum += (int32_t)(int8_t)(w & 0xffu) + (int32_t)(int8_t)((w >> 8) & 0xffu) +
+             (int32_t)(int8_t)((w >> 16) & 0xffu) + (int32_t)(int8_t)(w >> 24);
+    }
+    const float sw = *(const float *)(blob + 128u + kn + 4u * (size_t)t);
+    const int32_t sums = *(const int32_t *)(blob + 128u + kn + 4u * (size_t)n + 4u * (size_t)t);
+    sw_out[t] = sw;
+    wsum128[t] = (int32_t)((uint32_t)sum << 7);
+    delta[t] = (int32_t)(((uint32_t)sum - (uint32_t)sums) << 7);
+  }
+  if (t < kp) {
+    inv_out[t] = t < k ? *(const float *)(blob + 128u + kn + 8u * (size_t)n + 4u * (size_t)t) : 0.0f;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Activation quantization: one wave per row, four rows per workgroup.
+// ---------------------------------------------------------------------------
+
+__device__ inline float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// u = rne(clamp(v, 1, 255)) with the clamp on the IEEE bits as signed
+// integers, returned as q = u - 128 in the low byte.
+__device__ inline uint32_t quantize_byte(float t, float r) {
+  const float v = __fadd_rn(__fmul_rn(t, r), 128.0f);
+  int32_t b = __float_as_int(v);
+  b = max(b, 0x3f800000);  // 1.0f
+  b = min(b, 0x437f0000);  // 255.0f
+  const int32_t u = (int32_t)rintf(__int_as_float(b));
+  return (uint32_t)(u - 128) & 0xffu;
+}
+
+// NV float4 vectors per lane stay in registers (row length k <= 256*NV).
+template <int NV>
+__global__ __launch_bounds__(256) void w8a8_quant_rows_reg(int8_t *__restrict__ q, float *__restrict__ scales,
+                                                          const float *__restrict__ x,
+                                                          const float *__restrict__ inv, int m, int k, int kp) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= m) return;
+  const float4 *xr = (const float4 *)(x + (size_t)row * k);
+  const float4 *iv = (const float4 *)inv;
+  const int nvec = k / 4;
+  float4 t[NV];
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int idx = lane + 64 * j;
+    if (idx < nvec) {
+      const float4 a = xr[idx];
+      const float4 b = iv[idx];
+      t[j] = make_float4(__fmul_rn(a.x, b.x), __fmul_rn(a.y, b.y), __fmul_rn(a.z, b.z), __fmul_rn(a.w, b.w));
+      amax = fmaxf(amax, fmaxf(fmaxf(fabsf(t[j].x), fabsf(t[j].y)), fmaxf(fabsf(t[j].z), fabsf(t[j].w))));
+    }
+  }
+  amax = wave_max(amax);
+  const float s = fmaxf(__fdiv_rn(amax, 127.0f), 1e-12f);
+  const float r = __fdiv_rn(1.0f, s);
+  if (lane == 0) scales[row] = s;
+  uint32_t *qr = (uint32_t *)(q + (size_t)row * kp);
+  const int qvec = kp / 4;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int idx = lane + 64 * j;
+    if (idx < nvec) {
+      qr[idx] = quantize_byte(t[j].x, r) | (quantize_byte(t[j].y, r) << 8) | (quantize_byte(t[j].z, r) << 16) |
+                (quantize_byte(t[j].w, r) << 24);
+    } else if (idx < qvec) {
+      qr[idx] = 0u;
+    }
+  }
+}
+
+// Any row length and 4-byte aligned pointers: two passes over the row
+// (the second pass re-reads x from cache and recomputes the same t).
+__global__ __launch_bounds__(256) void w8a8_quant_rows_any(int8_t *__restrict__ q, float *__restrict__ scales,
+                                                          const float *__restrict__ x,
+                                                          const float *__restrict__ inv, int m, int k, int kp) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= m) return;
+  const float *xr = x + (size_t)row * k;
+  float amax = 0.0f;
+  for (int i = lane; i < k; i += 64) amax = fmaxf(amax, fabsf(__fmul_rn(xr[i], inv[i])));
+  amax = wave_max(amax);
+  const float s = fmaxf(__fdiv_rn(amax, 127.0f), 1e-12f);
+  const float r = __fdiv_rn(1.0f, s);
+  if (lane == 0) scales[row] = s;
+  uint8_t *qr = (uint8_t *)(q + (size_t)row * kp);
+  for (int i = lane; i < kp; i += 64) qr[i] = i < k ? (uint8_t)quantize_byte(__fmul_rn(xr[i], inv[i]), r) : 0u;
+}
+
+// ---------------------------------------------------------------------------
+// Output epilogue shared by both GEMM kernels.
+// ---------------------------------------------------------------------------
+
+__device__ inline float gelu_tanh(float z) {
+  // z * sigmoid(1.5957691216057308*(z + 0.044715*z^3)), stable sigmoid
+  // (reference src/dsp/ops/mat_mul.c:788-826, mode 1).
+  const float cubic = __fmul_rn(__fmul_rn(z, z), z);
+  const float inner = __fadd_rn(z, __fmul_rn(cubic, 0.044715f));
+  const float a = __fmul_rn(inner, 1.5957691216057308f);
+  const float neg = fmaxf(__fmul_rn(fabsf(a), -1.4426950408889634f), -126.0f);
+  const float e = exp2f(neg);
+  const float inv = __fdiv_rn(1.0f, __fadd_rn(e, 1.0f));
+  const float sig = a < 0.0f ? __fmul_rn(e, inv) : inv;
+  return __fmul_rn(z, sig);
+}
+
+template <int EPI>
+__device__ inline void store_result(void *y, int ldy, int row, int col, int32_t acc, int32_t corr, float sw,
+                                    float s) {
+  const size_t idx = (size_t)row * (size_t)ldy + (size_t)col;
+  if (EPI == HB_W8A8_EPI_RAW) {
+    __builtin_nontemporal_store((int32_t)((uint32_t)acc + (uint32_t)corr), (int32_t *)y + idx);
+  } else {
+    const int32_t c = (int32_t)((uint32_t)acc + (uint32_t)corr);
+    float v = __fmul_rn(__fmul_rn((float)c, sw), s);
+    if (EPI == HB_W8A8_EPI_SCALE_GELU) v = gelu_tanh(v);
+    __builtin_nontemporal_store(v, (float *)y + idx);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Tiled GEMM: BM x BN output tile per workgroup of WM x WN waves, k-step 64,
+// operands staged through double-buffered LDS in MFMA lane order.
+// A = q int8 [mp][kp] row-major; B = packed tiles (see hb.h).
+// ---------------------------------------------------------------------------
+
+template <int BM, int BN, int WM, int WN, int EPI>
+__global__ __launch_bounds__(64 * WM *WN) void w8a8_gemm_tiles(void *__restrict__ y, int ldy,
+                                                               const int8_t *__restrict__ q,
+                                                               const float *__restrict__ scales,
+                                                               const int8_t *__restrict__ wpack,
+                                                               const float *__restrict__ sw,
+                                                               const int32_t *__restrict__ corr, int m, int n,
+                                                               int kp) {
+  constexpr int NT = 64 * WM * WN;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int FM = WTM / 16, FN = WTN / 16;
+  constexpr int A_BYTES = BM * kKStep, B_BYTES = BN * kKStep;
+  constexpr int A_CH = A_BYTES / 16 / NT, B_CH = B_BYTES / 16 / NT;
+  static_assert(A_CH * 16 * NT == A_BYTES && B_CH * 16 * NT == B_BYTES, "tile/thread mismatch");
+  __shared__ __attribute__((aligned(16))) int8_t lds[2][A_BYTES + B_BYTES];
+
+  const int tiles_n = (n + BN - 1) / BN;
+  const int tm = blockIdx.x / tiles_n, tn = blockIdx.x % tiles_n;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int kt_count = kp / kKStep;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int wm = wave / WN, wn = wave % WN;
+
+  // Global sources and LDS destinations of this thread's 16-byte chunks.
+  const int8_t *a_src[A_CH];
+  int a_dst[A_CH];
+#pragma unroll
+  for (int i = 0; i < A_CH; ++i) {
+    const int c = tid + NT * i;
+    const int row = c >> 2, kc = c & 3;
+    const int grow = min(m0 + row, m - 1);
+    a_src[i] = q + (size_t)grow * kp + kc * 16;
+    a_dst[i] = (row >> 4) * kFragBytes + ((row & 15) + 16 * kc) * 16;
+  }
+  const int8_t *b_src[B_CH];
+  int b_dst[B_CH];
+  const int nblocks = n / 16;
+#pragma unroll
+  for (int i = 0; i < B_CH; ++i) {
+    const int c = tid + NT * i;
+    const int blk = c >> 6, slot = c & 63;
+    const int gnb = min(n0 / 16 + blk, nblocks - 1);
+    b_src[i] = wpack + (size_t)gnb * kt_count * kFragBytes + slot * 16;
+    b_dst[i] = A_BYTES + blk * kFragBytes + slot * 16;
+  }
+
+  uint4 ra[A_CH], rb[B_CH];
+  auto load = [&](int kt) {
+#pragma unroll
+    for (int i = 0; i < A_CH; ++i) ra[i] = *(const uint4 *)(a_src[i] + (size_t)kt * kKStep);
+#pragma unroll
+    for (int i = 0; i < B_CH; ++i) rb[i] = *(const uint4 *)(b_src[i] + (size_t)kt * kFragBytes);
+  };
+  auto stash = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < A_CH; ++i) *(uint4 *)(&lds[buf][a_dst[i]]) = ra[i];
+#pragma unroll
+    for (int i = 0; i < B_CH; ++i) *(uint4 *)(&lds[buf][b_dst[i]]) = rb[i];
+  };
+
+  hb_i32x4 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = hb_i32x4{0, 0, 0, 0};
+
+  load(0);
+  stash(0);
+  __syncthreads();
+  for (int kt = 0; kt < kt_count; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < kt_count) load(kt + 1);
+    const int8_t *la = &lds[cur][(wm * FM) * kFragBytes + lane * 16];
+    const int8_t *lb = &lds[cur][A_BYTES + (wn * FN) * kFragBytes + lane * 16];
+    hb_i32x4 bf[FN];
+#pragma unroll
+    for (int j = 0; j < FN; ++j) bf[j] = *(const hb_i32x4 *)(lb + j * kFragBytes);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const hb_i32x4 af = *(const hb_i32x4 *)(la + i * kFragBytes);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf[j], acc[i][j], 0, 0, 0);
+    }
+    if (kt + 1 < kt_count) stash(cur ^ 1);
+    __syncthreads();
+  }
+
+  // Epilogue in registers: lane holds rows 4*(lane/16)+r, column lane%16 of each 16x16 block.
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int col = n0 + wn * WTN + j * 16 + (lane & 15);
+    if (col >= n) continue;
+    const int32_t cc = corr[col];
+    const float sc = sw[col];
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = m0 + wm * WTM + i * 16 + (lane >> 4) * 4 + r;
+        if (row < m) store_result<EPI>(y, ldy, row, col, acc[i][j][r], cc, sc, EPI == HB_W8A8_EPI_RAW ? 0.0f : scales[row]);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Small-M (decode) GEMM, m <= 16: one workgroup per 16-column block streams
+// that block's packed weights once; WAVES waves split K, each keeping U
+// one-kilobyte weight loads in flight.  Integer partial sums are combined in
+// LDS, so the result is independent of the split.
+// ---------------------------------------------------------------------------
+
+template <int WAVES, int U, int EPI>
+__global__ __launch_bounds__(64 * WAVES) void w8a8_gemm_decode(void *__restrict__ y, int ldy,
+                                                               const int8_t *__restrict__ q,
+                                                               const float *__restrict__ scales,
+                                                               const int8_t *__restrict__ wpack,
+                                                               const float *__restrict__ sw,
+                                                               const int32_t *__restrict__ corr, int m, int n,
+                                                               int kp) {
+  __shared__ hb_i32x4 part[WAVES][64];
+  const int nb = blockIdx.x;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int kt_count = kp / kKStep;
+  const int8_t *wb = wpack + (size_t)nb * kt_count * kFragBytes + lane * 16;
+  const int arow = lane & 15;
+  const bool has_row = arow < m;
+  const int8_t *qa = q + (size_t)arow * kp + (lane >> 4) * 16;
+
+  hb_i32x4 acc = {0, 0, 0, 0};
+  for (int kt0 = wave * U; kt0 < kt_count; kt0 += WAVES * U) {
+    hb_i32x4 b[U], a[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int kt = kt0 + u;
+      const bool ok = kt < kt_count;
+      b[u] = ok ? *(const hb_i32x4 *)(wb + (size_t)kt * kFragBytes) : hb_i32x4{0, 0, 0, 0};
+      a[u] = (ok && has_row) ? *(const hb_i32x4 *)(qa + (size_t)kt * kKStep) : hb_i32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[u], b[u], acc, 0, 0, 0);
+  }
+  part[wave][lane] = acc;
+  __syncthreads();
+  if (wave != 0) return;
+  hb_i32x4 total = part[0][lane];
+#pragma unroll
+  for (int w = 1; w < WAVES; ++w) {
+    const hb_i32x4 p = part[w][lane];
+    total = hb_i32x4{(int)((uint32_t)total[0] + (uint32_t)p[0]), (int)((uint32_t)total[1] + (uint32_t)p[1]),
+                     (int)((uint32_t)total[2] + (uint32_t)p[2]), (int)((uint32_t)total[3] + (uint32_t)p[3])};
+  }
+  const int col = nb * 16 + (lane & 15);
+  const int32_t cc = corr[col];
+  const float sc = sw[col];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int row = (lane >> 4) * 4 + r;
+    if (row < m) store_result<EPI>(y, ldy, row, col, total[r], cc, sc, EPI == HB_W8A8_EPI_RAW ? 0.0f : scales[row]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Raw accumulator -> byte-plane export of the CPU-control variant.
+// One thread per output byte position (row, 32-column half, byte in 128).
+// ---------------------------------------------------------------------------
+
+__global__ __launch_bounds__(256) void w8a8_planes(uint8_t *__restrict__ out, const int32_t *__restrict__ raw, int m,
+                                                  int n) {
+  const size_t total = (size_t)m * (size_t)n * 4u;
+  for (size_t pos = (size_t)blockIdx.x * blockDim.x + threadIdx.x; pos < total;
+       pos += (size_t)gridDim.x * blockDim.x) {
+    const size_t row = pos / ((size_t)n * 4u);
+    const int byte_in_row = (int)(pos % ((size_t)n * 4u));
+    const int n0 = (byte_in_row / 128) * 32;
+    const int within = byte_in_row % 128;
+    const int tile = (int)(row / 64u);
+    const int rows = m - tile * 64 < 64 ? m - tile * 64 : 64;
+    const size_t flat = (row - (size_t)tile * 64u) * 128u + (size_t)within;
+    const int p = (int)(flat / ((size_t)rows * 32u));
+    const size_t rem = flat % ((size_t)rows * 32u);
+    const int r = (int)(rem / 32u), c = (int)(rem % 32u);
+    const uint32_t v = (uint32_t)raw[(size_t)(tile * 64 + r) * n + n0 + c];
+    out[pos] = (uint8_t)(v >> (8 * p));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host-side dispatch.
+// ---------------------------------------------------------------------------
+
+struct TileShape {
+  int bm, bn;
+};
+
+template <int EPI>
+int launch_tiles(void *y, int ldy, const int8_t *q, const float *scales, const int8_t *wpack, const float *sw,
+                 const int32_t *corr, int m, int n, int kp, hipStream_t st) {
+  const long long big_tiles = ((m + 255) / 256) * (long long)((n + 255) / 256);
+  const long long mid_tiles = ((m + 127) / 128) * (long long)((n + 127) / 128);
+  if (big_tiles >= 256) {
+    const int grid = (int)big_tiles;
+    hipLaunchKernelGGL((w8a8_gemm_tiles<256, 256, 2, 4, EPI>), dim3(grid), dim3(512), 0, st, y, ldy, q, scales,
+                       wpack, sw, corr, m, n, kp);
+  } else if (mid_tiles >= 256) {
+    const int grid = (int)mid_tiles;
+    hipLaunchKernelGGL((w8a8_gemm_tiles<128, 128, 2, 2, EPI>), dim3(grid), dim3(256), 0, st, y, ldy, q, scales,
+                       wpack, sw, corr, m, n, kp);
+  } else {
+    const int grid = ((m + 63) / 64) * ((n + 63) / 64);
+    hipLaunchKernelGGL((w8a8_gemm_tiles<64, 64, 2, 2, EPI>), dim3(grid), dim3(256), 0, st, y, ldy, q, scales, wpack,
+                       sw, corr, m, n, kp);
+  }
+  return hb_check_launch("w8a8_gemm_tiles");
+}
+
+template <int EPI>
+int launch_decode(void *y, int ldy, const int8_t *q, const float *scales, const int8_t *wpack, const float *sw,
+                  const int32_t *corr, int m, int n, int kp, hipStream_t st) {
+  const int nblocks = n / 16;
+  if (nblocks >= 2048) {
+    hipLaunchKernelGGL((w8a8_gemm_decode<4, 8, EPI>), dim3(nblocks), dim3(256), 0, st, y, ldy, q, scales, wpack, sw,
+                       corr, m, n, kp);
+  } else if (nblocks >= 512) {
+    hipLaunchKernelGGL((w8a8_gemm_decode<8, 8, EPI>), dim3(nblocks), dim3(512), 0, st, y, ldy, q, scales, wpack,
+                       sw, corr, m, n, kp);
+  } else {
+    hipLaunchKernelGGL((w8a8_gemm_decode<16, 4, EPI>), dim3(nblocks), dim3(1024), 0, st, y, ldy, q, scales, wpack,
+                       sw, corr, m, n, kp);
+  }
+  return hb_check_launch("w8a8_gemm_decode");
+}
+
+template <int EPI>
+int launch_gemm(void *y, int ldy, const int8_t *q, const float *scales, const int8_t *wpack, const float *sw,
+                const int32_t *corr, int m, int n, int kp, hipStream_t st) {
+  if (m <= 16) return launch_decode<EPI>(y, ldy, q, scales, wpack, sw, corr, m, n, kp, st);
+  return launch_tiles<EPI>(y, ldy, q, scales, wpack, sw, corr, m, n, kp, st);
+}
+
+bool aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+size_t hb_w8a8_packed_offset(int k, int n, int section) {
+  if (k <= 0 || n <= 0) return 0;
+  const size_t kp = kp_of(k);
+  const size_t w = hb_round_up((size_t)n * kp, 256);
+  const size_t vec = hb_round_up((size_t)n * 4u, 256);
+  switch (section) {
+    case HB_W8A8_WEIGHTS: return 0;
+    case HB_W8A8_SW: return w;
+    case HB_W8A8_DELTA: return w + vec;
+    case HB_W8A8_WSUM128: return w + 2 * vec;
+    case HB_W8A8_INV: return w + 3 * vec;
+    default: return 0;
+  }
+}
+
+size_t hb_w8a8_packed_bytes(int k, int n) {
+  if (k <= 0 || n <= 0) return 0;
+  return hb_w8a8_packed_offset(k, n, HB_W8A8_INV) + hb_round_up(kp_of(k) * 4u, 256);
+}
+
+int hb_w8a8_prepack(void *d_packed, const uint8_t *d_blob, int k, int n, hb_stream s) {
+  if (d_packed == nullptr || d_blob == nullptr) return hb_invalid("hb_w8a8_prepack null pointer");
+  // The blob stores weights in whole 64-column groups (reference op_executor.cc:320 requires n % 64 == 0).
+  if (k < 32 || k % 32 || n < 64 || n % 64) return hb_invalid("hb_w8a8_prepack shape (k%32, n%64)");
+  if (!aligned(d_blob, 4) || !aligned(d_packed, 256)) return hb_invalid("hb_w8a8_prepack alignment");
+  hipStream_t st = hb_resolve_stream(s);
+  const int kp = (int)kp_of(k);
+  uint8_t *base = (uint8_t *)d_packed;
+  const size_t slots = (size_t)n * kp / 16u;
+  const int grid = (int)((slots + 255) / 256 < 65536 ? (slots + 255) / 256 : 65536);
+  hipLaunchKernelGGL(w8a8_prepack_weights, dim3(grid), dim3(256), 0, st,
+                     (uint4 *)(base + hb_w8a8_packed_offset(k, n, HB_W8A8_WEIGHTS)), d_blob, k, n, kp);
+  int rc = hb_check_launch("w8a8_prepack_weights");
+  if (rc) return rc;
+  const int cols = n > kp ? n : kp;
+  hipLaunchKernelGGL(w8a8_prepack_columns, dim3((cols + 255) / 256), dim3(256), 0, st,
+                     (float *)(base + hb_w8a8_packed_offset(k, n, HB_W8A8_SW)),
+                     (int32_t *)(base + hb_w8a8_packed_offset(k, n, HB_W8A8_DELTA)),
+                     (int32_t *)(base + hb_w8a8_packed_offset(k, n, HB_W8A8_WSUM128)),
+                     (float *)(base + hb_w8a8_packed_offset(k, n, HB_W8A8_INV)), d_blob, k, n, kp);
+  return hb_check_launch("w8a8_prepack_columns");
+}
+
+size_t hb_w8a8_workspace_bytes(int m, int k) {
+  if (m <= 0 || k <= 0) return 0;
+  return hb_round_up(mp_of(m) * kp_of(k), 256) + hb_round_up(mp_of(m) * 4u, 256);
+}
+
+int hb_w8a8_quantize(int8_t *d_q, float *d_scales, const float *d_x, const float *d_inv, int m, int k,
+                     hb_stream s) {
+  if (!d_q || !d_scales || !d_x || !d_inv) return hb_invalid("hb_w8a8_quantize null pointer");
+  if (m < 1 || k < 32 || k % 32) return hb_invalid("hb_w8a8_quantize shape");
+  if (!aligned(d_x, 4) || !aligned(d_inv, 4) || !aligned(d_q, 16) || !aligned(d_scales, 4))
+    return hb_invalid("hb_w8a8_quantize alignment");
+  hipStream_t st = hb_resolve_stream(s);
+  const int kp = (int)kp_of(k);
+  const dim3 grid((m + 3) / 4), block(256);
+  const bool vec = aligned(d_x, 16) && aligned(d_inv, 16);
+  if (vec && k <= 256 * 2) {
+    hipLaunchKernelGGL(w8a8_quant_rows_reg<2>, grid, block, 0, st, d_q, d_scales, d_x, d_inv, m, k, kp);
+  } else if (vec && k <= 256 * 6) {
+    hipLaunchKernelGGL(w8a8_quant_rows_reg<6>, grid, block, 0, st, d_q, d_scales, d_x, d_inv, m, k, kp);
+  } else if (vec && k <= 256 * 16) {
+    hipLaunchKernelGGL(w8a8_quant_rows_reg<16>, grid, block, 0, st, d_q, d_scales, d_x, d_inv, m, k, kp);
+  } else if (vec && k <= 256 * 24) {
+    hipLaunchKernelGGL(w8a8_quant_rows_reg<24>, grid, block, 0, st, d_q, d_scales, d_x, d_inv, m, k, kp);
+  } else {
+    hipLaunchKernelGGL(w8a8_quant_rows_any, grid, block, 0, st, d_q, d_scales, d_x, d_inv, m, k, kp);
+  }
+  return hb_check_launch("w8a8_quant_rows");
+}
+
+int hb_w8a8_gemm(void *d_y, int ldy, const int8_t *d_q, const float *d_scales, const void *d_packed, int m, int k,
+                 int n, int epilogue, hb_stream s) {
+  if (!d_y || !d_q || !d_packed || (epilogue != HB_W8A8_EPI_RAW && !d_scales))
+    return hb_invalid("hb_w8a8_gemm null pointer");
+  if (m < 1 || k < 32 || k % 32 || n < 16 || n % 16 || ldy < n) return hb_invalid("hb_w8a8_gemm shape");
+  if (!aligned(d_y, 4) || !aligned(d_q, 16) || !aligned(d_packed, 256)) return hb_invalid("hb_w8a8_gemm alignment");
+  hipStream_t st = hb_resolve_stream(s);
+  const int kp = (int)kp_of(k);
+  const uint8_t *base = (const uint8_t *)d_packed;
+  const int8_t *wpack = (const int8_t *)(base + hb_w8a8_packed_offset(k, n, HB_W8A8_WEIGHTS));
+  const float *sw = (const float *)(base + hb_w8a8_packed_offset(k, n, HB_W8A8_SW));
+  const int32_t *delta = (const int32_t *)(base + hb_w8a8_packed_offset(k, n, HB_W8A8_DELTA));
+  const int32_t *wsum = (const int32_t *)(base + hb_w8a8_packed_offset(k, n, HB_W8A8_WSUM128));
+  switch (epilogue) {
+    case HB_W8A8_EPI_SCALE:
+      return launch_gemm<HB_W8A8_EPI_SCALE>(d_y, ldy, d_q, d_scales, wpack, sw, delta, m, n, kp, st);
+    case HB_W8A8_EPI_SCALE_GELU:
+      return launch_gemm<HB_W8A8_EPI_SCALE_GELU>(d_y, ldy, d_q, d_scales, wpack, sw, delta, m, n, kp, st);
+    case HB_W8A8_EPI_RAW:
+      return launch_gemm<HB_W8A8_EPI_RAW>(d_y, ldy, d_q, d_scales, wpack, sw, wsum, m, n, kp, st);
+    default: return hb_invalid("hb_w8a8_gemm epilogue");
+  }
+}
+
+int hb_w8a8_linear(float *d_y, const float *d_x, const void *d_packed, int m, int k, int n, int epilogue,
+                   void *d_workspace, size_t workspace_bytes, hb_stream s) {
+  if (!d_workspace || workspace_bytes < hb_w8a8_workspace_bytes(m, k))
+    return hb_invalid("hb_w8a8_linear workspace too small");
+  if (!d_packed) return hb_invalid("hb_w8a8_linear packed weights");
+  if (!aligned(d_workspace, 256)) return hb_invalid("hb_w8a8_linear workspace alignment");
+  int8_t *q = (int8_t *)d_workspace;
+  float *scales = (float *)((uint8_t *)d_workspace + hb_round_up(mp_of(m) * kp_of(k), 256));
+  const float *inv = (const float *)((const uint8_t *)d_packed + hb_w8a8_packed_offset(k, n, HB_W8A8_INV));
+  int rc = hb_w8a8_quantize(q, scales, d_x, inv, m, k, s);
+  if (rc) return rc;
+  return hb_w8a8_gemm(d_y, n, q, scales, d_packed, m, k, n, epilogue, s);
+}
+
+int hb_w8a8_planes_from_raw(uint8_t *d_out, const int32_t *d_raw, int m, int n, hb_stream s) {
+  if (!d_out || !d_raw) return hb_invalid("hb_w8a8_planes_from_raw null pointer");
+  if (m < 1 || n < 32 || n % 32) return hb_invalid("hb_w8a8_planes_from_raw shape");
+  const size_t total = (size_t)m * n * 4u;
+  const int grid = (int)((total + 255) / 256 < 65536 ? (total + 255) / 256 : 65536);
+  hipLaunchKernelGGL(w8a8_planes, dim3(grid), dim3(256), 0, hb_resolve_stream(s), d_out, d_raw, m, n);
+  return hb_check_launch("w8a8_planes");
+}
+
+}  // extern "C"

@@ -1,0 +1,337 @@
+"""ctypes bindings of libhtp_ops.so (the C ABI declared in include/htp_ops/*.h).
+
+Tests, the smoke check and bench.py drive the library through these bindings:
+the hb_* kernel layer (device buffers, W8A8 / F16 kernels), the executor
+(execute_op_simple, mailbox messages), the session / channel API and the
+rpcmem buffer registry.  Nothing here computes: a missing or unloadable
+library raises immediately.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libhtp_ops.so")
+
+HB_OK = 0
+HB_E_HIP = -5
+HB_E_NOMEM = -12
+HB_E_NODEV = -19
+HB_E_INVAL = -22
+
+EPI_SCALE = 0
+EPI_SCALE_GELU = 1
+EPI_RAW = 2
+
+SECTION_WEIGHTS, SECTION_SW, SECTION_DELTA, SECTION_WSUM128, SECTION_INV = range(5)
+
+_c_void_p = ctypes.c_void_p
+_c_int = ctypes.c_int
+_c_size_t = ctypes.c_size_t
+
+# name -> (restype, argtypes)
+_SIGNATURES = {
+    # hb runtime
+    "hb_device_count": (_c_int, []),
+    "hb_init": (_c_int, [_c_int]),
+    "hb_last_error": (ctypes.c_char_p, []),
+    "hb_default_stream": (_c_void_p, []),
+    "hb_malloc": (_c_int, [ctypes.POINTER(_c_void_p), _c_size_t]),
+    "hb_free": (_c_int, [_c_void_p]),
+    "hb_host_malloc": (_c_int, [ctypes.POINTER(_c_void_p), _c_size_t]),
+    "hb_host_free": (_c_int, [_c_void_p]),
+    "hb_memcpy_h2d": (_c_int, [_c_void_p, _c_void_p, _c_size_t, _c_void_p]),
+    "hb_memcpy_d2h": (_c_int, [_c_void_p, _c_void_p, _c_size_t, _c_void_p]),
+    "hb_memcpy_d2d": (_c_int, [_c_void_p, _c_void_p, _c_size_t, _c_void_p]),
+    "hb_memset": (_c_int, [_c_void_p, _c_int, _c_size_t, _c_void_p]),
+    "hb_stream_create": (_c_int, [ctypes.POINTER(_c_void_p)]),
+    "hb_stream_destroy": (_c_int, [_c_void_p]),
+    "hb_stream_sync": (_c_int, [_c_void_p]),
+    "hb_device_sync": (_c_int, []),
+    "hb_event_create": (_c_int, [ctypes.POINTER(_c_void_p)]),
+    "hb_event_destroy": (_c_int, [_c_void_p]),
+    "hb_event_record": (_c_int, [_c_void_p, _c_void_p]),
+    "hb_event_sync": (_c_int, [_c_void_p]),
+    "hb_event_elapsed_ms": (_c_int, [ctypes.POINTER(ctypes.c_float), _c_void_p, _c_void_p]),
+    # W8A8
+    "hb_w8a8_packed_bytes": (_c_size_t, [_c_int, _c_int]),
+    "hb_w8a8_packed_offset": (_c_size_t, [_c_int, _c_int, _c_int]),
+    "hb_w8a8_prepack": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
+    "hb_w8a8_workspace_bytes": (_c_size_t, [_c_int, _c_int]),
+    "hb_w8a8_quantize": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
+    "hb_w8a8_gemm": (_c_int, [_c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int,
+                              _c_int, _c_void_p]),
+    "hb_w8a8_linear": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_void_p,
+                                _c_size_t, _c_void_p]),
+    "hb_w8a8_planes_from_raw": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
+    # F16
+    "hb_f16_packed_bytes": (_c_size_t, [_c_int, _c_int]),
+    "hb_f16_prepack": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
+    "hb_f16_gemm": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int,
+                             _c_void_p]),
+}
+
+# Host-library symbols (session, executor, registry); bound when present.
+_HOST_SIGNATURES = {
+    "execute_op_simple": (_c_int, [_c_void_p, _c_size_t]),
+    "htp_ops_execute_message": (_c_int, [_c_void_p, _c_size_t]),
+    "rpcmem_init": (None, []),
+    "rpcmem_deinit": (None, []),
+    "rpcmem_alloc": (_c_void_p, [_c_int, ctypes.c_uint32, _c_int]),
+    "rpcmem_alloc2": (_c_void_p, [_c_int, ctypes.c_uint32, _c_size_t]),
+    "rpcmem_free": (None, [_c_void_p]),
+    "rpcmem_to_fd": (_c_int, [_c_void_p]),
+    "fastrpc_mmap": (_c_int, [_c_int, _c_int, _c_void_p, _c_int, _c_size_t, _c_int]),
+    "fastrpc_munmap": (_c_int, [_c_int, _c_int, _c_void_p, _c_size_t]),
+    "htp_ops_amd_buffer_size": (ctypes.c_int64, [_c_int]),
+    "htp_ops_amd_buffer_is_device": (_c_int, [_c_int]),
+    "htp_ops_amd_buffer_device_ptr": (_c_void_p, [_c_int]),
+    "htp_ops_amd_buffer_write": (_c_int, [_c_int, _c_size_t, _c_void_p, _c_size_t]),
+    "htp_ops_amd_buffer_read": (_c_int, [_c_int, _c_size_t, _c_void_p, _c_size_t]),
+    "htp_ops_amd_invalidate_weights": (_c_int, [_c_int]),
+    "htp_ops_open": (_c_int, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint64)]),
+    "htp_ops_close": (_c_int, [ctypes.c_uint64]),
+    "htp_ops_init_backend": (_c_int, [ctypes.c_uint64]),
+    "htp_ops_init_backend_fraction": (_c_int, [ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32]),
+    "htp_ops_init_mapping_backend": (_c_int, [ctypes.c_uint64]),
+    "htp_ops_release_backend": (_c_int, [ctypes.c_uint64]),
+    "htp_ops_create_channel": (_c_int, [ctypes.c_uint64, ctypes.c_int32, ctypes.c_uint32]),
+    "htp_ops_create_channel_with_token": (_c_int, [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_int32,
+                                                   ctypes.c_uint32]),
+    "htp_ops_destroy_channel": (_c_int, [ctypes.c_uint64]),
+    "htp_ops_rms_norm_f32": (_c_int, [ctypes.c_uint64] + [ctypes.c_int32] * 6),
+    "htp_ops_mat_mul_permuted_w16a32": (_c_int, [ctypes.c_uint64] + [ctypes.c_int32] * 9),
+    "htp_ops_mat_mul_permuted_w16a32_trace": (_c_int, [ctypes.c_uint64] + [ctypes.c_int32] * 9 +
+                                              [ctypes.POINTER(ctypes.c_uint64)] * 3),
+    "htp_ops_test_ops": (_c_int, [ctypes.c_uint64, ctypes.POINTER(ctypes.c_int32)]),
+    "htp_ops_session_open": (_c_int, [ctypes.POINTER(_c_void_p), _c_int, ctypes.c_char_p, _c_int]),
+    "htp_ops_default_session": (_c_void_p, []),
+    "htp_ops_session_init_backend": (_c_int, [_c_void_p]),
+    "htp_ops_session_acquire_backend": (_c_int, [_c_void_p]),
+    "htp_ops_session_release_backend": (_c_int, [_c_void_p]),
+    "htp_ops_session_create_channel": (_c_int, [_c_void_p, _c_int, ctypes.c_uint]),
+    "htp_ops_session_create_channel_with_token": (_c_int, [_c_void_p, _c_int, ctypes.c_uint]),
+    "htp_ops_session_destroy_channel": (_c_int, [_c_void_p]),
+    "htp_ops_session_handle": (ctypes.c_uint64, [_c_void_p]),
+    "htp_ops_set_active_session": (_c_int, [_c_void_p]),
+    "htp_ops_set_default_session": (_c_int, []),
+    "htp_ops_session_id": (ctypes.c_uint32, [_c_void_p]),
+    "htp_ops_session_domain": (ctypes.c_uint32, [_c_void_p]),
+    "htp_ops_session_is_reserved": (_c_int, [_c_void_p]),
+    "htp_ops_session_is_initialized": (_c_int, [_c_void_p]),
+    "htp_ops_session_has_channel": (_c_int, [_c_void_p]),
+    "htp_ops_session_close": (None, [_c_void_p]),
+    "open_dsp_session": (_c_int, [_c_int, _c_int]),
+    "close_dsp_session": (None, []),
+    "get_global_handle": (ctypes.c_uint64, []),
+    "init_htp_backend": (None, []),
+    "release_htp_backend": (_c_int, []),
+    "create_htp_message_channel": (_c_int, [_c_int, ctypes.c_uint]),
+    "destroy_htp_message_channel": (_c_int, []),
+    "htp_ops_rpc_rms_norm_f32": (_c_int, [_c_int] * 6),
+    "htp_ops_rpc_rms_norm_f32_session": (_c_int, [_c_void_p] + [_c_int] * 6),
+    "htp_ops_rpc_mat_mul_permuted_w16a32": (_c_int, [_c_int] * 9),
+    "htp_ops_rpc_mat_mul_permuted_w16a32_session": (_c_int, [_c_void_p] + [_c_int] * 9),
+    "htp_ops_rpc_mat_mul_permuted_w16a32_trace_session": (_c_int, [_c_void_p] + [_c_int] * 9 +
+                                                          [ctypes.POINTER(ctypes.c_uint64)] * 3),
+    "htp_ops_f16_epilogue_version": (_c_int, []),
+    "htp_ops_native_model_version": (_c_int, []),
+    "htp_ops_dit_aux_version": (_c_int, []),
+    "htp_ops_dit_concat_version": (_c_int, []),
+}
+
+_lib = None
+
+
+class HtpOpsError(RuntimeError):
+    pass
+
+
+def lib():
+    """Loads libhtp_ops.so once; raises if it is missing (no fallback)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise HtpOpsError(f"{LIB_PATH} is not built; run __graft_entry__.build() or make -C {HERE}")
+        handle = ctypes.CDLL(LIB_PATH, mode=ctypes.RTLD_GLOBAL)
+        for name, (res, args) in list(_SIGNATURES.items()) + list(_HOST_SIGNATURES.items()):
+            fn = getattr(handle, name, None)
+            if fn is None:
+                continue
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+def last_error():
+    msg = lib().hb_last_error()
+    return msg.decode() if msg else ""
+
+
+def check(rc, what):
+    if rc != HB_OK:
+        raise HtpOpsError(f"{what} failed with {rc}: {last_error()}")
+
+
+_initialized = False
+
+
+def init(device=0):
+    """Selects the GPU; raises HtpOpsError when no GPU is usable."""
+    global _initialized
+    check(lib().hb_init(device), "hb_init")
+    _initialized = True
+
+
+def device_count():
+    return lib().hb_device_count()
+
+
+def sync():
+    check(lib().hb_device_sync(), "hb_device_sync")
+
+
+class DeviceBuffer:
+    """Owned device allocation."""
+
+    def __init__(self, nbytes):
+        self.nbytes = int(nbytes)
+        p = ctypes.c_void_p()
+        check(lib().hb_malloc(ctypes.byref(p), max(self.nbytes, 1)), "hb_malloc")
+        self.ptr = p.value
+
+    @classmethod
+    def from_array(cls, arr):
+        arr = np.ascontiguousarray(arr)
+        buf = cls(arr.nbytes)
+        buf.write(arr)
+        return buf
+
+    def write(self, arr, offset=0):
+        arr = np.ascontiguousarray(arr)
+        assert offset + arr.nbytes <= self.nbytes
+        check(lib().hb_memcpy_h2d(self.ptr + offset, arr.ctypes.data, arr.nbytes, None), "hb_memcpy_h2d")
+
+    def read(self, dtype, count=None, offset=0):
+        dtype = np.dtype(dtype)
+        if count is None:
+            count = (self.nbytes - offset) // dtype.itemsize
+        out = np.empty(count, dtype=dtype)
+        assert offset + out.nbytes <= self.nbytes
+        check(lib().hb_memcpy_d2h(out.ctypes.data, self.ptr + offset, out.nbytes, None), "hb_memcpy_d2h")
+        return out
+
+    def zero(self):
+        check(lib().hb_memset(self.ptr, 0, self.nbytes, None), "hb_memset")
+        sync()
+
+    def fill(self, byte):
+        check(lib().hb_memset(self.ptr, byte, self.nbytes, None), "hb_memset")
+        sync()
+
+    def free(self):
+        if self.ptr:
+            lib().hb_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+# ---- W8A8 ------------------------------------------------------------------
+
+def kp_of(k):
+    return (k + 63) // 64 * 64
+
+
+def w8a8_packed_bytes(k, n):
+    return lib().hb_w8a8_packed_bytes(k, n)
+
+
+def w8a8_packed_offset(k, n, section):
+    return lib().hb_w8a8_packed_offset(k, n, section)
+
+
+def w8a8_prepack(blob_dev, k, n):
+    """blob_dev: DeviceBuffer holding the constants blob -> packed DeviceBuffer."""
+    packed = DeviceBuffer(w8a8_packed_bytes(k, n))
+    check(lib().hb_w8a8_prepack(packed.ptr, blob_dev.ptr, k, n, None), "hb_w8a8_prepack")
+    sync()
+    return packed
+
+
+def w8a8_workspace_bytes(m, k):
+    return lib().hb_w8a8_workspace_bytes(m, k)
+
+
+def w8a8_quantize(x_dev, inv_ptr, m, k):
+    """Returns (q DeviceBuffer [mp][kp] int8, scales DeviceBuffer f32[mp])."""
+    mp = (m + 15) // 16 * 16
+    q = DeviceBuffer(mp * kp_of(k))
+    s = DeviceBuffer(mp * 4)
+    check(lib().hb_w8a8_quantize(q.ptr, s.ptr, x_dev.ptr, inv_ptr, m, k, None), "hb_w8a8_quantize")
+    sync()
+    return q, s
+
+
+def w8a8_gemm(y_dev, q_dev, s_dev, packed, m, k, n, epilogue=EPI_SCALE, ldy=None, stream=None):
+    check(lib().hb_w8a8_gemm(y_dev.ptr, n if ldy is None else ldy, q_dev.ptr, s_dev.ptr if s_dev else None,
+                             packed.ptr, m, k, n, epilogue, stream), "hb_w8a8_gemm")
+
+
+def w8a8_linear(y_dev, x_dev, packed, m, k, n, workspace, epilogue=EPI_SCALE, stream=None):
+    check(lib().hb_w8a8_linear(y_dev.ptr, x_dev.ptr, packed.ptr, m, k, n, epilogue, workspace.ptr,
+                               workspace.nbytes, stream), "hb_w8a8_linear")
+
+
+def w8a8_planes_from_raw(out_dev, raw_dev, m, n):
+    check(lib().hb_w8a8_planes_from_raw(out_dev.ptr, raw_dev.ptr, m, n, None), "hb_w8a8_planes_from_raw")
+
+
+# ---- F16 -------------------------------------------------------------------
+
+def f16_prepack(permuted_dev, k, n):
+    packed = DeviceBuffer(lib().hb_f16_packed_bytes(k, n))
+    check(lib().hb_f16_prepack(packed.ptr, permuted_dev.ptr, k, n, None), "hb_f16_prepack")
+    sync()
+    return packed
+
+
+def f16_gemm(y_dev, x_dev, packed, bias_dev, m, k, n, channels, mode, stream=None):
+    check(lib().hb_f16_gemm(y_dev.ptr, x_dev.ptr, packed.ptr, bias_dev.ptr if bias_dev else None, m, k, n,
+                            channels, mode, stream), "hb_f16_gemm")
+
+
+# ---- events ----------------------------------------------------------------
+
+class Event:
+    def __init__(self):
+        e = ctypes.c_void_p()
+        check(lib().hb_event_create(ctypes.byref(e)), "hb_event_create")
+        self.ptr = e.value
+
+    def record(self, stream=None):
+        check(lib().hb_event_record(self.ptr, stream), "hb_event_record")
+
+    def synchronize(self):
+        check(lib().hb_event_sync(self.ptr), "hb_event_sync")
+
+    def elapsed_ms(self, later):
+        ms = ctypes.c_float()
+        check(lib().hb_event_elapsed_ms(ctypes.byref(ms), self.ptr, later.ptr), "hb_event_elapsed_ms")
+        return ms.value
+
+    def __del__(self):
+        try:
+            lib().hb_event_destroy(self.ptr)
+        except Exception:
+            pass
+
+
+def default_stream():
+    return lib().hb_default_stream()

@@ -1,0 +1,48 @@
+/*
+ * Request executor: the in-process counterpart of the reference's DSP-side
+ * dispatcher, same entry point and return codes.
+ *
+ *   execute_op_simple   reference include/dsp/op_executor.h:32, src/dsp/op_executor.cc:274-1118
+ *     opcode 15 (W8A8)  reference src/dsp/op_executor.cc:314-353
+ *     opcode 16 (F16+epilogue) reference src/dsp/op_executor.cc:446-471
+ *     opcode 1  (F16)   reference src/dsp/op_executor.cc:473-540
+ *
+ * Return codes (unchanged from the reference):
+ *   opcode 15: -1 payload size / shape / profile mode, -2 unmapped buffer,
+ *              -3 constants header mismatch, -10 kernel argument error,
+ *              -12 CPU-control batch overflow.
+ *   opcode 16: -1 validation or unmapped buffer, -10/-11/-12 kernel argument errors.
+ *   opcode 1:  -1 short payload, -2 unmapped buffer, -3 misaligned buffer (128 B).
+ *   other opcodes: HTP_OPS_E_UNSUPPORTED (the reference silently returns 0).
+ *   A GPU runtime failure while executing a valid request returns -5.
+ * All argument checks happen before any GPU work is queued.
+ */
+#ifndef HTP_OPS_EXECUTOR_H
+#define HTP_OPS_EXECUTOR_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "htp_ops/message.h"
+#include "htp_ops/op_reg.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Executes one compute request in place: req points at the OpComputeRequest,
+ * req_size counts the opcode word plus the payload.  Output tensors are
+ * host-visible when this returns. */
+int execute_op_simple(struct OpComputeRequest *req, size_t req_size);
+
+/* Executes every request of a mailbox message in order, exactly as the
+ * channel thread does, without touching the state word.  Returns 0 when the
+ * layout is valid (per-request codes are in each RequestHeader.state) and -1
+ * when the layout is invalid (nothing executed). */
+int htp_ops_execute_message(struct MessageHeader *msg, size_t capacity);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HTP_OPS_EXECUTOR_H */

@@ -1,0 +1,134 @@
+/*
+ * hb_*: the thin C ABI between the C host library and the gfx950 kernels.
+ * Plain pointers, sizes and status codes only.  Every pointer named d_* is a
+ * device address; every kernel call is asynchronous on the given stream
+ * (NULL = the library's own stream on the current device).
+ *
+ * This layer replaces the reference's DSP-side kernel entry points:
+ *   hb_w8a8_linear / _quantize / _gemm  reference include/dsp/ops.h:20-31,
+ *       src/dsp/ops/linear_w8a8.c:327-558 (hmx_mat_mul_native_w8a8*)
+ *   hb_w8a8_prepack   consumes the constants blob of reference include/op_reg.h:80-85
+ *       (header checks src/dsp/op_executor.cc:331-335); no reference counterpart:
+ *       the reference re-copies weights from DDR on every call
+ *       (src/dsp/ops/linear_w8a8.c:242-268, :459)
+ *   hb_f16_gemm       reference src/dsp/ops/mat_mul.c:937-1049
+ *       (hmx_mat_mul_f16_epilogue, hmx_mat_mul_permuted_w16a32)
+ *   hb_f16_prepack    no reference counterpart (reference copies the permuted
+ *       weight into VTCM per call, src/dsp/ops/mat_mul.c:157-244)
+ *
+ * Status codes: 0 success, HB_E_INVAL bad argument, HB_E_NODEV no usable GPU,
+ * HB_E_HIP a HIP runtime error (text in hb_last_error()), HB_E_NOMEM.
+ */
+#ifndef HTP_OPS_HB_H
+#define HTP_OPS_HB_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HB_OK 0
+#define HB_E_HIP (-5)
+#define HB_E_NOMEM (-12)
+#define HB_E_NODEV (-19)
+#define HB_E_INVAL (-22)
+
+typedef void *hb_stream; /* a hipStream_t */
+typedef void *hb_event;  /* a hipEvent_t */
+
+/* ---- runtime ------------------------------------------------------------- */
+int hb_device_count(void);
+int hb_init(int device); /* selects the device for the calling thread and creates the library stream */
+const char *hb_last_error(void);
+hb_stream hb_default_stream(void);
+int hb_malloc(void **d_ptr, size_t bytes);
+int hb_free(void *d_ptr);
+int hb_host_malloc(void **h_ptr, size_t bytes); /* pinned */
+int hb_host_free(void *h_ptr);
+int hb_memcpy_h2d(void *d_dst, const void *h_src, size_t bytes, hb_stream s);
+int hb_memcpy_d2h(void *h_dst, const void *d_src, size_t bytes, hb_stream s);
+int hb_memcpy_d2d(void *d_dst, const void *d_src, size_t bytes, hb_stream s);
+int hb_memset(void *d_dst, int value, size_t bytes, hb_stream s);
+int hb_stream_create(hb_stream *s);
+int hb_stream_destroy(hb_stream s);
+int hb_stream_sync(hb_stream s);
+int hb_device_sync(void);
+int hb_event_create(hb_event *e);
+int hb_event_destroy(hb_event e);
+int hb_event_record(hb_event e, hb_stream s);
+int hb_event_sync(hb_event e);
+int hb_event_elapsed_ms(float *ms, hb_event start, hb_event stop);
+
+/* ---- W8A8 (opcode 15) ----------------------------------------------------- */
+
+/*
+ * Packed weight image produced once per constants blob by hb_w8a8_prepack.
+ * kp = k rounded up to 64.  Sections (byte offsets from the image base):
+ *   [0]                      int8 W in 16(n) x 64(k) MFMA tiles: element (n,k) at
+ *                            ((n/16)*(kp/64) + k/64)*1024 + ((n%16) + 16*((k%64)/16))*16 + k%16,
+ *                            zero for k >= k_real
+ *   [HB_W8A8_SW]             f32 sw[n]        per-column scale (copied from the blob)
+ *   [HB_W8A8_DELTA]          i32 delta[n]     128*(sum_k W(n,k) - blob.sums[n]), wrapping
+ *   [HB_W8A8_WSUM128]        i32 wsum128[n]   128*sum_k W(n,k), wrapping
+ *   [HB_W8A8_INV]            f32 inv[k]       smoothing vector (copied from the blob)
+ */
+enum { HB_W8A8_WEIGHTS = 0, HB_W8A8_SW = 1, HB_W8A8_DELTA = 2, HB_W8A8_WSUM128 = 3, HB_W8A8_INV = 4 };
+size_t hb_w8a8_packed_bytes(int k, int n);
+size_t hb_w8a8_packed_offset(int k, int n, int section);
+
+/* Blob (device copy of the constants buffer, header already validated) -> packed image. */
+int hb_w8a8_prepack(void *d_packed, const uint8_t *d_blob, int k, int n, hb_stream s);
+
+/* Workspace for quantized activations: int8 q[mp][kp] (mp = m rounded up to 16) then f32 scales[mp]. */
+size_t hb_w8a8_workspace_bytes(int m, int k);
+
+/*
+ * Per-token dynamic quantization (reference linear_w8a8.c:34-120):
+ *   t = x*inv; s = max(max|t|/127, 1e-12); u = rint(clamp(t*(1/s)+128, 1, 255))
+ * writes q = u - 128 (int8, row stride kp, zero for k >= k_real) and s (f32[m]).
+ */
+int hb_w8a8_quantize(int8_t *d_q, float *d_scales, const float *d_x, const float *d_inv, int m, int k,
+                     hb_stream s);
+
+/* Output epilogues of hb_w8a8_gemm. */
+enum {
+  HB_W8A8_EPI_SCALE = 0,      /* y = (float)(acc - 128*sums) * sw[n] * s[m], f32 [m][n] */
+  HB_W8A8_EPI_SCALE_GELU = 1, /* GELU (tanh form) of the above (no reference opcode) */
+  HB_W8A8_EPI_RAW = 2,        /* int32 raw accumulator sum_k u*W, stored as [m][n] int32 */
+};
+
+/* INT8 GEMM on quantized activations + fused epilogue; picks the decode
+ * (m <= 16) or tiled kernel.  d_y has row stride ldy (elements, >= n). */
+int hb_w8a8_gemm(void *d_y, int ldy, const int8_t *d_q, const float *d_scales, const void *d_packed, int m, int k,
+                 int n, int epilogue, hb_stream s);
+
+/* Full opcode-15 computation: quantize + GEMM + epilogue (workspace from hb_w8a8_workspace_bytes). */
+int hb_w8a8_linear(float *d_y, const float *d_x, const void *d_packed, int m, int k, int n, int epilogue,
+                   void *d_workspace, size_t workspace_bytes, hb_stream s);
+
+/* CPU-control variant: raw accumulator byte planes in the reference's export
+ * format (reference linear_w8a8.c:209-227) written over the f32 output tensor. */
+int hb_w8a8_planes_from_raw(uint8_t *d_out, const int32_t *d_raw, int m, int n, hb_stream s);
+
+/* ---- packed-F16 GEMM (opcodes 1 and 16) ------------------------------------ */
+
+/* Permuted fp16 weight (reference layout) -> 16(n) x 32(k) MFMA tiles:
+ * element (n,k) at ((n/16)*(k/32) + k/32)*512 + ((n%16) + 16*((k%32)/8))*8 + k%8 (fp16 units). */
+size_t hb_f16_packed_bytes(int k, int n);
+int hb_f16_prepack(uint16_t *d_packed, const uint16_t *d_permuted, int k, int n, hb_stream s);
+
+/*
+ * y = epilogue(fp16(fp16(x) @ W)); x f32 [m][k]; bias f32[channels] or NULL.
+ * mode 0: + bias; 1: + bias, GELU (tanh form); 2: + bias, QuickGELU;
+ * mode 3: + bias, stored channel-major y[c][m] for c < channels.
+ */
+int hb_f16_gemm(float *d_y, const float *d_x, const uint16_t *d_packed, const float *d_bias, int m, int k, int n,
+                int channels, int mode, hb_stream s);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HTP_OPS_HB_H */

@@ -1,0 +1,551 @@
+/*
+ * CPU oracle for the quantized-linear path -- TEST INFRASTRUCTURE ONLY.
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load
+ * this code; the product library (htp-ops-lib-sd.cpp_amd) never does.
+ *
+ * Build: gcc -std=c11 -O3 -march=native -ffp-contract=off -fno-fast-math -pthread
+ *
+ * Each function names the reference lines it restates.  Parity status of each
+ * function (what pins it) is listed in tests/test_oracle.py and DESIGN.md.
+ */
+#define _GNU_SOURCE
+#include "htp_oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+#include <unistd.h>
+
+/* ------------------------------------------------------------------------ */
+/* helpers                                                                   */
+/* ------------------------------------------------------------------------ */
+
+static uint32_t f32_bits(float f) {
+  uint32_t u;
+  memcpy(&u, &f, sizeof(u));
+  return u;
+}
+
+static float bits_f32(uint32_t u) {
+  float f;
+  memcpy(&f, &u, sizeof(f));
+  return f;
+}
+
+int oracle_num_threads(void) {
+  long n = sysconf(_SC_NPROCESSORS_ONLN);
+  return n < 1 ? 1 : (int)n;
+}
+
+typedef void (*range_fn)(void *ctx, int begin, int end);
+
+typedef struct {
+  range_fn fn;
+  void *ctx;
+  int begin, end;
+} range_job;
+
+static void *range_thread(void *arg) {
+  range_job *job = (range_job *)arg;
+  job->fn(job->ctx, job->begin, job->end);
+  return NULL;
+}
+
+/* Runs fn over [0, total) split into contiguous chunks on nthreads threads. */
+static void parallel_for(int total, int nthreads, range_fn fn, void *ctx) {
+  if (nthreads <= 0) nthreads = oracle_num_threads();
+  if (nthreads > total) nthreads = total;
+  if (nthreads <= 1) {
+    if (total > 0) fn(ctx, 0, total);
+    return;
+  }
+  pthread_t *threads = (pthread_t *)malloc(sizeof(pthread_t) * (size_t)nthreads);
+  range_job *jobs = (range_job *)malloc(sizeof(range_job) * (size_t)nthreads);
+  for (int t = 0; t < nthreads; ++t) {
+    jobs[t].fn = fn;
+    jobs[t].ctx = ctx;
+    jobs[t].begin = (int)((long long)total * t / nthreads);
+    jobs[t].end = (int)((long long)total * (t + 1) / nthreads);
+  }
+  for (int t = 1; t < nthreads; ++t) pthread_create(&threads[t], NULL, range_thread, &jobs[t]);
+  range_thread(&jobs[0]);
+  for (int t = 1; t < nthreads; ++t) pthread_join(threads[t], NULL);
+  free(jobs);
+  free(threads);
+}
+
+/* ------------------------------------------------------------------------ */
+/* binary16 conversion (IEEE 754-2008 binary16, round to nearest even)      */
+/* Stands for the reference's fp32->fp16 activation conversion              */
+/* (hvx_convert.h:5-12, mat_mul.c:114-148) and the HMX cvt.hf readout        */
+/* (hmx_utils.h:34-40), both defined here as IEEE RNE.                       */
+/* ------------------------------------------------------------------------ */
+
+uint16_t oracle_f32_to_f16(float x) {
+  const uint32_t u = f32_bits(x);
+  const uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+  const uint32_t absu = u & 0x7fffffffu;
+  if (absu >= 0x7f800000u) { /* inf or nan */
+    if (absu == 0x7f800000u) return (uint16_t)(sign | 0x7c00u);
+    return (uint16_t)(sign | 0x7e00u | ((absu >> 13) & 0x3ffu));
+  }
+  const int exp = (int)(absu >> 23) - 127;
+  if (exp > 15) return (uint16_t)(sign | 0x7c00u); /* overflow -> inf */
+  uint32_t mant = (absu & 0x7fffffu) | 0x800000u;  /* 24-bit significand */
+  int shift;                                       /* bits dropped from the 24-bit significand */
+  uint32_t biased;
+  if (exp >= -14) { /* normal half */
+    shift = 13;
+    biased = (uint32_t)(exp + 15);
+  } else { /* subnormal half (or underflow to zero) */
+    if (absu == 0) return sign;
+    shift = 13 + (-14 - exp);
+    biased = 0;
+    if (shift > 25) return sign; /* below half of the smallest subnormal */
+  }
+  uint32_t q = mant >> shift;
+  const uint32_t rem = mant & ((1u << shift) - 1u);
+  const uint32_t half = 1u << (shift - 1);
+  if (rem > half || (rem == half && (q & 1u))) ++q;
+  if (biased == 0) {
+    /* q counts subnormal units; a carry into 0x400 yields the smallest normal */
+    return (uint16_t)(sign | q);
+  }
+  /* q has the implicit bit at 0x400; a carry to 0x800 bumps the exponent */
+  uint32_t e = biased;
+  if (q & 0x800u) {
+    q >>= 1;
+    ++e;
+  }
+  if (e >= 31) return (uint16_t)(sign | 0x7c00u);
+  return (uint16_t)(sign | (e << 10) | (q & 0x3ffu));
+}
+
+float oracle_f16_to_f32(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  const uint32_t e = (h >> 10) & 0x1fu;
+  uint32_t m = h & 0x3ffu;
+  if (e == 31) return bits_f32(sign | 0x7f800000u | (m << 13));
+  if (e == 0) {
+    if (m == 0) return bits_f32(sign);
+    /* subnormal: value = m * 2^-24, exact in binary32 */
+    float v = (float)m * 0x1p-24f;
+    return sign ? -v : v;
+  }
+  return bits_f32(sign | ((e + 112u) << 23) | (m << 13));
+}
+
+/* ------------------------------------------------------------------------ */
+/* W8A8 constants blob (reference include/op_reg.h:80-85,                  */
+/* src/dsp/op_executor.cc:321-335; weight addressing                        */
+/* src/dsp/ops/linear_w8a8.c:453,482,486-488 and                            */
+/* tests/hmx-probe/study_dsp.c:82-84)                                       */
+/* ------------------------------------------------------------------------ */
+
+size_t oracle_w8a8_blob_bytes(int k, int n) {
+  return 128u + (size_t)k * (size_t)n + (size_t)n * 8u + (size_t)k * 4u;
+}
+
+size_t oracle_w8a8_weight_offset(int k, int n_idx, int k_idx) {
+  return 128u + (size_t)(n_idx / 64) * 64u * (size_t)k + (size_t)(k_idx / 32) * 2048u +
+         (size_t)((n_idx % 64) / 32) * 1024u + (size_t)((k_idx % 32) / 4) * 128u + (size_t)(n_idx % 32) * 4u +
+         (size_t)(k_idx % 4);
+}
+
+static void put_u32(uint8_t *p, uint32_t v) { memcpy(p, &v, 4); }
+static uint32_t get_u32(const uint8_t *p) {
+  uint32_t v;
+  memcpy(&v, p, 4);
+  return v;
+}
+
+void oracle_w8a8_pack_blob(uint8_t *blob, const int8_t *w, const float *sw, const int32_t *sums,
+                           const float *inv, int k, int n, uint64_t signature) {
+  const size_t kn = (size_t)k * (size_t)n;
+  memset(blob, 0, 128);
+  put_u32(blob + 0, 0x38574d48u);
+  put_u32(blob + 4, 1u);
+  put_u32(blob + 8, (uint32_t)k);
+  put_u32(blob + 12, (uint32_t)n);
+  put_u32(blob + 16, 128u);
+  put_u32(blob + 20, (uint32_t)(128u + kn));
+  put_u32(blob + 24, (uint32_t)(128u + kn + 4u * (size_t)n));
+  put_u32(blob + 28, (uint32_t)(128u + kn + 8u * (size_t)n));
+  put_u32(blob + 32, (uint32_t)oracle_w8a8_blob_bytes(k, n));
+  memcpy(blob + 40, &signature, 8);
+  for (int c = 0; c < n; ++c)
+    for (int r = 0; r < k; ++r) blob[oracle_w8a8_weight_offset(k, c, r)] = (uint8_t)w[(size_t)c * k + r];
+  uint8_t *scale = blob + 128 + kn;
+  uint8_t *sum = scale + 4u * (size_t)n;
+  uint8_t *inverse = sum + 4u * (size_t)n;
+  for (int c = 0; c < n; ++c) {
+    memcpy(scale + 4u * (size_t)c, &sw[c], 4);
+    int32_t s = 0;
+    if (sums) {
+      s = sums[c];
+    } else {
+      for (int r = 0; r < k; ++r) s += w[(size_t)c * k + r];
+    }
+    memcpy(sum + 4u * (size_t)c, &s, 4);
+  }
+  for (int r = 0; r < k; ++r) {
+    const float one = 1.0f;
+    memcpy(inverse + 4u * (size_t)r, inv ? &inv[r] : &one, 4);
+  }
+}
+
+void oracle_w8a8_unpack_weights(int8_t *w, const uint8_t *blob, int k, int n) {
+  for (int c = 0; c < n; ++c)
+    for (int r = 0; r < k; ++r) w[(size_t)c * k + r] = (int8_t)blob[oracle_w8a8_weight_offset(k, c, r)];
+}
+
+/* Header acceptance of reference src/dsp/op_executor.cc:331-335; -3 on mismatch. */
+int oracle_w8a8_check_header(const uint8_t *blob, int k, int n) {
+  const size_t kn = (size_t)k * (size_t)n;
+  const size_t scale = 128u + kn;
+  if (get_u32(blob + 0) != 0x38574d48u || get_u32(blob + 4) != 1u || get_u32(blob + 8) != (uint32_t)k ||
+      get_u32(blob + 12) != (uint32_t)n || get_u32(blob + 16) != 128u || get_u32(blob + 20) != scale ||
+      get_u32(blob + 24) != scale + 4u * (size_t)n || get_u32(blob + 28) != get_u32(blob + 24) + 4u * (size_t)n ||
+      get_u32(blob + 32) != oracle_w8a8_blob_bytes(k, n))
+    return -3;
+  return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* W8A8 activation quantization                                             */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * Clamp of v to [1, 255] done on the IEEE bit pattern as signed integers
+ * (negative values and -NaN -> 1.0, +NaN and values above 255 -> 255.0),
+ * then round-to-nearest-even of the significand by shifting
+ * (reference src/dsp/ops/linear_w8a8.c:47-58).
+ */
+uint8_t oracle_w8a8_quantize_value(float v) {
+  int32_t b = (int32_t)f32_bits(v);
+  const int32_t lo = (int32_t)f32_bits(1.0f), hi = (int32_t)f32_bits(255.0f);
+  if (b < lo) b = lo;
+  if (b > hi) b = hi;
+  const int32_t e = (int32_t)(((uint32_t)b >> 23) & 0xffu) - 127; /* 0..7 */
+  const int32_t shift = 23 - e;                                   /* 16..23 */
+  const int32_t mant = (b & 0x7fffff) | 0x800000;
+  const int32_t whole = mant >> shift;
+  const int32_t half = 1 << (shift - 1);
+  return (uint8_t)((mant + (half - 1) + (whole & 1)) >> shift);
+}
+
+typedef struct {
+  uint8_t *u;
+  float *s;
+  const float *x;
+  const float *inv;
+  int k;
+} quant_ctx;
+
+/*
+ * Per-token dynamic quantization, reference src/dsp/ops/linear_w8a8.c:
+ *   t[k] = x[k]*inv[k]                              :83-87
+ *   s    = fmaxf(max_k |t[k]| / 127, 1e-12f)         :34-40, :92-95, :102-105
+ *   r    = 1/s                                      :106-109
+ *   u[k] = rne(clamp(t[k]*r + 128, 1, 255))           :42-59, :110-118
+ */
+static void quant_rows(void *arg, int begin, int end) {
+  quant_ctx *c = (quant_ctx *)arg;
+  const int k = c->k;
+  float *t = (float *)malloc(sizeof(float) * (size_t)k);
+  for (int row = begin; row < end; ++row) {
+    const float *x = c->x + (size_t)row * k;
+    float amax = 0.0f;
+    for (int i = 0; i < k; ++i) {
+      t[i] = x[i] * c->inv[i];
+      const float a = fabsf(t[i]);
+      if (a > amax) amax = a;
+    }
+    const float s = fmaxf(amax / 127.0f, 1e-12f);
+    const float r = 1.0f / s;
+    c->s[row] = s;
+    uint8_t *u = c->u + (size_t)row * k;
+    for (int i = 0; i < k; ++i) {
+      const float scaled = t[i] * r;
+      const float v = scaled + 128.0f;
+      u[i] = oracle_w8a8_quantize_value(v);
+    }
+  }
+  free(t);
+}
+
+void oracle_w8a8_quantize(uint8_t *u, float *s, const float *x, const float *inv, int m, int k, int nthreads) {
+  quant_ctx c = {u, s, x, inv, k};
+  parallel_for(m, nthreads, quant_rows, &c);
+}
+
+/* ------------------------------------------------------------------------ */
+/* W8A8 integer accumulation: acc[m][n] = sum_k u[m][k] * W(n,k) (int32)     */
+/* reference src/dsp/ops/linear_w8a8.c:478-502 (HMX u8 x s8 MAC), :130-138   */
+/* ------------------------------------------------------------------------ */
+
+typedef struct {
+  int32_t *acc;
+  const uint8_t *u;
+  const int8_t *w; /* [n][k] */
+  int k, n;
+} acc_ctx;
+
+static void acc_rows(void *arg, int begin, int end) {
+  acc_ctx *c = (acc_ctx *)arg;
+  const int k = c->k, n = c->n;
+  const int nblock = 128;
+  for (int n0 = 0; n0 < n; n0 += nblock) {
+    const int n1 = n0 + nblock < n ? n0 + nblock : n;
+    for (int row = begin; row < end; ++row) {
+      const uint8_t *u = c->u + (size_t)row * k;
+      int32_t *out = c->acc + (size_t)row * n;
+      for (int col = n0; col < n1; ++col) {
+        const int8_t *w = c->w + (size_t)col * k;
+        int32_t sum = 0;
+        for (int i = 0; i < k; ++i) sum += (int32_t)u[i] * (int32_t)w[i];
+        out[col] = sum;
+      }
+    }
+  }
+}
+
+void oracle_w8a8_accumulate(int32_t *acc, const uint8_t *u, const uint8_t *blob, int m, int k, int n,
+                            int nthreads) {
+  int8_t *w = (int8_t *)malloc((size_t)k * (size_t)n);
+  oracle_w8a8_unpack_weights(w, blob, k, n);
+  acc_ctx c = {acc, u, w, k, n};
+  parallel_for(m, nthreads, acc_rows, &c);
+  free(w);
+}
+
+/* ------------------------------------------------------------------------ */
+/* W8A8 output: c = acc - (sums[n] << 7) (int32 wrap);                      */
+/*              y = ((float)c * sw[n]) * s[m]                                */
+/* reference src/dsp/ops/linear_w8a8.c:140-192                              */
+/* ------------------------------------------------------------------------ */
+
+typedef struct {
+  float *y;
+  const int32_t *acc;
+  const float *s;
+  const float *sw;
+  const int32_t *sums;
+  int n;
+} out_ctx;
+
+static void out_rows(void *arg, int begin, int end) {
+  out_ctx *c = (out_ctx *)arg;
+  for (int row = begin; row < end; ++row) {
+    for (int col = 0; col < c->n; ++col) {
+      const size_t i = (size_t)row * c->n + col;
+      const int32_t corrected = (int32_t)((uint32_t)c->acc[i] - ((uint32_t)c->sums[col] << 7));
+      const float value = (float)corrected;
+      const float scaled = value * c->sw[col];
+      c->y[i] = scaled * c->s[row];
+    }
+  }
+}
+
+void oracle_w8a8_output(float *y, const int32_t *acc, const float *s, const uint8_t *blob, int m, int k, int n,
+                        int nthreads) {
+  const size_t kn = (size_t)k * (size_t)n;
+  float *sw = (float *)malloc(sizeof(float) * (size_t)n);
+  int32_t *sums = (int32_t *)malloc(sizeof(int32_t) * (size_t)n);
+  memcpy(sw, blob + 128 + kn, 4u * (size_t)n);
+  memcpy(sums, blob + 128 + kn + 4u * (size_t)n, 4u * (size_t)n);
+  out_ctx c = {y, acc, s, sw, sums, n};
+  parallel_for(m, nthreads, out_rows, &c);
+  free(sums);
+  free(sw);
+}
+
+/* Whole opcode-15 computation on a blob; no envelope checks (K may exceed the
+ * reference's 6144 limit, int32 stays exact up to K = 65535). */
+void oracle_w8a8_linear(float *y, const float *x, const uint8_t *blob, int m, int k, int n, int nthreads) {
+  const size_t kn = (size_t)k * (size_t)n;
+  const float *inv_src = (const float *)(const void *)(blob + 128 + kn + 8u * (size_t)n);
+  float *inv = (float *)malloc(sizeof(float) * (size_t)k);
+  memcpy(inv, inv_src, 4u * (size_t)k);
+  uint8_t *u = (uint8_t *)malloc((size_t)m * (size_t)k);
+  float *s = (float *)malloc(sizeof(float) * (size_t)m);
+  int32_t *acc = (int32_t *)malloc(sizeof(int32_t) * (size_t)m * (size_t)n);
+  oracle_w8a8_quantize(u, s, x, inv, m, k, nthreads);
+  oracle_w8a8_accumulate(acc, u, blob, m, k, n, nthreads);
+  oracle_w8a8_output(y, acc, s, blob, m, k, n, nthreads);
+  free(acc);
+  free(s);
+  free(u);
+  free(inv);
+}
+
+/*
+ * Raw-plane export of the CPU-control variant (reference
+ * src/dsp/ops/linear_w8a8.c:209-227, byte order from :159-171): for every
+ * 64-row tile and 32-column half, the four little-endian byte planes of the
+ * raw accumulator (rows x 32 bytes each, plane 0 = low byte) are written as
+ * one flat stream over the same rows x 128 bytes the f32 outputs occupy.
+ */
+void oracle_w8a8_planes(uint8_t *out, const int32_t *acc, int m, int n) {
+  for (int tile = 0; tile * 64 < m; ++tile) {
+    const int rows = m - tile * 64 < 64 ? m - tile * 64 : 64;
+    for (int n0 = 0; n0 < n; n0 += 32) {
+      for (int p = 0; p < 4; ++p) {
+        for (int r = 0; r < rows; ++r) {
+          for (int c = 0; c < 32; ++c) {
+            const uint32_t v = (uint32_t)acc[(size_t)(tile * 64 + r) * n + n0 + c];
+            const size_t flat = (size_t)p * rows * 32u + (size_t)r * 32u + (size_t)c;
+            const size_t row = (size_t)tile * 64u + flat / 128u;
+            out[(row * (size_t)n + (size_t)n0) * 4u + flat % 128u] = (uint8_t)(v >> (8 * p));
+          }
+        }
+      }
+    }
+  }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Epilogue activations, reference src/dsp/ops/mat_mul.c:788-826             */
+/* (mode 1: z*sigmoid(1.5957691216057308*(z + 0.044715*z^3)); mode 2:        */
+/* z*sigmoid(1.702*z); sigmoid in the stable form e/(1+e) for negative       */
+/* arguments and 1/(1+e) otherwise with e = 2^max(-|a|*log2(e), -126)).      */
+/* The reference evaluates 2^x with a degree-6 polynomial and the reciprocal */
+/* with Newton steps in QFloat; the oracle uses libm exp2f and IEEE division.*/
+/* ------------------------------------------------------------------------ */
+
+static float stable_sigmoid(float a) {
+  const float absa = fabsf(a);
+  float neg = absa * -1.4426950408889634f;
+  if (neg < -126.0f) neg = -126.0f;
+  const float e = exp2f(neg);
+  const float denom = e + 1.0f;
+  const float inv = 1.0f / denom;
+  return a < 0.0f ? e * inv : inv;
+}
+
+float oracle_gelu_tanh(float z) {
+  const float cubic = (z * z) * z;
+  const float inner = z + cubic * 0.044715f;
+  const float a = inner * 1.5957691216057308f;
+  return z * stable_sigmoid(a);
+}
+
+float oracle_quick_gelu(float z) {
+  const float a = z * 1.702f;
+  return z * stable_sigmoid(a);
+}
+
+void oracle_gelu_tanh_inplace(float *y, size_t count) {
+  for (size_t i = 0; i < count; ++i) y[i] = oracle_gelu_tanh(y[i]);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Packed F16 GEMM with epilogue (opcodes 1/16)                             */
+/* layout: reference src/host/test.c:547-558 (writer);                      */
+/* semantics: reference src/dsp/ops/mat_mul.c:937-1049                      */
+/* ------------------------------------------------------------------------ */
+
+size_t oracle_f16_permuted_index(int k_total, int k_idx, int n_idx) {
+  return ((size_t)(n_idx / 32) * (size_t)(k_total / 32) + (size_t)(k_idx / 32)) * 1024u +
+         (size_t)((k_idx % 32) / 2) * 64u + (size_t)(n_idx % 32) * 2u + (size_t)(k_idx % 2);
+}
+
+void oracle_f16_permute(uint16_t *permuted, const uint16_t *w_kn, int k, int n) {
+  for (int r = 0; r < k; ++r)
+    for (int c = 0; c < n; ++c) permuted[oracle_f16_permuted_index(k, r, c)] = w_kn[(size_t)r * n + c];
+}
+
+typedef struct {
+  float *y;
+  const float *x;
+  const double *w; /* [n][k] */
+  const float *bias;
+  int m, k, n, channels, mode;
+} f16_ctx;
+
+/*
+ * a = fp16(x); acc = sum_k a*W exactly (double); h = fp16(acc); v = (float)h
+ * (mat_mul.c:114-148 conversion, :724-748 HMX core, :751-778 readout), then
+ *   mode 0: v + bias                        (:864-882)
+ *   mode 1/2: activation(v + bias)          (:864-882, :788-826)
+ *   mode 3: yt[c][row] = v + bias, c < channels  (:830-862)
+ */
+static void f16_rows(void *arg, int begin, int end) {
+  f16_ctx *c = (f16_ctx *)arg;
+  const int k = c->k, n = c->n;
+  double *a = (double *)malloc(sizeof(double) * (size_t)k);
+  for (int row = begin; row < end; ++row) {
+    for (int i = 0; i < k; ++i) a[i] = (double)oracle_f16_to_f32(oracle_f32_to_f16(c->x[(size_t)row * k + i]));
+    const int cols = c->mode == 3 ? c->channels : n;
+    for (int col = 0; col < cols; ++col) {
+      const double *w = c->w + (size_t)col * k;
+      double acc = 0.0;
+      for (int i = 0; i < k; ++i) acc += a[i] * w[i];
+      const float v = oracle_f16_to_f32(oracle_f32_to_f16((float)acc));
+      float z = c->bias ? v + c->bias[col] : v;
+      if (c->mode == 1) z = oracle_gelu_tanh(z);
+      if (c->mode == 2) z = oracle_quick_gelu(z);
+      if (c->mode == 3)
+        c->y[(size_t)col * c->m + row] = z;
+      else
+        c->y[(size_t)row * n + col] = z;
+    }
+  }
+  free(a);
+}
+
+void oracle_f16_gemm_epilogue(float *y, const float *x, const uint16_t *permuted, const float *bias, int m, int k,
+                              int n, int channels, int mode, int nthreads) {
+  double *w = (double *)malloc(sizeof(double) * (size_t)k * (size_t)n);
+  for (int c = 0; c < n; ++c)
+    for (int r = 0; r < k; ++r)
+      w[(size_t)c * k + r] = (double)oracle_f16_to_f32(permuted[oracle_f16_permuted_index(k, r, c)]);
+  f16_ctx ctx = {y, x, w, bias, m, k, n, channels, mode};
+  parallel_for(m, nthreads, f16_rows, &ctx);
+  free(w);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Deterministic synthetic inputs: splitmix64, Box-Muller in double          */
+/* ------------------------------------------------------------------------ */
+
+uint64_t oracle_splitmix64(uint64_t *state) {
+  uint64_t z = (*state += 0x9e3779b97f4a7c15ull);
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  return z ^ (z >> 31);
+}
+
+static double unit_double(uint64_t *state) { return (double)(oracle_splitmix64(state) >> 11) * 0x1.0p-53; }
+
+void oracle_fill_normal(float *dst, size_t count, float mean, float stddev, uint64_t seed) {
+  uint64_t st = seed;
+  for (size_t i = 0; i < count; i += 2) {
+    double u1 = unit_double(&st);
+    const double u2 = unit_double(&st);
+    if (u1 < 0x1.0p-60) u1 = 0x1.0p-60;
+    const double r = sqrt(-2.0 * log(u1));
+    const double th = 6.283185307179586 * u2;
+    dst[i] = (float)(mean + stddev * r * cos(th));
+    if (i + 1 < count) dst[i + 1] = (float)(mean + stddev * r * sin(th));
+  }
+}
+
+void oracle_fill_uniform(float *dst, size_t count, float lo, float hi, uint64_t seed) {
+  uint64_t st = seed;
+  for (size_t i = 0; i < count; ++i) dst[i] = (float)(lo + (hi - lo) * unit_double(&st));
+}
+
+void oracle_fill_int8(int8_t *dst, size_t count, int lo, int hi, uint64_t seed) {
+  uint64_t st = seed;
+  const uint64_t span = (uint64_t)(hi - lo + 1);
+  const uint64_t limit = UINT64_MAX - UINT64_MAX % span; /* unbiased draw */
+  for (size_t i = 0; i < count; ++i) {
+    uint64_t v;
+    do {
+      v = oracle_splitmix64(&st);
+    } while (v >= limit);
+    dst[i] = (int8_t)(lo + (int)(v % span));
+  }
+}

@@ -1,0 +1,71 @@
+/*
+ * CPU oracle for the quantized-linear path -- TEST INFRASTRUCTURE ONLY.
+ *
+ * A portable C11 restatement of the reference's arithmetic for opcodes 15, 16
+ * and 1.  It is linked only by tests/, __graft_entry__.smoke() (as the checker)
+ * and bench.py's cpu_baseline leg; the product library never calls it.
+ *
+ * Floating point is IEEE-754 binary32 with round-to-nearest-even on every
+ * operation and no contraction (build with -ffp-contract=off, no fast-math).
+ * The reference performs the same steps in Hexagon QFloat followed by IEEE
+ * conversion; the bit-level QFloat rounding is not observable from the
+ * reference's own tests, so the reference contract is defined as IEEE per
+ * operation (see the per-function notes in htp_oracle.c).
+ */
+#ifndef HTP_ORACLE_H
+#define HTP_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- binary16 ------------------------------------------------------------ */
+uint16_t oracle_f32_to_f16(float x);
+float oracle_f16_to_f32(uint16_t h);
+
+/* ---- W8A8 constants blob ---------------------------------------------------- */
+size_t oracle_w8a8_blob_bytes(int k, int n);
+size_t oracle_w8a8_weight_offset(int k, int n_idx, int k_idx);
+/* w: int8 [n][k]; sums == NULL -> sum_k w; inv == NULL -> 1.0f. */
+void oracle_w8a8_pack_blob(uint8_t *blob, const int8_t *w, const float *sw, const int32_t *sums,
+                           const float *inv, int k, int n, uint64_t signature);
+void oracle_w8a8_unpack_weights(int8_t *w, const uint8_t *blob, int k, int n);
+int oracle_w8a8_check_header(const uint8_t *blob, int k, int n);
+
+/* ---- W8A8 arithmetic -------------------------------------------------------- */
+uint8_t oracle_w8a8_quantize_value(float v);
+void oracle_w8a8_quantize(uint8_t *u, float *s, const float *x, const float *inv, int m, int k, int nthreads);
+void oracle_w8a8_accumulate(int32_t *acc, const uint8_t *u, const uint8_t *blob, int m, int k, int n,
+                            int nthreads);
+void oracle_w8a8_output(float *y, const int32_t *acc, const float *s, const uint8_t *blob, int m, int k, int n,
+                        int nthreads);
+void oracle_w8a8_linear(float *y, const float *x, const uint8_t *blob, int m, int k, int n, int nthreads);
+void oracle_w8a8_planes(uint8_t *out, const int32_t *acc, int m, int n);
+
+/* ---- epilogues ----------------------------------------------------------- */
+float oracle_gelu_tanh(float z);
+float oracle_quick_gelu(float z);
+void oracle_gelu_tanh_inplace(float *y, size_t count);
+
+/* ---- packed F16 GEMM -------------------------------------------------------- */
+size_t oracle_f16_permuted_index(int k_total, int k_idx, int n_idx);
+void oracle_f16_permute(uint16_t *permuted, const uint16_t *w_kn, int k, int n);
+void oracle_f16_gemm_epilogue(float *y, const float *x, const uint16_t *permuted, const float *bias, int m, int k,
+                              int n, int channels, int mode, int nthreads);
+
+/* ---- deterministic inputs --------------------------------------------------- */
+uint64_t oracle_splitmix64(uint64_t *state);
+void oracle_fill_normal(float *dst, size_t count, float mean, float stddev, uint64_t seed);
+void oracle_fill_uniform(float *dst, size_t count, float lo, float hi, uint64_t seed);
+void oracle_fill_int8(int8_t *dst, size_t count, int lo, int hi, uint64_t seed);
+
+int oracle_num_threads(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HTP_ORACLE_H */

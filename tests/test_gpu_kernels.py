@@ -1,0 +1,209 @@
+"""GPU parity of the hb_* kernels against the CPU oracle, called through the C ABI.
+
+Bar: quantized activations, row scales, int32 accumulators and W8A8 f32
+outputs bit-exact; the W8A8 GELU extension within 1e-5 relative (libm exp2f vs
+device exp2f); F16 GEMM + epilogues within 2e-3 relative to the magnitude of
+the fp16-rounded pre-activation (|y - ref| <= 2e-3 * (|ref| + |v| + |bias|)),
+since one fp16 ulp of v (2^-10 |v|) is the dominant legitimate difference and
+the activations are 1.13-Lipschitz.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def make_w8a8(orc, m, k, n, seed, inv_kind="ones", sums_kind="exact", scale_lo=1e-4, scale_hi=1e-3, outliers=0.0):
+    x = orc.normal(m * k, 0.0, 1.0, seed).reshape(m, k)
+    if outliers:
+        rng = np.random.default_rng(seed + 7)
+        chans = rng.choice(k, max(1, int(outliers * k)), replace=False)
+        x[:, chans] *= 20.0
+    w = orc.int8_uniform(n * k, -127, 127, seed + 1).reshape(n, k)
+    sw = orc.uniform(n, scale_lo, scale_hi, seed + 2)
+    inv = None
+    if inv_kind == "uniform":
+        inv = orc.uniform(k, 0.5, 2.0, seed + 3)
+    sums = None
+    if sums_kind == "random":
+        sums = np.random.default_rng(seed + 4).integers(-2**20, 2**20, n).astype(np.int32)
+    blob = orc.pack_blob(w, sw, sums=sums, inv=inv, signature=seed)
+    return x, w, blob
+
+
+def upload_blob(hip, blob):
+    return hip.DeviceBuffer.from_array(blob)
+
+
+@pytest.mark.parametrize("m,k,inv_kind", [(77, 768, "ones"), (77, 768, "uniform"), (1, 96, "ones"), (5, 32, "uniform"),
+                                          (33, 6144, "uniform"), (4, 14336, "ones"), (130, 1536, "uniform")])
+def test_quantize_bit_exact(hip, orc, m, k, inv_kind):
+    x, _, blob = make_w8a8(orc, m, k, 64, seed=m + k, inv_kind=inv_kind)
+    x[0, :] = 0.0  # zero row: s = 1e-12, u = 128
+    packed = hip.w8a8_prepack(upload_blob(hip, blob), k, 64)
+    xd = hip.DeviceBuffer.from_array(x)
+    inv_ptr = packed.ptr + hip.w8a8_packed_offset(k, 64, hip.SECTION_INV)
+    q, s = hip.w8a8_quantize(xd, inv_ptr, m, k)
+    kp = hip.kp_of(k)
+    qh = q.read(np.int8, m * kp).reshape(m, kp)
+    sh = s.read(np.float32, m)
+    inv = np.frombuffer(blob[128 + k * 64 + 8 * 64:].tobytes(), np.float32)[:k]
+    u_ref, s_ref = orc.quantize(x, inv)
+    np.testing.assert_array_equal(sh.view(np.uint32), s_ref.view(np.uint32))
+    np.testing.assert_array_equal((qh[:, :k].astype(np.int16) + 128).astype(np.uint8), u_ref)
+    assert not qh[:, k:].any()
+    assert sh[0] == np.float32(1e-12) and (u_ref[0] == 128).all()
+
+
+def test_prepack_layout(hip, orc):
+    k, n = 96, 64  # k % 64 == 32 exercises the zero padding
+    _, w, blob = make_w8a8(orc, 2, k, n, seed=3, sums_kind="random")
+    packed = hip.w8a8_prepack(upload_blob(hip, blob), k, n)
+    kp = hip.kp_of(k)
+    img = packed.read(np.int8, n * kp)
+    nn, kk = np.meshgrid(np.arange(n), np.arange(kp), indexing="ij")
+    idx = ((nn // 16) * (kp // 64) + kk // 64) * 1024 + ((nn % 16) + 16 * ((kk % 64) // 16)) * 16 + kk % 16
+    expect = np.zeros((n, kp), np.int8)
+    expect[:, :k] = w
+    np.testing.assert_array_equal(img[idx], expect)
+    sums = np.frombuffer(blob[128 + k * n + 4 * n:128 + k * n + 8 * n].tobytes(), np.int32)
+    wsum = w.astype(np.int64).sum(axis=1)
+    delta = packed.read(np.int32, n, hip.w8a8_packed_offset(k, n, hip.SECTION_DELTA))
+    wsum128 = packed.read(np.int32, n, hip.w8a8_packed_offset(k, n, hip.SECTION_WSUM128))
+    np.testing.assert_array_equal(delta, ((wsum - sums) * 128).astype(np.int64).astype(np.uint32).view(np.int32))
+    np.testing.assert_array_equal(wsum128, (wsum * 128).astype(np.int32))
+
+
+GEMM_SHAPES = [
+    (5, 64, 128),      # small tile path, M tail
+    (77, 768, 3072),   # C1
+    (1, 4096, 1024),   # decode, 8-wave variant
+    (4, 4096, 512),    # decode
+    (16, 1024, 2048),  # decode, full 16 rows
+    (16, 14336, 256),  # decode, K beyond the reference envelope
+    (1, 96, 64),       # decode, K % 64 == 32
+    (300, 1536, 768),  # 64x64 tiles
+    (2048, 128, 2048),  # 128x128 tiles
+    (4096, 64, 4096),  # 256x256 tiles
+    (1000, 96, 4096),  # 256x256 tiles with M tail and K % 64 == 32
+]
+
+
+@pytest.mark.parametrize("m,k,n", GEMM_SHAPES)
+def test_w8a8_raw_accumulator_bit_exact(hip, orc, m, k, n):
+    x, _, blob = make_w8a8(orc, m, k, n, seed=m * 7 + n, inv_kind="uniform", sums_kind="random")
+    packed = hip.w8a8_prepack(upload_blob(hip, blob), k, n)
+    xd = hip.DeviceBuffer.from_array(x)
+    q, s = hip.w8a8_quantize(xd, packed.ptr + hip.w8a8_packed_offset(k, n, hip.SECTION_INV), m, k)
+    raw = hip.DeviceBuffer(m * n * 4)
+    hip.w8a8_gemm(raw, q, s, packed, m, k, n, hip.EPI_RAW)
+    hip.sync()
+    inv = np.frombuffer(blob[128 + k * n + 8 * n:].tobytes(), np.float32)[:k]
+    u, _ = orc.quantize(x, inv)
+    acc_ref = orc.accumulate(u, blob, k, n)
+    np.testing.assert_array_equal(raw.read(np.int32, m * n).reshape(m, n), acc_ref)
+
+
+@pytest.mark.parametrize("m,k,n", GEMM_SHAPES)
+def test_w8a8_linear_bit_exact(hip, orc, m, k, n):
+    x, _, blob = make_w8a8(orc, m, k, n, seed=m + 3 * n + k, inv_kind="uniform", sums_kind="random",
+                           outliers=0.01)
+    packed = hip.w8a8_prepack(upload_blob(hip, blob), k, n)
+    xd = hip.DeviceBuffer.from_array(x)
+    ws = hip.DeviceBuffer(hip.w8a8_workspace_bytes(m, k))
+    y = hip.DeviceBuffer(m * n * 4)
+    hip.w8a8_linear(y, xd, packed, m, k, n, ws)
+    hip.sync()
+    ref = orc.linear(x, blob, k, n)
+    got = y.read(np.float32, m * n).reshape(m, n)
+    np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("m,k,n", [(77, 768, 3072), (4, 1536, 1024), (1000, 96, 4096)])
+def test_w8a8_gelu_epilogue(hip, orc, m, k, n):
+    x, _, blob = make_w8a8(orc, m, k, n, seed=11, scale_lo=1e-3, scale_hi=1e-2)
+    packed = hip.w8a8_prepack(upload_blob(hip, blob), k, n)
+    xd = hip.DeviceBuffer.from_array(x)
+    ws = hip.DeviceBuffer(hip.w8a8_workspace_bytes(m, k))
+    y = hip.DeviceBuffer(m * n * 4)
+    hip.w8a8_linear(y, xd, packed, m, k, n, ws, epilogue=hip.EPI_SCALE_GELU)
+    hip.sync()
+    ref = orc.gelu_tanh_array(orc.linear(x, blob, k, n))
+    got = y.read(np.float32, m * n).reshape(m, n)
+    np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-30)
+
+
+def test_w8a8_planes_export(hip, orc):
+    m, k, n = 77, 64, 128
+    x, _, blob = make_w8a8(orc, m, k, n, seed=5)
+    packed = hip.w8a8_prepack(upload_blob(hip, blob), k, n)
+    xd = hip.DeviceBuffer.from_array(x)
+    q, s = hip.w8a8_quantize(xd, packed.ptr + hip.w8a8_packed_offset(k, n, hip.SECTION_INV), m, k)
+    raw = hip.DeviceBuffer(m * n * 4)
+    hip.w8a8_gemm(raw, q, s, packed, m, k, n, hip.EPI_RAW)
+    planes = hip.DeviceBuffer(m * n * 4)
+    hip.w8a8_planes_from_raw(planes, raw, m, n)
+    hip.sync()
+    acc = raw.read(np.int32, m * n).reshape(m, n)
+    np.testing.assert_array_equal(planes.read(np.uint8, m * n * 4), orc.planes(acc))
+
+
+def f16_case(orc, m, k, n, seed, bias=True):
+    x = orc.normal(m * k, 0.0, 1.0, seed).reshape(m, k)
+    w = orc.normal(k * n, 0.0, 0.02, seed + 1).reshape(k, n)
+    wbits = w.astype(np.float16).view(np.uint16)
+    perm = orc.f16_permute(wbits)
+    b = orc.normal(n, 0.0, 0.02, seed + 2) if bias else None
+    return x, perm, b
+
+
+def f16_check(got, ref, v_ref, bias_cols):
+    bound = 2e-3 * (np.abs(ref) + np.abs(v_ref) + bias_cols)
+    assert np.all(np.isfinite(got))
+    bad = np.abs(got - ref) > bound
+    assert not bad.any(), f"{bad.sum()} elements out of tolerance; worst {np.max(np.abs(got - ref) - bound)}"
+
+
+@pytest.mark.parametrize("m,k,n,mode,channels,bias", [
+    (77, 768, 3072, 2, 3072, True),   # C2 first GEMM: QuickGELU
+    (77, 3072, 768, 0, 768, True),    # C2 second GEMM: bias only
+    (77, 768, 3072, 1, 3072, True),   # GELU
+    (77, 768, 3072, 1, 3072, False),  # GELU without bias
+    (64, 96, 64, 0, 64, False),       # opcode-1 semantics, K % 64 == 32
+    (300, 256, 512, 3, 480, True),    # channel-major store, channels < n
+    (1024, 256, 4096, 0, 4096, True), # 128x128 tiles
+    (1, 128, 32, 2, 32, True),
+])
+def test_f16_gemm_epilogue(hip, orc, m, k, n, mode, channels, bias):
+    x, perm, b = f16_case(orc, m, k, n, seed=m + n + mode, bias=bias)
+    permd = hip.DeviceBuffer.from_array(perm)
+    packed = hip.f16_prepack(permd, k, n)
+    xd = hip.DeviceBuffer.from_array(x)
+    bd = hip.DeviceBuffer.from_array(b[:channels] if b is not None else np.zeros(1, np.float32)) if bias else None
+    out_elems = m * (channels if mode == 3 else n)
+    y = hip.DeviceBuffer(out_elems * 4)
+    hip.f16_gemm(y, xd, packed, bd, m, k, n, channels, mode)
+    hip.sync()
+    got = y.read(np.float32, out_elems)
+    ref = orc.f16_gemm_epilogue(x, perm, None if b is None else b[:channels].copy() if mode == 3 else b, m, k, n,
+                                channels, mode)
+    v_ref = orc.f16_gemm_epilogue(x, perm, None, m, k, n, n, 0)
+    if mode == 3:
+        got = got.reshape(channels, m)
+        v_ref = v_ref.T[:channels]
+        bias_cols = np.abs(b[:channels])[:, None] if b is not None else 0.0
+    else:
+        got = got.reshape(m, n)
+        bias_cols = np.abs(b)[None, :] if b is not None else 0.0
+    f16_check(got, ref, v_ref, bias_cols)
+
+
+def test_f16_all_ones_gives_k(hip, orc):
+    m, k, n = 32, 256, 64
+    x = np.ones((m, k), np.float32)
+    perm = orc.f16_permute(np.ones((k, n), np.float16).view(np.uint16))
+    packed = hip.f16_prepack(hip.DeviceBuffer.from_array(perm), k, n)
+    y = hip.DeviceBuffer(m * n * 4)
+    hip.f16_gemm(y, hip.DeviceBuffer.from_array(x), packed, None, m, k, n, n, 0)
+    hip.sync()
+    assert (y.read(np.float32, m * n) == k).all()
