@@ -1,0 +1,450 @@
+/*
+ * Request executor for opcodes 1, 15 and 16.
+ *
+ * Validation order and return codes follow the reference dispatcher
+ * (reference src/dsp/op_executor.cc:274-540) and its kernels' argument checks
+ * (reference src/dsp/ops/linear_w8a8.c:337-338, src/dsp/ops/mat_mul.c:939-955):
+ * every check that can fail does so before any GPU work is queued.  Compute
+ * runs on the library stream; host-resident tensors are staged through their
+ * device mirrors, HBM-resident tensors are used in place, and outputs are
+ * host-visible when the call returns.
+ */
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+#include <time.h>
+
+#include "host_internal.h"
+#include "htp_ops/executor.h"
+#include "htp_ops/op_reg.h"
+
+/* Envelope of opcode 15.  The reference accepts m <= 4096 and k <= 6144
+ * (reference src/dsp/op_executor.cc:320); this library extends both (the
+ * int32 accumulator stays exact while 255*128*k < 2^31, i.e. k < 65793). */
+#define W8A8_MAX_M 65536
+#define W8A8_MAX_K 32768
+#define W8A8_MAX_N 65536
+
+#define QTIMER_HZ 19200000.0
+
+static pthread_mutex_t g_exec_lock = PTHREAD_MUTEX_INITIALIZER;
+static void *g_scratch[4];
+static size_t g_scratch_size[4];
+static __thread int t_device_ready = 0;
+
+int htp_executor_ensure_device(void) {
+  if (t_device_ready) return 0;
+  const int rc = hb_init(htp_backend_device());
+  if (rc != HB_OK) return rc;
+  t_device_ready = 1;
+  return 0;
+}
+
+hb_stream htp_executor_stream(void) { return hb_default_stream(); }
+
+void *htp_executor_scratch(int slot, size_t bytes) {
+  if (slot < 0 || slot >= 4) return NULL;
+  if (bytes == 0) bytes = 256;
+  if (g_scratch_size[slot] < bytes) {
+    if (g_scratch[slot]) hb_free(g_scratch[slot]);
+    g_scratch[slot] = NULL;
+    g_scratch_size[slot] = 0;
+    const size_t grown = bytes + bytes / 4;
+    if (hb_malloc(&g_scratch[slot], grown) != HB_OK) return NULL;
+    g_scratch_size[slot] = grown;
+  }
+  return g_scratch[slot];
+}
+
+static double now_seconds(void) {
+  struct timespec ts;
+  clock_gettime(CLOCK_MONOTONIC, &ts);
+  return (double)ts.tv_sec + (double)ts.tv_nsec * 1e-9;
+}
+
+static int checked_mul(size_t a, size_t b, size_t *out) {
+  if (a != 0 && b > SIZE_MAX / a) return 0;
+  *out = a * b;
+  return 1;
+}
+
+/* Content signature of a host-resident weight: FNV-1a of the first 128 bytes
+ * plus 64 evenly spaced 64-byte samples.  HBM-resident weights change only
+ * through this library, which bumps the fd generation instead. */
+static uint64_t weight_signature(const htp_view *v) {
+  if (v->is_device || !v->host) return 0;
+  uint64_t h = htp_fnv1a64(v->host, v->bytes < 128 ? v->bytes : 128);
+  if (v->bytes > 128) {
+    const size_t span = v->bytes - 128;
+    for (int i = 0; i < 64; ++i) {
+      const size_t off = 128 + span / 64 * (size_t)i;
+      const size_t len = v->bytes - off < 64 ? v->bytes - off : 64;
+      h ^= htp_fnv1a64(v->host + off, len) + 0x9e3779b97f4a7c15ull * (uint64_t)(i + 1);
+    }
+  }
+  return h;
+}
+
+/* Resolves a tensor without touching the GPU; maps registry errors to the
+ * opcode's "unmapped" code. */
+static int resolve(const struct RpcmemBufAddr *a, size_t bytes, htp_view *v, int unmapped_code) {
+  const int rc = htp_registry_host_view(a->fd, a->offset, bytes, v);
+  if (rc == -1) return unmapped_code;
+  if (rc != 0) return -5;
+  return 0;
+}
+
+/* After validation: gives a host-resident view its device mirror. */
+static int materialize(htp_view *v) {
+  if (v->dev) return 0;
+  return htp_registry_view(v->fd, (int64_t)v->offset, v->bytes, v) == 0 ? 0 : -5;
+}
+
+static int stage_in(const htp_view *v, hb_stream s) {
+  if (v->is_device || v->bytes == 0) return 0;
+  return hb_memcpy_h2d(v->dev, v->host, v->bytes, s) == HB_OK ? 0 : -5;
+}
+
+static int stage_out(const htp_view *v, hb_stream s) {
+  if (v->is_device || v->bytes == 0) return 0;
+  return hb_memcpy_d2h(v->host, v->dev, v->bytes, s) == HB_OK ? 0 : -5;
+}
+
+/* A device pointer with at least `align` alignment holding the view's bytes
+ * (the view itself, or a copy in scratch slot `slot`). */
+static const void *aligned_input(const htp_view *v, size_t align, int slot, hb_stream s) {
+  if (((uintptr_t)v->dev % align) == 0) return v->dev;
+  void *tmp = htp_executor_scratch(slot, v->bytes);
+  if (!tmp || hb_memcpy_d2d(tmp, v->dev, v->bytes, s) != HB_OK) return NULL;
+  return tmp;
+}
+
+typedef struct {
+  hb_event e[5];
+  int n;
+} event_set;
+
+static int events_open(event_set *ev, int count) {
+  ev->n = 0;
+  for (int i = 0; i < count; ++i) {
+    if (hb_event_create(&ev->e[i]) != HB_OK) return -5;
+    ev->n = i + 1;
+  }
+  return 0;
+}
+
+static void events_close(event_set *ev) {
+  for (int i = 0; i < ev->n; ++i) hb_event_destroy(ev->e[i]);
+  ev->n = 0;
+}
+
+static double event_ms(const event_set *ev, int a, int b) {
+  float ms = 0.0f;
+  if (hb_event_elapsed_ms(&ms, ev->e[a], ev->e[b]) != HB_OK) return 0.0;
+  return (double)ms;
+}
+
+/* ---- opcode 15 --------------------------------------------------------------- */
+
+static int exec_w8a8(uint8_t *payload, size_t payload_size) {
+  /* reference src/dsp/op_executor.cc:314-353 */
+  if (payload_size != sizeof(struct NativeW8A8Params) && payload_size != sizeof(struct NativeW8A8ProfileParams) &&
+      payload_size != sizeof(struct NativeW8A8CpuParams))
+    return -1;
+  struct NativeW8A8Params p;
+  memcpy(&p, payload, sizeof(p));
+  const int m = p.m, k = p.k, n = p.n;
+  if (m < 1 || m > W8A8_MAX_M || k < 32 || k > W8A8_MAX_K || k % 32 || n < 64 || n > W8A8_MAX_N || n % 64)
+    return -1;
+  const int cpu_output = payload_size == sizeof(struct NativeW8A8CpuParams);
+  const int profiled = payload_size == sizeof(struct NativeW8A8ProfileParams);
+  if (cpu_output && m > 4096) return -1; /* W8A8CpuControl.scales holds 4096 rows */
+  const size_t constants_size = 128u + (size_t)k * n + (size_t)n * 8u + (size_t)k * 4u;
+  htp_view out, act, cst, ctl;
+  int rc = resolve(&p.output, (size_t)m * n * 4u, &out, -2);
+  if (!rc) rc = resolve(&p.activation, (size_t)m * k * 4u, &act, -2);
+  if (!rc) rc = resolve(&p.constants, constants_size, &cst, -2);
+  struct NativeW8A8CpuParams cp;
+  if (!rc && cpu_output) {
+    memcpy(&cp, payload, sizeof(cp));
+    rc = resolve(&cp.control, sizeof(struct W8A8CpuControl), &ctl, -2);
+  }
+  if (rc) return rc;
+
+  /* Header acceptance, reference src/dsp/op_executor.cc:331-335. */
+  struct W8A8Header h;
+  if (cst.is_device) {
+    if (hb_memcpy_d2h(&h, cst.dev, sizeof(h), htp_executor_stream()) != HB_OK) return -5;
+  } else {
+    memcpy(&h, cst.host, sizeof(h));
+  }
+  const size_t scale_off = 128u + (size_t)k * n;
+  if (h.magic != W8A8_BLOB_MAGIC || h.version != W8A8_BLOB_VERSION || h.k != (uint32_t)k || h.n != (uint32_t)n ||
+      h.weight_offset != 128u || h.scale_offset != scale_off || h.sum_offset != scale_off + (size_t)n * 4u ||
+      h.inverse_offset != (size_t)h.sum_offset + (size_t)n * 4u || h.bytes != constants_size)
+    return -3;
+
+  struct NativeW8A8Profile profile;
+  memset(&profile, 0, sizeof(profile));
+  if (profiled) {
+    memcpy(&profile, payload + sizeof(struct NativeW8A8Params), sizeof(profile));
+    if (profile.mode != 1 && profile.mode != 2 && profile.mode != 3) return -1;
+    const uint32_t mode = profile.mode;
+    memset(&profile, 0, sizeof(profile));
+    profile.mode = mode;
+  }
+
+  const double t_setup = now_seconds();
+  if (htp_executor_ensure_device() != 0) return -5;
+  if (materialize(&out) || materialize(&act) || materialize(&cst) || (cpu_output && materialize(&ctl))) return -5;
+  hb_stream s = htp_executor_stream();
+  void *packed = NULL;
+  int built = 0;
+  const double t_w0 = now_seconds();
+  rc = htp_weight_cache_get(HTP_WEIGHT_W8A8, &cst, k, n, weight_signature(&cst), &packed, &built, s);
+  if (rc) return rc;
+  const double t_w1 = now_seconds();
+  if (stage_in(&act, s)) return -5;
+  const float *x = (const float *)aligned_input(&act, 16, 2, s);
+  if (!x) return -5;
+  const size_t ws_bytes = hb_w8a8_workspace_bytes(m, k);
+  uint8_t *ws = (uint8_t *)htp_executor_scratch(0, ws_bytes);
+  if (!ws) return -5;
+  int8_t *q = (int8_t *)ws;
+  const size_t q_bytes = ((size_t)(m + 15) / 16 * 16) * ((size_t)(k + 63) / 64 * 64);
+  float *scales = (float *)(ws + (q_bytes + 255u) / 256u * 256u); /* layout of hb_w8a8_workspace_bytes */
+  const float *inv = (const float *)((const uint8_t *)packed + hb_w8a8_packed_offset(k, n, HB_W8A8_INV));
+  float *y = ((uintptr_t)out.dev % 4u) == 0 ? (float *)out.dev : (float *)htp_executor_scratch(3, out.bytes);
+  void *raw = cpu_output ? htp_executor_scratch(1, (size_t)m * n * 4u) : NULL;
+  if (!y || (cpu_output && !raw)) return -5;
+
+  event_set ev;
+  if (events_open(&ev, 4)) {
+    events_close(&ev);
+    return -5;
+  }
+  int hrc = hb_event_record(ev.e[0], s);
+  if (!hrc) hrc = hb_w8a8_quantize(q, scales, x, inv, m, k, s);
+  if (!hrc) hrc = hb_event_record(ev.e[1], s);
+  if (!hrc) {
+    hrc = cpu_output ? hb_w8a8_gemm(raw, n, q, scales, packed, m, k, n, HB_W8A8_EPI_RAW, s)
+                     : hb_w8a8_gemm(y, n, q, scales, packed, m, k, n, HB_W8A8_EPI_SCALE, s);
+  }
+  if (!hrc) hrc = hb_event_record(ev.e[2], s);
+  if (!hrc && cpu_output) hrc = hb_w8a8_planes_from_raw((uint8_t *)y, (const int32_t *)raw, m, n, s);
+  if (!hrc) hrc = hb_event_record(ev.e[3], s);
+  if (!hrc && (void *)y != (void *)out.dev) hrc = hb_memcpy_d2d(out.dev, y, out.bytes, s);
+  if (!hrc) hrc = hb_stream_sync(s);
+  if (hrc) {
+    events_close(&ev);
+    return hrc == HB_E_INVAL ? -10 : -5;
+  }
+  const double quant_ms = event_ms(&ev, 0, 1), gemm_ms = event_ms(&ev, 1, 2), out_ms = event_ms(&ev, 2, 3);
+  events_close(&ev);
+  const double weight_s = built ? t_w1 - t_w0 : 0.0;
+
+  if (cpu_output) {
+    /* Publish row scales and one batch covering every row
+     * (reference src/dsp/ops/linear_w8a8.c:413-438, :512-526). */
+    struct W8A8CpuControl *c = (struct W8A8CpuControl *)malloc(sizeof(*c));
+    if (!c) return -5;
+    int crc = 0;
+    if (ctl.is_device) crc = hb_memcpy_d2h(c, ctl.dev, sizeof(*c), s) != HB_OK;
+    else memcpy(c, ctl.host, sizeof(*c));
+    if (!crc) crc = hb_memcpy_d2h(c->scales, scales, (size_t)m * 4u, s) != HB_OK;
+    if (!crc) {
+      c->vtcm_bytes = 0;
+      c->activation_rows = (uint32_t)((m + 63) / 64 * 64);
+      c->weight_columns = (uint32_t)(n / 64);
+      c->weight_loads = built ? 1u : 0u;
+      c->weight_loaded_bytes = built ? (uint64_t)k * n : 0u;
+      c->batches[0].m0 = 0;
+      c->batches[0].rows = m;
+      c->batches[0].n0 = 0;
+      c->batches[0].columns = n / 64;
+      c->produced = 1;
+      if (ctl.is_device) crc = hb_memcpy_h2d(ctl.dev, c, sizeof(*c), s) != HB_OK;
+      else memcpy(ctl.host, c, sizeof(*c));
+    }
+    free(c);
+    if (crc) return -5;
+  }
+  if (stage_out(&out, s)) return -5;
+  htp_registry_touch(out.fd);
+
+  const double total_us = (quant_ms + gemm_ms + out_ms) * 1e3 + weight_s * 1e6;
+  p.elapsed_us = (int32_t)total_us;
+  memcpy(payload + offsetof(struct NativeW8A8Params, elapsed_us), &p.elapsed_us, sizeof(int32_t));
+  if (profiled) {
+    profile.setup_ticks = (uint64_t)((t_w0 - t_setup) * QTIMER_HZ);
+    profile.activation_ticks = (uint64_t)(quant_ms * 1e-3 * QTIMER_HZ);
+    profile.weight_ticks = (uint64_t)(weight_s * QTIMER_HZ);
+    profile.hmx_ticks = (uint64_t)(gemm_ms * 1e-3 * QTIMER_HZ);
+    profile.output_ticks = (uint64_t)(out_ms * 1e-3 * QTIMER_HZ);
+    if (profile.mode == 2) {
+      /* The epilogue is fused into the GEMM: all GEMM time counts as MAC time. */
+      profile.mac_ticks = profile.hmx_ticks;
+      profile.readout_ticks = 0;
+    } else if (profile.mode == 3) {
+      /* reserved: low 16 bits = rows per workgroup tile, high 16 = columns;
+       * mac/readout = weight loads / bytes during this call. */
+      const uint32_t bm = m <= 16 ? 16u : 0u, bn = 16u;
+      profile.reserved = bm | (bn << 16);
+      profile.mac_ticks = built ? 1u : 0u;
+      profile.readout_ticks = built ? (uint64_t)k * n : 0u;
+    }
+    memcpy(payload + sizeof(struct NativeW8A8Params), &profile, sizeof(profile));
+  }
+  return 0;
+}
+
+/* ---- opcodes 16 and 1 -------------------------------------------------------- */
+
+static uintptr_t primary_address(const htp_view *v) {
+  return v->is_device ? (uintptr_t)v->dev : (uintptr_t)v->host;
+}
+
+/* Shared F16 compute after validation.  Returns 0 or a negative code. */
+static int run_f16(htp_view *out, htp_view *act, htp_view *wgt, htp_view *bias, int m, int k, int n, int channels,
+                   int mode, int32_t *elapsed_us) {
+  if (htp_executor_ensure_device() != 0) return -5;
+  if (materialize(out) || materialize(act) || materialize(wgt) || (bias && materialize(bias))) return -5;
+  hb_stream s = htp_executor_stream();
+  void *packed = NULL;
+  int built = 0;
+  const double t_w0 = now_seconds();
+  int rc = htp_weight_cache_get(HTP_WEIGHT_F16, wgt, k, n, weight_signature(wgt), &packed, &built, s);
+  if (rc) return rc;
+  const double t_w1 = now_seconds();
+  if (stage_in(act, s)) return -5;
+  const float *x = (const float *)aligned_input(act, 16, 2, s);
+  if (!x) return -5;
+  const float *b = NULL;
+  if (bias) {
+    if (stage_in(bias, s)) return -5;
+    b = (const float *)aligned_input(bias, 4, 1, s);
+    if (!b) return -5;
+  }
+  const size_t out_bytes = out->bytes;
+  float *y = ((uintptr_t)out->dev % 4u) == 0 ? (float *)out->dev : (float *)htp_executor_scratch(3, out_bytes);
+  if (!y) return -5;
+  event_set ev;
+  if (events_open(&ev, 2)) {
+    events_close(&ev);
+    return -5;
+  }
+  int hrc = hb_event_record(ev.e[0], s);
+  if (!hrc) hrc = hb_f16_gemm(y, x, (const uint16_t *)packed, b, m, k, n, channels, mode, s);
+  if (!hrc) hrc = hb_event_record(ev.e[1], s);
+  if (!hrc && (void *)y != (void *)out->dev) hrc = hb_memcpy_d2d(out->dev, y, out_bytes, s);
+  if (!hrc) hrc = hb_stream_sync(s);
+  const double gemm_ms = hrc ? 0.0 : event_ms(&ev, 0, 1);
+  events_close(&ev);
+  if (hrc) return hrc == HB_E_INVAL ? -11 : -5;
+  if (stage_out(out, s)) return -5;
+  htp_registry_touch(out->fd);
+  if (elapsed_us) *elapsed_us = (int32_t)(gemm_ms * 1e3 + (built ? (t_w1 - t_w0) * 1e6 : 0.0));
+  return 0;
+}
+
+static int exec_f16_epilogue(uint8_t *payload, size_t payload_size) {
+  /* reference src/dsp/op_executor.cc:446-471, src/dsp/ops/mat_mul.c:937-955 */
+  if (payload_size != sizeof(struct F16EpilogueParams)) return -1;
+  struct F16EpilogueParams p;
+  memcpy(&p, payload, sizeof(p));
+  if (p.m <= 0 || p.k <= 0 || p.n <= 0 || p.k % 32 || p.n % 32 || p.channels <= 0 || p.channels > p.n ||
+      p.mode < 0 || p.mode > 3 || (p.mode != 3 && p.channels != p.n))
+    return -1;
+  size_t out_size, act_size, weight_size;
+  if (!checked_mul((size_t)p.m, (size_t)p.channels * sizeof(float), &out_size) ||
+      !checked_mul((size_t)p.m, (size_t)p.k * sizeof(float), &act_size) ||
+      !checked_mul((size_t)p.k, (size_t)p.n * 2u, &weight_size))
+    return -1;
+  htp_view out, act, wgt, bias;
+  int rc = resolve(&p.output, out_size, &out, -1);
+  if (!rc) rc = resolve(&p.activation, act_size, &act, -1);
+  if (!rc) rc = resolve(&p.weight, weight_size, &wgt, -1);
+  if (!rc && p.bias.fd >= 0) rc = resolve(&p.bias, (size_t)p.channels * sizeof(float), &bias, -1);
+  if (rc) return rc;
+  /* Kernel alignment contract: 128-byte aligned dst/activation/weight
+   * (reference src/dsp/ops/mat_mul.c:947-949). */
+  if ((primary_address(&out) | primary_address(&act) | primary_address(&wgt)) & 127u) return -12;
+  int32_t elapsed = 0;
+  rc = run_f16(&out, &act, &wgt, p.bias.fd >= 0 ? &bias : NULL, p.m, p.k, p.n, p.channels, p.mode, &elapsed);
+  if (rc) return rc;
+  memcpy(payload + offsetof(struct F16EpilogueParams, elapsed_us), &elapsed, sizeof(elapsed));
+  return 0;
+}
+
+static int exec_matmul_params(const struct MatMulParams *p, int32_t *elapsed_us, uint64_t *act_hash,
+                              uint64_t *out_hash) {
+  /* reference src/dsp/op_executor.cc:473-540, src/dsp/ops/mat_mul.c:1046-1049 */
+  const int m = p->m, k = p->k, n = p->n;
+  const int dims_ok = m > 0 && k > 0 && n > 0;
+  htp_view out, act, wgt;
+  int rc = resolve(&p->output, dims_ok ? (size_t)m * n * 4u : 0, &out, -2);
+  if (!rc) rc = resolve(&p->activation, dims_ok ? (size_t)m * k * 4u : 0, &act, -2);
+  if (!rc) rc = resolve(&p->weight, dims_ok ? (size_t)k * n * 2u : 0, &wgt, -2);
+  if (rc) return rc;
+  if ((primary_address(&out) | primary_address(&act) | primary_address(&wgt)) & 127u) return -3;
+  if (m == 0 || n == 0 || k == 0) return -10;
+  if (!dims_ok || k % 32 || n % 32) return -11;
+  if (act_hash) {
+    *act_hash = 0;
+    if (act.host) *act_hash = htp_fnv1a64(act.host, act.bytes);
+  }
+  rc = run_f16(&out, &act, &wgt, NULL, m, k, n, n, 0, elapsed_us);
+  if (rc) return rc;
+  if (out_hash) {
+    *out_hash = 0;
+    if (out.host) *out_hash = htp_fnv1a64(out.host, out.bytes);
+  }
+  return 0;
+}
+
+static int exec_matmul(uint8_t *payload, size_t payload_size) {
+  if (payload_size < sizeof(struct MatMulParams)) return -1;
+  struct MatMulParams p;
+  memcpy(&p, payload, sizeof(p));
+  int32_t elapsed = 0;
+  const int rc = exec_matmul_params(&p, &elapsed, NULL, NULL);
+  if (rc == 0 && payload_size >= sizeof(struct MatMulProfileParams))
+    memcpy(payload + offsetof(struct MatMulProfileParams, elapsed_us), &elapsed, sizeof(elapsed));
+  return rc;
+}
+
+/* Direct (non-mailbox) opcode-1 entry used by htp_ops_mat_mul_permuted_w16a32[_trace]. */
+int htp_exec_matmul_w16a32(const struct MatMulParams *p, int32_t *elapsed_us, uint64_t *act_hash,
+                           uint64_t *out_hash) {
+  pthread_mutex_lock(&g_exec_lock);
+  const int rc = exec_matmul_params(p, elapsed_us, act_hash, out_hash);
+  pthread_mutex_unlock(&g_exec_lock);
+  return rc;
+}
+
+/* ---- dispatcher ---------------------------------------------------------------- */
+
+int execute_op_simple(struct OpComputeRequest *req, size_t req_size) {
+  if (req == NULL || req_size < sizeof(struct OpComputeRequest)) return -1;
+  const size_t payload_size = req_size - sizeof(struct OpComputeRequest);
+  uint8_t *payload = (uint8_t *)req + sizeof(struct OpComputeRequest);
+  uint32_t op;
+  memcpy(&op, req, sizeof(op));
+  int rc;
+  pthread_mutex_lock(&g_exec_lock);
+  switch (op) {
+    case HTP_OPS_MAT_MUL_NATIVE_W8A8: rc = exec_w8a8(payload, payload_size); break;
+    case HTP_OPS_MAT_MUL_F16_EPILOGUE: rc = exec_f16_epilogue(payload, payload_size); break;
+    case HTP_OPS_MAT_MUL_PERMUTED_W16A32: rc = exec_matmul(payload, payload_size); break;
+    default: rc = HTP_OPS_E_UNSUPPORTED; break;
+  }
+  pthread_mutex_unlock(&g_exec_lock);
+  return rc;
+}
+
+int htp_ops_execute_message(struct MessageHeader *msg, size_t capacity) {
+  size_t total = 0;
+  if (!message_header_validate_layout(msg, capacity, &total)) return -1;
+  htp_channel_process(NULL, msg, capacity, 0);
+  return 0;
+}

@@ -139,6 +139,12 @@ _HOST_SIGNATURES = {
     "htp_ops_native_model_version": (_c_int, []),
     "htp_ops_dit_aux_version": (_c_int, []),
     "htp_ops_dit_concat_version": (_c_int, []),
+    "htp_ops_w8a8_constants_bytes": (_c_size_t, [_c_int, _c_int]),
+    "htp_ops_w8a8_pack_constants": (_c_int, [_c_void_p, _c_size_t, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                             _c_int, _c_int, ctypes.c_uint64]),
+    "htp_ops_w8a8_quantize_weights": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int]),
+    "htp_ops_fnv1a64": (ctypes.c_uint64, [_c_void_p, _c_size_t]),
+    "htp_ops_f16_permute_weights": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_int]),
 }
 
 _lib = None
@@ -335,3 +341,175 @@ class Event:
 
 def default_stream():
     return lib().hb_default_stream()
+
+
+# ---- host packers ------------------------------------------------------------
+
+def _arr_ptr(a):
+    return None if a is None else a.ctypes.data
+
+
+def pack_constants(w_nk, sw, sums=None, inv=None, signature=0):
+    """int8 weights [n][k] + per-column scales -> W8A8 constants blob (uint8)."""
+    w_nk = np.ascontiguousarray(w_nk, np.int8)
+    n, k = w_nk.shape
+    nbytes = lib().htp_ops_w8a8_constants_bytes(k, n)
+    blob = np.zeros(nbytes, np.uint8)
+    sw = np.ascontiguousarray(sw, np.float32)
+    sums = None if sums is None else np.ascontiguousarray(sums, np.int32)
+    inv = None if inv is None else np.ascontiguousarray(inv, np.float32)
+    rc = lib().htp_ops_w8a8_pack_constants(blob.ctypes.data, nbytes, w_nk.ctypes.data, sw.ctypes.data,
+                                           _arr_ptr(sums), _arr_ptr(inv), k, n, signature)
+    if rc != 0:
+        raise HtpOpsError(f"htp_ops_w8a8_pack_constants failed ({rc})")
+    return blob
+
+
+def quantize_weights(w_nk_f32, inv=None):
+    w = np.ascontiguousarray(w_nk_f32, np.float32)
+    n, k = w.shape
+    q = np.empty((n, k), np.int8)
+    sw = np.empty(n, np.float32)
+    inv = None if inv is None else np.ascontiguousarray(inv, np.float32)
+    rc = lib().htp_ops_w8a8_quantize_weights(q.ctypes.data, sw.ctypes.data, w.ctypes.data, _arr_ptr(inv), k, n)
+    if rc != 0:
+        raise HtpOpsError("htp_ops_w8a8_quantize_weights failed")
+    return q, sw
+
+
+def permute_f16(w_kn_bits):
+    w = np.ascontiguousarray(w_kn_bits, np.uint16)
+    k, n = w.shape
+    out = np.zeros(k * n, np.uint16)
+    rc = lib().htp_ops_f16_permute_weights(out.ctypes.data, w.ctypes.data, k, n)
+    if rc != 0:
+        raise HtpOpsError("htp_ops_f16_permute_weights failed")
+    return out
+
+
+# ---- wire format ---------------------------------------------------------------
+
+import struct as _struct
+
+OP_MAT_MUL_PERMUTED_W16A32 = 1
+OP_MAT_MUL_NATIVE_W8A8 = 15
+OP_MAT_MUL_F16_EPILOGUE = 16
+E_UNSUPPORTED = -95
+REQUEST_TYPE_NO_OP, REQUEST_TYPE_RPCMEM_MAP, REQUEST_TYPE_OP_COMPUTE = 0, 1, 2
+RPCMEM_FLAG_AMD_DEVICE = 1 << 30
+RPCMEM_HEAP_ID_SYSTEM = 25
+AEE_SUCCESS, AEE_EFAILED, AEE_ENOMEMORY, AEE_EBADSTATE, AEE_EBADPARM, AEE_EUNSUPPORTED, AEE_EALREADY = \
+    0, 1, 2, 13, 14, 20, 26
+
+
+def w8a8_params(out, act, cst, m, k, n, elapsed=0):
+    """NativeW8A8Params (40 bytes); out/act/cst are (fd, offset)."""
+    return _struct.pack("<6i4i", *out, *act, *cst, m, k, n, elapsed)
+
+
+def w8a8_profile(mode):
+    """NativeW8A8Profile trailer (64 bytes)."""
+    return _struct.pack("<2I7Q", mode, 0, 0, 0, 0, 0, 0, 0, 0)
+
+
+def unpack_w8a8_profile(raw):
+    f = _struct.unpack("<2I7Q", raw)
+    keys = ("mode", "reserved", "setup_ticks", "activation_ticks", "weight_ticks", "hmx_ticks", "output_ticks",
+            "mac_ticks", "readout_ticks")
+    return dict(zip(keys, f))
+
+
+def f16_epilogue_params(out, act, wgt, bias, m, k, n, channels, mode, elapsed=0):
+    """F16EpilogueParams (56 bytes)."""
+    return _struct.pack("<8i6i", *out, *act, *wgt, *bias, m, k, n, channels, mode, elapsed)
+
+
+def matmul_params(out, act, wgt, m, k, n, with_elapsed=False):
+    """MatMulParams (92 bytes), optionally with the elapsed_us trailer (96)."""
+    raw = _struct.pack("<6i3iQIiiQiQQQ", *out, *act, *wgt, m, k, n, 0, 0, 0, 0, 0, 0, 0, 0, 0)
+    assert len(raw) == 92
+    return raw + (_struct.pack("<i", 0) if with_elapsed else b"")
+
+
+def compute_request(op, payload):
+    """OpComputeRequest bytes: opcode + payload."""
+    return _struct.pack("<I", op) + payload
+
+
+def execute(op, payload):
+    """Runs execute_op_simple on a copy of the request; returns (rc, payload after)."""
+    req = bytearray(compute_request(op, payload))
+    buf = (ctypes.c_uint8 * len(req)).from_buffer(req)
+    rc = lib().execute_op_simple(ctypes.addressof(buf), len(req))
+    return rc, bytes(req[4:])
+
+
+def build_message(requests, capacity):
+    """requests: list of (type, data bytes) -> mailbox bytes (state zeroed)."""
+    n = len(requests)
+    header = 16 + 4 * (n + 1)
+    offsets = [header]
+    for _, data in requests:
+        offsets.append(offsets[-1] + 8 + len(data))
+    assert offsets[-1] <= capacity
+    msg = bytearray(capacity)
+    _struct.pack_into("<QIi", msg, 0, 0, 0, n)
+    _struct.pack_into(f"<{n + 1}i", msg, 16, *offsets)
+    for i, (rtype, data) in enumerate(requests):
+        _struct.pack_into("<ii", msg, offsets[i], 0, rtype)
+        msg[offsets[i] + 8:offsets[i] + 8 + len(data)] = data
+    return msg, offsets
+
+
+def request_state(msg, offsets, i):
+    return _struct.unpack_from("<i", msg, offsets[i])[0]
+
+
+def request_data(msg, offsets, i):
+    return bytes(msg[offsets[i] + 8:offsets[i + 1]])
+
+
+class RpcBuffer:
+    """An rpcmem allocation registered with the library (host or HBM)."""
+
+    def __init__(self, nbytes, device=False, map_it=True):
+        self.nbytes = int(nbytes)
+        self.device = device
+        flags = RPCMEM_FLAG_AMD_DEVICE if device else 0
+        self.ptr = lib().rpcmem_alloc2(RPCMEM_HEAP_ID_SYSTEM, flags, self.nbytes)
+        if not self.ptr:
+            raise HtpOpsError("rpcmem_alloc2 failed")
+        self.fd = lib().rpcmem_to_fd(self.ptr)
+        if map_it:
+            rc = lib().fastrpc_mmap(3, self.fd, self.ptr, 0, self.nbytes, 2)
+            if rc != 0:
+                raise HtpOpsError(f"fastrpc_mmap failed ({rc})")
+
+    def write(self, arr, offset=0):
+        raw = np.ascontiguousarray(arr).view(np.uint8).ravel()
+        rc = lib().htp_ops_amd_buffer_write(self.fd, offset, raw.ctypes.data, raw.nbytes)
+        if rc != 0:
+            raise HtpOpsError(f"htp_ops_amd_buffer_write failed ({rc})")
+
+    def read(self, dtype, count, offset=0):
+        out = np.empty(count, np.dtype(dtype))
+        rc = lib().htp_ops_amd_buffer_read(self.fd, offset, out.ctypes.data, out.nbytes)
+        if rc != 0:
+            raise HtpOpsError(f"htp_ops_amd_buffer_read failed ({rc})")
+        return out
+
+    def host_view(self):
+        """uint8 numpy view of host memory (host buffers only)."""
+        assert not self.device
+        return np.ctypeslib.as_array((ctypes.c_uint8 * self.nbytes).from_address(self.ptr))
+
+    def free(self):
+        if self.ptr:
+            lib().rpcmem_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass

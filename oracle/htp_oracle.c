@@ -122,6 +122,14 @@ uint16_t oracle_f32_to_f16(float x) {
   return (uint16_t)(sign | (e << 10) | (q & 0x3ffu));
 }
 
+void oracle_f32_to_f16_array(uint16_t *dst, const float *src, size_t count) {
+  for (size_t i = 0; i < count; ++i) dst[i] = oracle_f32_to_f16(src[i]);
+}
+
+void oracle_f16_to_f32_array(float *dst, const uint16_t *src, size_t count) {
+  for (size_t i = 0; i < count; ++i) dst[i] = oracle_f16_to_f32(src[i]);
+}
+
 float oracle_f16_to_f32(uint16_t h) {
   const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
   const uint32_t e = (h >> 10) & 0x1fu;
@@ -233,6 +241,10 @@ uint8_t oracle_w8a8_quantize_value(float v) {
   const int32_t whole = mant >> shift;
   const int32_t half = 1 << (shift - 1);
   return (uint8_t)((mant + (half - 1) + (whole & 1)) >> shift);
+}
+
+void oracle_w8a8_quantize_values(uint8_t *dst, const float *v, size_t count) {
+  for (size_t i = 0; i < count; ++i) dst[i] = oracle_w8a8_quantize_value(v[i]);
 }
 
 typedef struct {

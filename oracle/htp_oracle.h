@@ -25,6 +25,8 @@ extern "C" {
 /* ---- binary16 ------------------------------------------------------------ */
 uint16_t oracle_f32_to_f16(float x);
 float oracle_f16_to_f32(uint16_t h);
+void oracle_f32_to_f16_array(uint16_t *dst, const float *src, size_t count);
+void oracle_f16_to_f32_array(float *dst, const uint16_t *src, size_t count);
 
 /* ---- W8A8 constants blob ---------------------------------------------------- */
 size_t oracle_w8a8_blob_bytes(int k, int n);
@@ -37,6 +39,7 @@ int oracle_w8a8_check_header(const uint8_t *blob, int k, int n);
 
 /* ---- W8A8 arithmetic -------------------------------------------------------- */
 uint8_t oracle_w8a8_quantize_value(float v);
+void oracle_w8a8_quantize_values(uint8_t *dst, const float *v, size_t count);
 void oracle_w8a8_quantize(uint8_t *u, float *s, const float *x, const float *inv, int m, int k, int nthreads);
 void oracle_w8a8_accumulate(int32_t *acc, const uint8_t *u, const uint8_t *blob, int m, int k, int n,
                             int nthreads);

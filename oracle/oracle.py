@@ -19,6 +19,9 @@ _S = ctypes.c_size_t
 _SIGS = {
     "oracle_f32_to_f16": (ctypes.c_uint16, [ctypes.c_float]),
     "oracle_f16_to_f32": (ctypes.c_float, [ctypes.c_uint16]),
+    "oracle_f32_to_f16_array": (None, [_P, _P, _S]),
+    "oracle_f16_to_f32_array": (None, [_P, _P, _S]),
+    "oracle_w8a8_quantize_values": (None, [_P, _P, _S]),
     "oracle_w8a8_blob_bytes": (_S, [_I, _I]),
     "oracle_w8a8_weight_offset": (_S, [_I, _I, _I]),
     "oracle_w8a8_pack_blob": (None, [_P, _P, _P, _P, _P, _I, _I, ctypes.c_uint64]),
@@ -103,14 +106,23 @@ def int8_uniform(count, lo=-127, hi=127, seed=0):
 
 def f32_to_f16_bits(x):
     x = np.ascontiguousarray(x, np.float32).ravel()
-    f = lib().oracle_f32_to_f16
-    return np.array([f(float(v)) for v in x], np.uint16)
+    out = np.empty(x.size, np.uint16)
+    lib().oracle_f32_to_f16_array(_ptr(out), _ptr(x), x.size)
+    return out
 
 
 def f16_bits_to_f32(h):
     h = np.ascontiguousarray(h, np.uint16).ravel()
-    f = lib().oracle_f16_to_f32
-    return np.array([f(int(v)) for v in h], np.float32)
+    out = np.empty(h.size, np.float32)
+    lib().oracle_f16_to_f32_array(_ptr(out), _ptr(h), h.size)
+    return out
+
+
+def quantize_values(v):
+    v = np.ascontiguousarray(v, np.float32).ravel()
+    out = np.empty(v.size, np.uint8)
+    lib().oracle_w8a8_quantize_values(_ptr(out), _ptr(v), v.size)
+    return out
 
 
 # ---- W8A8 --------------------------------------------------------------------
