@@ -17,6 +17,7 @@ static inline int hb_check_launch(const char *what) {
 }
 
 typedef int hb_i32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int hb_u32x4 __attribute__((ext_vector_type(4)));
 typedef float hb_f32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 hb_f16x8 __attribute__((ext_vector_type(8)));
 

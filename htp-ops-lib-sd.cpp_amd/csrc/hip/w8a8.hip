@@ -113,17 +113,23 @@ __global__ __launch_bounds__(256) void w8a8_quant_rows_reg(int8_t *__restrict__ 
   const float4 *xr = (const float4 *)(x + (size_t)row * k);
   const float4 *iv = (const float4 *)inv;
   const int nvec = k / 4;
+  // Loads are unconditional (index clamped into the row) so all 2*NV of them
+  // issue back to back; lanes past the row end contribute nothing.
+  float4 a[NV], b[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int idx = min(lane + 64 * j, nvec - 1);
+    a[j] = xr[idx];
+    b[j] = iv[idx];
+  }
   float4 t[NV];
   float amax = 0.0f;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
-    const int idx = lane + 64 * j;
-    if (idx < nvec) {
-      const float4 a = xr[idx];
-      const float4 b = iv[idx];
-      t[j] = make_float4(__fmul_rn(a.x, b.x), __fmul_rn(a.y, b.y), __fmul_rn(a.z, b.z), __fmul_rn(a.w, b.w));
+    t[j] = make_float4(__fmul_rn(a[j].x, b[j].x), __fmul_rn(a[j].y, b[j].y), __fmul_rn(a[j].z, b[j].z),
+                       __fmul_rn(a[j].w, b[j].w));
+    if (lane + 64 * j < nvec)
       amax = fmaxf(amax, fmaxf(fmaxf(fabsf(t[j].x), fabsf(t[j].y)), fmaxf(fabsf(t[j].z), fabsf(t[j].w))));
-    }
   }
   amax = wave_max(amax);
   const float s = fmaxf(__fdiv_rn(amax, 127.0f), 1e-12f);
@@ -179,27 +185,89 @@ __device__ inline float gelu_tanh(float z) {
   return __fmul_rn(z, sig);
 }
 
+// Bits of one output element: int32 raw accumulator, or the scaled f32.
+template <int EPI>
+__device__ inline uint32_t epilogue_bits(int32_t acc, int32_t corr, float sw, float s) {
+  const int32_t c = (int32_t)((uint32_t)acc + (uint32_t)corr);
+  if (EPI == HB_W8A8_EPI_RAW) return (uint32_t)c;
+  float v = __fmul_rn(__fmul_rn((float)c, sw), s);
+  if (EPI == HB_W8A8_EPI_SCALE_GELU) v = gelu_tanh(v);
+  return __float_as_uint(v);
+}
+
 template <int EPI>
 __device__ inline void store_result(void *y, int ldy, int row, int col, int32_t acc, int32_t corr, float sw,
                                     float s) {
   const size_t idx = (size_t)row * (size_t)ldy + (size_t)col;
-  if (EPI == HB_W8A8_EPI_RAW) {
-    __builtin_nontemporal_store((int32_t)((uint32_t)acc + (uint32_t)corr), (int32_t *)y + idx);
-  } else {
-    const int32_t c = (int32_t)((uint32_t)acc + (uint32_t)corr);
-    float v = __fmul_rn(__fmul_rn((float)c, sw), s);
-    if (EPI == HB_W8A8_EPI_SCALE_GELU) v = gelu_tanh(v);
-    __builtin_nontemporal_store(v, (float *)y + idx);
-  }
+  __builtin_nontemporal_store(epilogue_bits<EPI>(acc, corr, sw, s), (uint32_t *)y + idx);
 }
 
 // ---------------------------------------------------------------------------
-// Tiled GEMM: BM x BN output tile per workgroup of WM x WN waves, k-step 64,
-// operands staged through double-buffered LDS in MFMA lane order.
+// Tiled GEMM: BM x BN output tile per workgroup of WM x WN waves, 64-k stages.
+// Operands move global -> LDS by direct DMA (global_load_lds_dwordx4): one
+// wave instruction fills one 1 KB, MFMA-lane-ordered 16 x 64 block (lane l's
+// 16 bytes land at l*16), so the MFMA loop reads LDS conflict-free with
+// ds_read_b128 at lane*16.  S stages form a ring: stage kt+S-1 is in flight
+// while stage kt is multiplied; each wave waits only for its own DMA of stage
+// kt (vmcnt), then one barrier publishes the stage to all waves.
 // A = q int8 [mp][kp] row-major; B = packed tiles (see hb.h).
 // ---------------------------------------------------------------------------
 
-template <int BM, int BN, int WM, int WN, int EPI>
+#define HB_LDS_PTR(p) ((__attribute__((address_space(3))) void *)(p))
+
+template <int N>
+__device__ inline void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+__device__ inline void block_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Waits until at most `ahead` later stages (PW DMA instructions each) are
+// still in flight for this wave; ahead <= A.
+template <int PW, int A>
+__device__ inline void wait_stage(int ahead) {
+  if constexpr (A == 0) {
+    wait_vmcnt<0>();
+  } else {
+    if (ahead >= A) {
+      wait_vmcnt<A * PW>();
+    } else {
+      wait_stage<PW, A - 1>(ahead);
+    }
+  }
+}
+
+// Workgroups are dispatched round-robin over the 8 XCDs: tile ids are first
+// made contiguous per XCD, then walked in groups of 4 row-blocks so that
+// workgroups resident together on one XCD share A and B blocks in its L2.
+__device__ inline void tile_coords(int bid, int tiles_m, int tiles_n, int &tm, int &tn) {
+  const int total = tiles_m * tiles_n;
+  const int pid = (total % 8 == 0) ? (bid % 8) * (total / 8) + bid / 8 : bid;
+  constexpr int G = 4;
+  const int first_m = (pid / (G * tiles_n)) * G;
+  const int gsize = min(tiles_m - first_m, G);
+  const int in_group = pid % (G * tiles_n);
+  tm = first_m + in_group % gsize;
+  tn = in_group / gsize;
+}
+
+// Issues one stage's DMA: instruction i of this wave fills block i*NW + wave.
+template <int PW, int NW>
+__device__ inline void dma_stage(int8_t *stage, const int8_t *const *src, const int *stride, int kt,
+                                 int wave, int lane) {
+  (void)lane;
+#pragma unroll
+  for (int i = 0; i < PW; ++i)
+    __builtin_amdgcn_global_load_lds(src[i] + (size_t)kt * stride[i],
+                                     HB_LDS_PTR(stage + (i * NW + wave) * kFragBytes), 16, 0, 0);
+}
+
+template <int BM, int BN, int WM, int WN, int S, int EPI>
 __global__ __launch_bounds__(64 * WM *WN) void w8a8_gemm_tiles(void *__restrict__ y, int ldy,
                                                                const int8_t *__restrict__ q,
                                                                const float *__restrict__ scales,
@@ -207,57 +275,40 @@ __global__ __launch_bounds__(64 * WM *WN) void w8a8_gemm_tiles(void *__restrict_
                                                                const float *__restrict__ sw,
                                                                const int32_t *__restrict__ corr, int m, int n,
                                                                int kp) {
-  constexpr int NT = 64 * WM * WN;
+  constexpr int NW = WM * WN;
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int FM = WTM / 16, FN = WTN / 16;
-  constexpr int A_BYTES = BM * kKStep, B_BYTES = BN * kKStep;
-  constexpr int A_CH = A_BYTES / 16 / NT, B_CH = B_BYTES / 16 / NT;
-  static_assert(A_CH * 16 * NT == A_BYTES && B_CH * 16 * NT == B_BYTES, "tile/thread mismatch");
-  __shared__ __attribute__((aligned(16))) int8_t lds[2][A_BYTES + B_BYTES];
+  constexpr int ABLK = BM / 16, BBLK = BN / 16;
+  constexpr int PW = (ABLK + BBLK) / NW;  // DMA instructions per wave per stage
+  static_assert(PW * NW == ABLK + BBLK, "blocks must split evenly over waves");
+  constexpr int STAGE = (ABLK + BBLK) * kFragBytes;
+  __shared__ __attribute__((aligned(1024))) int8_t lds[S * STAGE];
 
-  const int tiles_n = (n + BN - 1) / BN;
-  const int tm = blockIdx.x / tiles_n, tn = blockIdx.x % tiles_n;
+  const int tiles_m = (m + BM - 1) / BM, tiles_n = (n + BN - 1) / BN;
+  int tm, tn;
+  tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   const int kt_count = kp / kKStep;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int wm = wave / WN, wn = wave % WN;
 
-  // Global sources and LDS destinations of this thread's 16-byte chunks.
-  const int8_t *a_src[A_CH];
-  int a_dst[A_CH];
-#pragma unroll
-  for (int i = 0; i < A_CH; ++i) {
-    const int c = tid + NT * i;
-    const int row = c >> 2, kc = c & 3;
-    const int grow = min(m0 + row, m - 1);
-    a_src[i] = q + (size_t)grow * kp + kc * 16;
-    a_dst[i] = (row >> 4) * kFragBytes + ((row & 15) + 16 * kc) * 16;
-  }
-  const int8_t *b_src[B_CH];
-  int b_dst[B_CH];
+  // DMA instruction i of this wave fills stage block b = i*NW + wave.
+  const int8_t *src[PW];
+  int stride[PW];
   const int nblocks = n / 16;
 #pragma unroll
-  for (int i = 0; i < B_CH; ++i) {
-    const int c = tid + NT * i;
-    const int blk = c >> 6, slot = c & 63;
-    const int gnb = min(n0 / 16 + blk, nblocks - 1);
-    b_src[i] = wpack + (size_t)gnb * kt_count * kFragBytes + slot * 16;
-    b_dst[i] = A_BYTES + blk * kFragBytes + slot * 16;
+  for (int i = 0; i < PW; ++i) {
+    const int b = i * NW + wave;
+    if (b < ABLK) {
+      const int row = min(m0 + b * 16 + (lane & 15), m - 1);
+      src[i] = q + (size_t)row * kp + (lane >> 4) * 16;
+      stride[i] = kKStep;
+    } else {
+      const int nb = min(n0 / 16 + (b - ABLK), nblocks - 1);
+      src[i] = wpack + (size_t)nb * kt_count * kFragBytes + lane * 16;
+      stride[i] = kFragBytes;
+    }
   }
-
-  uint4 ra[A_CH], rb[B_CH];
-  auto load = [&](int kt) {
-#pragma unroll
-    for (int i = 0; i < A_CH; ++i) ra[i] = *(const uint4 *)(a_src[i] + (size_t)kt * kKStep);
-#pragma unroll
-    for (int i = 0; i < B_CH; ++i) rb[i] = *(const uint4 *)(b_src[i] + (size_t)kt * kFragBytes);
-  };
-  auto stash = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < A_CH; ++i) *(uint4 *)(&lds[buf][a_dst[i]]) = ra[i];
-#pragma unroll
-    for (int i = 0; i < B_CH; ++i) *(uint4 *)(&lds[buf][b_dst[i]]) = rb[i];
-  };
 
   hb_i32x4 acc[FM][FN];
 #pragma unroll
@@ -265,14 +316,17 @@ __global__ __launch_bounds__(64 * WM *WN) void w8a8_gemm_tiles(void *__restrict_
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = hb_i32x4{0, 0, 0, 0};
 
-  load(0);
-  stash(0);
-  __syncthreads();
+#pragma unroll
+  for (int s = 0; s < S - 1; ++s)
+    if (s < kt_count) dma_stage<PW, NW>(lds + (s % S) * STAGE, src, stride, s, wave, lane);
   for (int kt = 0; kt < kt_count; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < kt_count) load(kt + 1);
-    const int8_t *la = &lds[cur][(wm * FM) * kFragBytes + lane * 16];
-    const int8_t *lb = &lds[cur][A_BYTES + (wn * FN) * kFragBytes + lane * 16];
+    wait_stage<PW, S - 2>(kt_count - 1 - kt);
+    block_barrier();
+    if (kt + S - 1 < kt_count)
+      dma_stage<PW, NW>(lds + ((kt + S - 1) % S) * STAGE, src, stride, kt + S - 1, wave, lane);
+    const int8_t *base = lds + (kt % S) * STAGE;
+    const int8_t *la = base + (wm * FM) * kFragBytes + lane * 16;
+    const int8_t *lb = base + (ABLK + wn * FN) * kFragBytes + lane * 16;
     hb_i32x4 bf[FN];
 #pragma unroll
     for (int j = 0; j < FN; ++j) bf[j] = *(const hb_i32x4 *)(lb + j * kFragBytes);
@@ -282,23 +336,46 @@ __global__ __launch_bounds__(64 * WM *WN) void w8a8_gemm_tiles(void *__restrict_
 #pragma unroll
       for (int j = 0; j < FN; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf[j], acc[i][j], 0, 0, 0);
     }
-    if (kt + 1 < kt_count) stash(cur ^ 1);
-    __syncthreads();
   }
 
-  // Epilogue in registers: lane holds rows 4*(lane/16)+r, column lane%16 of each 16x16 block.
+  // Epilogue.  The lane holds rows 4*(lane/16)+r, column lane%16 of each
+  // 16x16 accumulator block.  Each 16-row chunk of the wave tile is finished
+  // in registers, staged in a wave-private padded LDS area, and written back
+  // as 16-byte vectors running along the output rows.
+  block_barrier();  // every wave is done with the operand stages: LDS becomes staging
+  constexpr int SROW = WTN + 4;  // padded staging row (32-bit words): row groups hit different banks
+  static_assert(16 * SROW * 4 * NW <= S * STAGE, "staging must fit in the operand LDS");
+  uint32_t *stg = (uint32_t *)lds + wave * 16 * SROW;
+  int32_t cc[FN];
+  float sc[FN];
 #pragma unroll
   for (int j = 0; j < FN; ++j) {
-    const int col = n0 + wn * WTN + j * 16 + (lane & 15);
-    if (col >= n) continue;
-    const int32_t cc = corr[col];
-    const float sc = sw[col];
+    const int col = min(n0 + wn * WTN + j * 16 + (lane & 15), n - 1);
+    cc[j] = corr[col];
+    sc[j] = sw[col];
+  }
+  const int row0 = m0 + wm * WTM;
+  const int col0 = n0 + wn * WTN;
+  constexpr int VPR = WTN / 4;  // 16-byte vectors per staged row
 #pragma unroll
-    for (int i = 0; i < FM; ++i) {
+  for (int i = 0; i < FM; ++i) {
+    float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (EPI != HB_W8A8_EPI_RAW) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = m0 + wm * WTM + i * 16 + (lane >> 4) * 4 + r;
-        if (row < m) store_result<EPI>(y, ldy, row, col, acc[i][j][r], cc, sc, EPI == HB_W8A8_EPI_RAW ? 0.0f : scales[row]);
+      for (int r = 0; r < 4; ++r) s[r] = scales[min(row0 + i * 16 + (lane >> 4) * 4 + r, m - 1)];
+    }
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        stg[((lane >> 4) * 4 + r) * SROW + j * 16 + (lane & 15)] = epilogue_bits<EPI>(acc[i][j][r], cc[j], sc[j], s[r]);
+#pragma unroll
+    for (int v = lane; v < 16 * VPR; v += 64) {
+      const int r = v / VPR, c4 = v % VPR;
+      const int row = row0 + i * 16 + r, col = col0 + c4 * 4;
+      if (row < m && col < n) {
+        const hb_u32x4 val = *(const hb_u32x4 *)(stg + r * SROW + c4 * 4);
+        __builtin_nontemporal_store(val, (hb_u32x4 *)((uint32_t *)y + (size_t)row * ldy + col));
       }
     }
   }
@@ -390,27 +467,55 @@ __global__ __launch_bounds__(256) void w8a8_planes(uint8_t *__restrict__ out, co
 // Host-side dispatch.
 // ---------------------------------------------------------------------------
 
+// Candidate tile shapes; occ = workgroups resident per CU (LDS bound).
 struct TileShape {
-  int bm, bn;
+  int bm, bn, occ;
 };
+constexpr TileShape kTileShapes[] = {{256, 256, 1}, {256, 192, 1}, {128, 128, 2}, {64, 64, 4}};
+constexpr int kCUs = 256;
+
+// Picks the shape minimising (rounds of resident workgroups) x (work per
+// round per CU); ties go to the larger tile (less operand traffic).
+int pick_tile_shape(int m, int n) {
+  int best = 0;
+  long long best_cost = -1;
+  for (int i = 0; i < 4; ++i) {
+    const TileShape t = kTileShapes[i];
+    if (t.bn == 192 && n % 192 != 0) continue;
+    const long long tiles = (long long)((m + t.bm - 1) / t.bm) * ((n + t.bn - 1) / t.bn);
+    const long long slots = (long long)kCUs * t.occ;
+    const long long cost = (tiles + slots - 1) / slots * t.bm * t.bn * t.occ;
+    if (best_cost < 0 || cost < best_cost) {
+      best_cost = cost;
+      best = i;
+    }
+  }
+  return best;
+}
 
 template <int EPI>
 int launch_tiles(void *y, int ldy, const int8_t *q, const float *scales, const int8_t *wpack, const float *sw,
                  const int32_t *corr, int m, int n, int kp, hipStream_t st) {
-  const long long big_tiles = ((m + 255) / 256) * (long long)((n + 255) / 256);
-  const long long mid_tiles = ((m + 127) / 128) * (long long)((n + 127) / 128);
-  if (big_tiles >= 256) {
-    const int grid = (int)big_tiles;
-    hipLaunchKernelGGL((w8a8_gemm_tiles<256, 256, 2, 4, EPI>), dim3(grid), dim3(512), 0, st, y, ldy, q, scales,
-                       wpack, sw, corr, m, n, kp);
-  } else if (mid_tiles >= 256) {
-    const int grid = (int)mid_tiles;
-    hipLaunchKernelGGL((w8a8_gemm_tiles<128, 128, 2, 2, EPI>), dim3(grid), dim3(256), 0, st, y, ldy, q, scales,
-                       wpack, sw, corr, m, n, kp);
-  } else {
-    const int grid = ((m + 63) / 64) * ((n + 63) / 64);
-    hipLaunchKernelGGL((w8a8_gemm_tiles<64, 64, 2, 2, EPI>), dim3(grid), dim3(256), 0, st, y, ldy, q, scales, wpack,
-                       sw, corr, m, n, kp);
+  const int shape = pick_tile_shape(m, n);
+  const TileShape t = kTileShapes[shape];
+  const int grid = ((m + t.bm - 1) / t.bm) * ((n + t.bn - 1) / t.bn);
+  switch (shape) {
+    case 0:
+      hipLaunchKernelGGL((w8a8_gemm_tiles<256, 256, 2, 2, 4, EPI>), dim3(grid), dim3(256), 0, st, y, ldy, q, scales,
+                         wpack, sw, corr, m, n, kp);
+      break;
+    case 1:
+      hipLaunchKernelGGL((w8a8_gemm_tiles<256, 192, 2, 2, 4, EPI>), dim3(grid), dim3(256), 0, st, y, ldy, q, scales,
+                         wpack, sw, corr, m, n, kp);
+      break;
+    case 2:
+      hipLaunchKernelGGL((w8a8_gemm_tiles<128, 128, 2, 2, 4, EPI>), dim3(grid), dim3(256), 0, st, y, ldy, q, scales,
+                         wpack, sw, corr, m, n, kp);
+      break;
+    default:
+      hipLaunchKernelGGL((w8a8_gemm_tiles<64, 64, 2, 2, 4, EPI>), dim3(grid), dim3(256), 0, st, y, ldy, q, scales,
+                         wpack, sw, corr, m, n, kp);
+      break;
   }
   return hb_check_launch("w8a8_gemm_tiles");
 }
@@ -418,12 +523,14 @@ int launch_tiles(void *y, int ldy, const int8_t *q, const float *scales, const i
 template <int EPI>
 int launch_decode(void *y, int ldy, const int8_t *q, const float *scales, const int8_t *wpack, const float *sw,
                   const int32_t *corr, int m, int n, int kp, hipStream_t st) {
+  // Size the workgroup so every wave is resident in a single round
+  // (about 16 waves per CU) with 8 one-kilobyte loads in flight each.
   const int nblocks = n / 16;
-  if (nblocks >= 2048) {
+  if (nblocks >= 512) {
     hipLaunchKernelGGL((w8a8_gemm_decode<4, 8, EPI>), dim3(nblocks), dim3(256), 0, st, y, ldy, q, scales, wpack, sw,
                        corr, m, n, kp);
-  } else if (nblocks >= 512) {
-    hipLaunchKernelGGL((w8a8_gemm_decode<8, 8, EPI>), dim3(nblocks), dim3(512), 0, st, y, ldy, q, scales, wpack,
+  } else if (nblocks >= 128) {
+    hipLaunchKernelGGL((w8a8_gemm_decode<16, 8, EPI>), dim3(nblocks), dim3(1024), 0, st, y, ldy, q, scales, wpack,
                        sw, corr, m, n, kp);
   } else {
     hipLaunchKernelGGL((w8a8_gemm_decode<16, 4, EPI>), dim3(nblocks), dim3(1024), 0, st, y, ldy, q, scales, wpack,
@@ -521,8 +628,9 @@ int hb_w8a8_gemm(void *d_y, int ldy, const int8_t *d_q, const float *d_scales, c
                  int n, int epilogue, hb_stream s) {
   if (!d_y || !d_q || !d_packed || (epilogue != HB_W8A8_EPI_RAW && !d_scales))
     return hb_invalid("hb_w8a8_gemm null pointer");
-  if (m < 1 || k < 32 || k % 32 || n < 16 || n % 16 || ldy < n) return hb_invalid("hb_w8a8_gemm shape");
-  if (!aligned(d_y, 4) || !aligned(d_q, 16) || !aligned(d_packed, 256)) return hb_invalid("hb_w8a8_gemm alignment");
+  if (m < 1 || k < 32 || k % 32 || n < 16 || n % 16 || ldy < n || ldy % 4) return hb_invalid("hb_w8a8_gemm shape");
+  // Output rows are written as 16-byte vectors.
+  if (!aligned(d_y, 16) || !aligned(d_q, 16) || !aligned(d_packed, 256)) return hb_invalid("hb_w8a8_gemm alignment");
   hipStream_t st = hb_resolve_stream(s);
   const int kp = (int)kp_of(k);
   const uint8_t *base = (const uint8_t *)d_packed;

@@ -214,7 +214,8 @@ static int exec_w8a8(uint8_t *payload, size_t payload_size) {
   const size_t q_bytes = ((size_t)(m + 15) / 16 * 16) * ((size_t)(k + 63) / 64 * 64);
   float *scales = (float *)(ws + (q_bytes + 255u) / 256u * 256u); /* layout of hb_w8a8_workspace_bytes */
   const float *inv = (const float *)((const uint8_t *)packed + hb_w8a8_packed_offset(k, n, HB_W8A8_INV));
-  float *y = ((uintptr_t)out.dev % 4u) == 0 ? (float *)out.dev : (float *)htp_executor_scratch(3, out.bytes);
+  /* The GEMM writes 16-byte vectors: a misaligned output is produced in scratch and copied. */
+  float *y = ((uintptr_t)out.dev % 16u) == 0 ? (float *)out.dev : (float *)htp_executor_scratch(3, out.bytes);
   void *raw = cpu_output ? htp_executor_scratch(1, (size_t)m * n * 4u) : NULL;
   if (!y || (cpu_output && !raw)) return -5;
 

@@ -100,7 +100,8 @@ enum {
 };
 
 /* INT8 GEMM on quantized activations + fused epilogue; picks the decode
- * (m <= 16) or tiled kernel.  d_y has row stride ldy (elements, >= n). */
+ * (m <= 16) or tiled kernel.  d_y is 16-byte aligned with row stride ldy
+ * (elements, >= n, a multiple of 4). */
 int hb_w8a8_gemm(void *d_y, int ldy, const int8_t *d_q, const float *d_scales, const void *d_packed, int m, int k,
                  int n, int epilogue, hb_stream s);
 

@@ -1,0 +1,228 @@
+"""Opcodes 15 / 16 / 1 through the drop-in boundary on the GPU, against the oracle.
+
+Requests go through execute_op_simple, the mailbox channel thread and the
+direct W16 entry points, with host (rpcmem) and HBM-resident tensors.
+W8A8 outputs are compared bit-exactly; F16 within 2e-3 of the fp16-rounded
+magnitude (see tests/test_gpu_kernels.py for the bound's derivation).
+"""
+import ctypes
+import struct
+import time
+
+import numpy as np
+import pytest
+
+import htp_ops as h
+from tolerances import assert_f16_close, f16_abs_dot
+
+pytestmark = pytest.mark.gpu
+
+
+def f16_weight(orc, k, n, seed):
+    w = orc.normal(k * n, 0, 0.02, seed).reshape(k, n).astype(np.float16)
+    return w, h.permute_f16(w.view(np.uint16))
+
+
+def w8a8_inputs(orc, m, k, n, seed, inv=False, sums=False):
+    x = orc.normal(m * k, 0.0, 1.0, seed).reshape(m, k)
+    w = orc.int8_uniform(n * k, -127, 127, seed + 1).reshape(n, k)
+    sw = orc.uniform(n, 1e-4, 1e-3, seed + 2)
+    invv = orc.uniform(k, 0.5, 2.0, seed + 3) if inv else None
+    sumv = np.random.default_rng(seed).integers(-2**20, 2**20, n).astype(np.int32) if sums else None
+    return x, h.pack_constants(w, sw, sums=sumv, inv=invv, signature=seed)
+
+
+def rpc(nbytes, device):
+    return h.RpcBuffer(nbytes, device=device)
+
+
+@pytest.mark.parametrize("device", [False, True])
+@pytest.mark.parametrize("m,k,n", [(77, 768, 3072), (1, 4096, 1024), (300, 96, 512)])
+def test_opcode15_bit_exact(hip, orc, device, m, k, n):
+    x, blob = w8a8_inputs(orc, m, k, n, seed=m + n, inv=True, sums=True)
+    out, act, cst = rpc(m * n * 4 + 256, device), rpc(m * k * 4 + 512, device), rpc(blob.nbytes + 1024, device)
+    act.write(x, 512)
+    cst.write(blob, 1024)
+    rc, payload = h.execute(15, h.w8a8_params((out.fd, 256), (act.fd, 512), (cst.fd, 1024), m, k, n))
+    assert rc == 0, h.last_error()
+    y = out.read(np.float32, m * n, 256).reshape(m, n)
+    ref = orc.linear(x, blob, k, n)
+    assert np.array_equal(y.view(np.uint32), ref.view(np.uint32))
+    elapsed = struct.unpack_from("<i", payload, 36)[0]
+    assert elapsed >= 0
+
+
+def test_opcode15_profile_modes(hip, orc):
+    m, k, n = 64, 256, 512
+    x, blob = w8a8_inputs(orc, m, k, n, seed=3)
+    out, act, cst = rpc(m * n * 4, False), rpc(m * k * 4, False), rpc(blob.nbytes, False)
+    act.write(x)
+    cst.write(blob)
+    ref = orc.linear(x, blob, k, n)
+    for mode in (1, 2, 3):
+        payload = h.w8a8_params((out.fd, 0), (act.fd, 0), (cst.fd, 0), m, k, n) + h.w8a8_profile(mode)
+        rc, after = h.execute(15, payload)
+        assert rc == 0
+        prof = h.unpack_w8a8_profile(after[40:])
+        assert prof["mode"] == mode
+        assert prof["hmx_ticks"] > 0 and prof["activation_ticks"] > 0
+        if mode == 2:
+            assert prof["mac_ticks"] == prof["hmx_ticks"]
+        assert np.array_equal(out.read(np.float32, m * n).reshape(m, n), ref)
+
+
+def test_opcode15_cpu_control_variant(hip, orc):
+    """Raw accumulator planes over the output + row scales + one batch."""
+    m, k, n = 77, 128, 128
+    x, blob = w8a8_inputs(orc, m, k, n, seed=9)
+    out, act, cst, ctl = (rpc(m * n * 4, False), rpc(m * k * 4, False), rpc(blob.nbytes, False),
+                          rpc(17536, False))
+    act.write(x)
+    cst.write(blob)
+    ctl.write(np.zeros(17536, np.uint8))
+    payload = h.w8a8_params((out.fd, 0), (act.fd, 0), (cst.fd, 0), m, k, n) + struct.pack("<ii", ctl.fd, 0)
+    rc, _ = h.execute(15, payload)
+    assert rc == 0
+    inv = np.ones(k, np.float32)
+    u, s = orc.quantize(x, inv)
+    acc = orc.accumulate(u, blob, k, n)
+    assert np.array_equal(out.read(np.uint8, m * n * 4), orc.planes(acc))
+    c = ctl.read(np.uint8, 17536)
+    assert struct.unpack_from("<I", c, 0)[0] == 1                      # produced
+    assert np.array_equal(np.frombuffer(c[128:128 + 4 * m].tobytes(), np.float32), s)
+    assert struct.unpack_from("<4i", c, 16512) == (0, m, 0, n // 64)
+
+
+def test_opcode15_weight_cache_follows_rewrites(hip, orc):
+    m, k, n = 16, 256, 256
+    x, blob1 = w8a8_inputs(orc, m, k, n, seed=21)
+    _, blob2 = w8a8_inputs(orc, m, k, n, seed=22)
+    out, act, cst = rpc(m * n * 4, False), rpc(m * k * 4, False), rpc(blob1.nbytes, False)
+    act.write(x)
+    params = h.w8a8_params((out.fd, 0), (act.fd, 0), (cst.fd, 0), m, k, n)
+    for blob in (blob1, blob1, blob2, blob1):
+        cst.write(blob)
+        assert h.execute(15, params)[0] == 0
+        ref = orc.linear(x, blob, k, n)
+        assert np.array_equal(out.read(np.float32, m * n).reshape(m, n), ref)
+    assert h.lib().htp_ops_amd_invalidate_weights(cst.fd) >= 1
+
+
+@pytest.mark.parametrize("device", [False, True])
+@pytest.mark.parametrize("mode,channels", [(0, 768), (1, 768), (2, 768), (3, 700)])
+def test_opcode16_modes(hip, orc, device, mode, channels):
+    m, k, n = 77, 3072 if mode == 0 else 768, 768
+    x = orc.normal(m * k, 0, 1, mode).reshape(m, k)
+    w, perm = f16_weight(orc, k, n, 10 + mode)
+    bias = orc.normal(channels, 0, 0.02, 20 + mode)
+    out_elems = m * channels
+    out, act, wgt, b = (rpc(out_elems * 4, device), rpc(m * k * 4, device), rpc(perm.nbytes, device),
+                        rpc(channels * 4, device))
+    act.write(x)
+    wgt.write(perm)
+    b.write(bias)
+    rc, payload = h.execute(16, h.f16_epilogue_params((out.fd, 0), (act.fd, 0), (wgt.fd, 0), (b.fd, 0), m, k, n,
+                                                      channels, mode))
+    assert rc == 0, h.last_error()
+    got = out.read(np.float32, out_elems)
+    ref = orc.f16_gemm_epilogue(x, perm, bias, m, k, n, channels, mode)
+    v = orc.f16_gemm_epilogue(x, perm, None, m, k, n, n, 0)
+    absdot = f16_abs_dot(x, w)
+    if mode == 3:
+        got, v, bterm, absdot = got.reshape(channels, m), v.T[:channels], np.abs(bias)[:, None], absdot.T[:channels]
+    else:
+        got, bterm = got.reshape(m, n), np.abs(bias)[None, :]
+    assert_f16_close(got, ref, v, bterm, absdot, k)
+    assert struct.unpack_from("<i", payload, 52)[0] >= 0
+
+
+def test_opcode1_and_direct_rpc(hip, orc):
+    m, k, n = 32, 256, 512
+    x = orc.normal(m * k, 0, 1, 31).reshape(m, k)
+    w, perm = f16_weight(orc, k, n, 32)
+    out, act, wgt = rpc(m * n * 4, False), rpc(m * k * 4, False), rpc(perm.nbytes, False)
+    act.write(x)
+    wgt.write(perm)
+    ref = orc.f16_gemm_epilogue(x, perm, None, m, k, n, n, 0)
+    absdot = f16_abs_dot(x, w)
+    rc, payload = h.execute(1, h.matmul_params((out.fd, 0), (act.fd, 0), (wgt.fd, 0), m, k, n, with_elapsed=True))
+    assert rc == 0
+    assert_f16_close(out.read(np.float32, m * n).reshape(m, n), ref, ref, 0.0, absdot, k)
+    assert struct.unpack_from("<i", payload, 92)[0] >= 0
+    lib = h.lib()
+    handle = ctypes.c_uint64()
+    assert lib.htp_ops_open(b"", ctypes.byref(handle)) == 0
+    assert lib.htp_ops_mat_mul_permuted_w16a32(handle, out.fd, 0, act.fd, 0, wgt.fd, 0, m, k, n) == h.AEE_EBADSTATE
+    assert lib.htp_ops_init_backend(handle) == 0
+    out.write(np.zeros(m * n, np.float32))
+    assert lib.htp_ops_mat_mul_permuted_w16a32(handle, out.fd, 0, act.fd, 0, wgt.fd, 0, m, k, n) == 0
+    y = out.read(np.float32, m * n)
+    assert_f16_close(y.reshape(m, n), ref, ref, 0.0, absdot, k)
+    ah, oh, orh = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_uint64()
+    assert lib.htp_ops_mat_mul_permuted_w16a32_trace(handle, out.fd, 0, act.fd, 0, wgt.fd, 0, m, k, n,
+                                                     ctypes.byref(ah), ctypes.byref(oh), ctypes.byref(orh)) == 0
+    xb = np.ascontiguousarray(x)
+    assert ah.value == lib.htp_ops_fnv1a64(xb.ctypes.data, xb.nbytes)
+    assert oh.value == orh.value == lib.htp_ops_fnv1a64(y.ctypes.data, y.nbytes)
+    assert lib.htp_ops_close(handle) == 0
+
+
+def post(chan_view, requests, capacity, timeout=60.0):
+    msg, offs = h.build_message(requests, capacity)
+    chan_view[8:len(msg)] = np.frombuffer(bytes(msg[8:]), np.uint8)
+    chan_view[:8] = 0
+    chan_view[0] = 1
+    t0 = time.time()
+    while chan_view[1] != 1:
+        assert time.time() - t0 < timeout
+        time.sleep(0.0002)
+    return bytearray(chan_view[:capacity].tobytes()), offs
+
+
+def test_mailbox_chained_requests(hip, orc):
+    """A W8A8 request whose output feeds an F16 request in the same message,
+    then a map put and a repeat: requests run in order on one channel."""
+    lib = h.lib()
+    assert lib.open_dsp_session(3, 1) == 0
+    lib.init_htp_backend()
+    assert lib.htp_ops_session_is_initialized(lib.htp_ops_default_session()) == 1
+    chan = h.RpcBuffer(4096)
+    assert lib.create_htp_message_channel(chan.fd, 4096) == 0
+    m, k, n, n2 = 77, 768, 768, 256
+    x, blob = w8a8_inputs(orc, m, k, n, seed=41)
+    w2, perm = f16_weight(orc, n, n2, 42)
+    tensors = h.RpcBuffer(1 << 24)
+    off_x, off_blob, off_y, off_w, off_z = 0, 1 << 20, 3 << 20, 4 << 20, 5 << 20
+    tensors.write(x, off_x)
+    tensors.write(blob, off_blob)
+    tensors.write(perm, off_w)
+    fd = tensors.fd
+    r1 = h.compute_request(15, h.w8a8_params((fd, off_y), (fd, off_x), (fd, off_blob), m, k, n))
+    r2 = h.compute_request(16, h.f16_epilogue_params((fd, off_z), (fd, off_y), (fd, off_w), (-1, 0), m, n, n2, n2, 1))
+    put = struct.pack("<ii", 1, 0) + struct.pack("<i", fd)
+    view = chan.host_view()
+    for _ in range(2):
+        done, offs = post(view, [(h.REQUEST_TYPE_OP_COMPUTE, r1), (h.REQUEST_TYPE_OP_COMPUTE, r2),
+                                 (h.REQUEST_TYPE_RPCMEM_MAP, put)], 4096)
+        assert [h.request_state(done, offs, i) for i in range(3)] == [0, 0, 0]
+        y = tensors.read(np.float32, m * n, off_y).reshape(m, n)
+        ref_y = orc.linear(x, blob, k, n)
+        assert np.array_equal(y.view(np.uint32), ref_y.view(np.uint32))
+        z = tensors.read(np.float32, m * n2, off_z).reshape(m, n2)
+        ref_z = orc.f16_gemm_epilogue(ref_y, perm, None, m, n, n2, n2, 1)
+        v = orc.f16_gemm_epilogue(ref_y, perm, None, m, n, n2, n2, 0)
+        assert_f16_close(z, ref_z, v, 0.0, f16_abs_dot(ref_y, w2), n)
+    assert lib.destroy_htp_message_channel() == 0
+    lib.close_dsp_session()
+    chan.free()
+    tensors.free()
+
+
+def test_test_ops_on_gpu_backend(hip):
+    lib = h.lib()
+    handle = ctypes.c_uint64()
+    assert lib.htp_ops_open(b"", ctypes.byref(handle)) == 0
+    assert lib.htp_ops_init_backend(handle) == 0
+    scope = ctypes.c_int32()
+    assert lib.htp_ops_test_ops(handle, ctypes.byref(scope)) == 0 and scope.value == 1
+    assert lib.htp_ops_close(handle) == 0
