@@ -12,6 +12,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <cstdlib>
 
 #include "hb_internal.h"
 
@@ -102,6 +103,15 @@ __device__ inline uint32_t quantize_byte(float t, float r) {
   return (uint32_t)(u - 128) & 0xffu;
 }
 
+// Quantized activations use the weights' MFMA tile layout: 16 rows x 64 k
+// per 1 KB block, element (m,k) at ((m/16)*(kp/64) + k/64)*1024 +
+// ((m%16) + 16*((k%64)/16))*16 + k%16.  Returns the word holding k..k+3 (k%4 == 0).
+__device__ inline uint32_t *q_word(int8_t *q, int kp, int row, int k) {
+  const size_t off = ((size_t)(row / 16) * (size_t)(kp / kKStep) + (size_t)(k / kKStep)) * kFragBytes +
+                     (size_t)((row % 16) + 16 * ((k % kKStep) / 16)) * 16u + (size_t)(k % 16);
+  return (uint32_t *)(q + off);
+}
+
 // NV float4 vectors per lane stay in registers (row length k <= 256*NV).
 template <int NV>
 __global__ __launch_bounds__(256) void w8a8_quant_rows_reg(int8_t *__restrict__ q, float *__restrict__ scales,
@@ -135,16 +145,15 @@ __global__ __launch_bounds__(256) void w8a8_quant_rows_reg(int8_t *__restrict__ 
   const float s = fmaxf(__fdiv_rn(amax, 127.0f), 1e-12f);
   const float r = __fdiv_rn(1.0f, s);
   if (lane == 0) scales[row] = s;
-  uint32_t *qr = (uint32_t *)(q + (size_t)row * kp);
   const int qvec = kp / 4;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int idx = lane + 64 * j;
     if (idx < nvec) {
-      qr[idx] = quantize_byte(t[j].x, r) | (quantize_byte(t[j].y, r) << 8) | (quantize_byte(t[j].z, r) << 16) |
-                (quantize_byte(t[j].w, r) << 24);
+      *q_word(q, kp, row, 4 * idx) = quantize_byte(t[j].x, r) | (quantize_byte(t[j].y, r) << 8) |
+                                    (quantize_byte(t[j].z, r) << 16) | (quantize_byte(t[j].w, r) << 24);
     } else if (idx < qvec) {
-      qr[idx] = 0u;
+      *q_word(q, kp, row, 4 * idx) = 0u;
     }
   }
 }
@@ -164,8 +173,14 @@ __global__ __launch_bounds__(256) void w8a8_quant_rows_any(int8_t *__restrict__ 
   const float s = fmaxf(__fdiv_rn(amax, 127.0f), 1e-12f);
   const float r = __fdiv_rn(1.0f, s);
   if (lane == 0) scales[row] = s;
-  uint8_t *qr = (uint8_t *)(q + (size_t)row * kp);
-  for (int i = lane; i < kp; i += 64) qr[i] = i < k ? (uint8_t)quantize_byte(__fmul_rn(xr[i], inv[i]), r) : 0u;
+  for (int i = 4 * lane; i < kp; i += 256) {
+    uint32_t word = 0u;
+    if (i < k) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) word |= quantize_byte(__fmul_rn(xr[i + e], inv[i + e]), r) << (8 * e);
+    }
+    *q_word(q, kp, row, i) = word;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -300,9 +315,10 @@ __global__ __launch_bounds__(64 * WM *WN) void w8a8_gemm_tiles(void *__restrict_
   for (int i = 0; i < PW; ++i) {
     const int b = i * NW + wave;
     if (b < ABLK) {
-      const int row = min(m0 + b * 16 + (lane & 15), m - 1);
-      src[i] = q + (size_t)row * kp + (lane >> 4) * 16;
-      stride[i] = kKStep;
+      // A is tiled like B: block row mb is 1 KB per k-step, contiguous over k.
+      const int mb = min(m0 / 16 + b, (m + 15) / 16 - 1);
+      src[i] = q + (size_t)mb * kt_count * kFragBytes + lane * 16;
+      stride[i] = kFragBytes;
     } else {
       const int nb = min(n0 / 16 + (b - ABLK), nblocks - 1);
       src[i] = wpack + (size_t)nb * kt_count * kFragBytes + lane * 16;
@@ -342,33 +358,37 @@ __global__ __launch_bounds__(64 * WM *WN) void w8a8_gemm_tiles(void *__restrict_
   // 16x16 accumulator block.  Each 16-row chunk of the wave tile is finished
   // in registers, staged in a wave-private padded LDS area, and written back
   // as 16-byte vectors running along the output rows.
-  block_barrier();  // every wave is done with the operand stages: LDS becomes staging
-  constexpr int SROW = WTN + 4;  // padded staging row (32-bit words): row groups hit different banks
-  static_assert(16 * SROW * 4 * NW <= S * STAGE, "staging must fit in the operand LDS");
-  uint32_t *stg = (uint32_t *)lds + wave * 16 * SROW;
+  // All per-row and per-column parameters are requested together so the
+  // epilogue pays one global-load latency, not one per 16-row chunk.
+  const int row0 = m0 + wm * WTM;
+  const int col0 = n0 + wn * WTN;
   int32_t cc[FN];
   float sc[FN];
 #pragma unroll
   for (int j = 0; j < FN; ++j) {
-    const int col = min(n0 + wn * WTN + j * 16 + (lane & 15), n - 1);
+    const int col = min(col0 + j * 16 + (lane & 15), n - 1);
     cc[j] = corr[col];
     sc[j] = sw[col];
   }
-  const int row0 = m0 + wm * WTM;
-  const int col0 = n0 + wn * WTN;
+  float sv[FM][4];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      sv[i][r] = EPI == HB_W8A8_EPI_RAW ? 0.0f : scales[min(row0 + i * 16 + (lane >> 4) * 4 + r, m - 1)];
+  block_barrier();  // every wave is done with the operand stages: LDS becomes staging
+  constexpr int SROW = WTN + 4;  // padded staging row (32-bit words): row groups hit different banks
+  static_assert(16 * SROW * 4 * NW <= S * STAGE, "staging must fit in the operand LDS");
+  uint32_t *stg = (uint32_t *)lds + wave * 16 * SROW;
   constexpr int VPR = WTN / 4;  // 16-byte vectors per staged row
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
-    float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (EPI != HB_W8A8_EPI_RAW) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) s[r] = scales[min(row0 + i * 16 + (lane >> 4) * 4 + r, m - 1)];
-    }
 #pragma unroll
     for (int j = 0; j < FN; ++j)
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        stg[((lane >> 4) * 4 + r) * SROW + j * 16 + (lane & 15)] = epilogue_bits<EPI>(acc[i][j][r], cc[j], sc[j], s[r]);
+        stg[((lane >> 4) * 4 + r) * SROW + j * 16 + (lane & 15)] =
+            epilogue_bits<EPI>(acc[i][j][r], cc[j], sc[j], sv[i][r]);
 #pragma unroll
     for (int v = lane; v < 16 * VPR; v += 64) {
       const int r = v / VPR, c4 = v % VPR;
@@ -403,7 +423,16 @@ __global__ __launch_bounds__(64 * WAVES) void w8a8_gemm_decode(void *__restrict_
   const int8_t *wb = wpack + (size_t)nb * kt_count * kFragBytes + lane * 16;
   const int arow = lane & 15;
   const bool has_row = arow < m;
-  const int8_t *qa = q + (size_t)arow * kp + (lane >> 4) * 16;
+  const int8_t *qa = q + lane * 16;  // tiled A: block row 0, lane-ordered 1 KB per k-step
+  // Epilogue parameters are requested before the weight stream so their
+  // latency is hidden behind it.
+  const int col = nb * 16 + (lane & 15);
+  const int32_t cc = corr[col];
+  const float sc = sw[col];
+  float sv[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    sv[r] = EPI == HB_W8A8_EPI_RAW ? 0.0f : scales[min((lane >> 4) * 4 + r, m - 1)];
 
   hb_i32x4 acc = {0, 0, 0, 0};
   for (int kt0 = wave * U; kt0 < kt_count; kt0 += WAVES * U) {
@@ -413,7 +442,7 @@ __global__ __launch_bounds__(64 * WAVES) void w8a8_gemm_decode(void *__restrict_
       const int kt = kt0 + u;
       const bool ok = kt < kt_count;
       b[u] = ok ? *(const hb_i32x4 *)(wb + (size_t)kt * kFragBytes) : hb_i32x4{0, 0, 0, 0};
-      a[u] = (ok && has_row) ? *(const hb_i32x4 *)(qa + (size_t)kt * kKStep) : hb_i32x4{0, 0, 0, 0};
+      a[u] = (ok && has_row) ? *(const hb_i32x4 *)(qa + (size_t)kt * kFragBytes) : hb_i32x4{0, 0, 0, 0};
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[u], b[u], acc, 0, 0, 0);
@@ -428,13 +457,10 @@ __global__ __launch_bounds__(64 * WAVES) void w8a8_gemm_decode(void *__restrict_
     total = hb_i32x4{(int)((uint32_t)total[0] + (uint32_t)p[0]), (int)((uint32_t)total[1] + (uint32_t)p[1]),
                      (int)((uint32_t)total[2] + (uint32_t)p[2]), (int)((uint32_t)total[3] + (uint32_t)p[3])};
   }
-  const int col = nb * 16 + (lane & 15);
-  const int32_t cc = corr[col];
-  const float sc = sw[col];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int row = (lane >> 4) * 4 + r;
-    if (row < m) store_result<EPI>(y, ldy, row, col, total[r], cc, sc, EPI == HB_W8A8_EPI_RAW ? 0.0f : scales[row]);
+    if (row < m) store_result<EPI>(y, ldy, row, col, total[r], cc, sc, sv[r]);
   }
 }
 
@@ -467,19 +493,33 @@ __global__ __launch_bounds__(256) void w8a8_planes(uint8_t *__restrict__ out, co
 // Host-side dispatch.
 // ---------------------------------------------------------------------------
 
-// Candidate tile shapes; occ = workgroups resident per CU (LDS bound).
+// Candidate tile shapes; occ = workgroups resident per CU (LDS / register bound).
 struct TileShape {
   int bm, bn, occ;
 };
-constexpr TileShape kTileShapes[] = {{256, 256, 1}, {256, 192, 1}, {128, 128, 2}, {64, 64, 4}};
+constexpr TileShape kTileShapes[] = {{256, 256, 1}, {256, 192, 1}, {128, 192, 2}, {128, 128, 2}, {64, 64, 4}};
+constexpr int kNumShapes = 5;
 constexpr int kCUs = 256;
+
+// HTP_OPS_AMD_W8A8_TILE=<index into kTileShapes> pins the tile shape (tuning sweeps).
+int forced_tile_shape() {
+  static int forced = -2;
+  if (forced == -2) {
+    const char *v = getenv("HTP_OPS_AMD_W8A8_TILE");
+    forced = (v && *v) ? atoi(v) : -1;
+    if (forced >= kNumShapes) forced = -1;
+  }
+  return forced;
+}
 
 // Picks the shape minimising (rounds of resident workgroups) x (work per
 // round per CU); ties go to the larger tile (less operand traffic).
 int pick_tile_shape(int m, int n) {
+  const int forced = forced_tile_shape();
+  if (forced >= 0 && (kTileShapes[forced].bn != 192 || n % 192 == 0)) return forced;
   int best = 0;
   long long best_cost = -1;
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < kNumShapes; ++i) {
     const TileShape t = kTileShapes[i];
     if (t.bn == 192 && n % 192 != 0) continue;
     const long long tiles = (long long)((m + t.bm - 1) / t.bm) * ((n + t.bn - 1) / t.bn);
@@ -509,6 +549,10 @@ int launch_tiles(void *y, int ldy, const int8_t *q, const float *scales, const i
                          wpack, sw, corr, m, n, kp);
       break;
     case 2:
+      hipLaunchKernelGGL((w8a8_gemm_tiles<128, 192, 2, 2, 4, EPI>), dim3(grid), dim3(256), 0, st, y, ldy, q, scales,
+                         wpack, sw, corr, m, n, kp);
+      break;
+    case 3:
       hipLaunchKernelGGL((w8a8_gemm_tiles<128, 128, 2, 2, 4, EPI>), dim3(grid), dim3(256), 0, st, y, ldy, q, scales,
                          wpack, sw, corr, m, n, kp);
       break;

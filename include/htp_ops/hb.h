@@ -81,13 +81,16 @@ size_t hb_w8a8_packed_offset(int k, int n, int section);
 /* Blob (device copy of the constants buffer, header already validated) -> packed image. */
 int hb_w8a8_prepack(void *d_packed, const uint8_t *d_blob, int k, int n, hb_stream s);
 
-/* Workspace for quantized activations: int8 q[mp][kp] (mp = m rounded up to 16) then f32 scales[mp]. */
+/* Workspace for quantized activations: int8 q (mp*kp bytes, mp = m rounded up
+ * to 16) then f32 scales[mp]. */
 size_t hb_w8a8_workspace_bytes(int m, int k);
 
 /*
  * Per-token dynamic quantization (reference linear_w8a8.c:34-120):
  *   t = x*inv; s = max(max|t|/127, 1e-12); u = rint(clamp(t*(1/s)+128, 1, 255))
- * writes q = u - 128 (int8, row stride kp, zero for k >= k_real) and s (f32[m]).
+ * writes q = u - 128 and s (f32[m]).  q uses the weights' tile layout:
+ * element (m,k) at ((m/16)*(kp/64) + k/64)*1024 + ((m%16) + 16*((k%64)/16))*16 + k%16,
+ * zero for k >= k_real; rows m..mp-1 are left unwritten.
  */
 int hb_w8a8_quantize(int8_t *d_q, float *d_scales, const float *d_x, const float *d_inv, int m, int k,
                      hb_stream s);

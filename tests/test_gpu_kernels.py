@@ -46,7 +46,11 @@ def test_quantize_bit_exact(hip, orc, m, k, inv_kind):
     inv_ptr = packed.ptr + hip.w8a8_packed_offset(k, 64, hip.SECTION_INV)
     q, s = hip.w8a8_quantize(xd, inv_ptr, m, k)
     kp = hip.kp_of(k)
-    qh = q.read(np.int8, m * kp).reshape(m, kp)
+    mp = (m + 15) // 16 * 16
+    img = q.read(np.int8, mp * kp)
+    rr, kk = np.meshgrid(np.arange(m), np.arange(kp), indexing="ij")
+    tiled = ((rr // 16) * (kp // 64) + kk // 64) * 1024 + ((rr % 16) + 16 * ((kk % 64) // 16)) * 16 + kk % 16
+    qh = img[tiled]
     sh = s.read(np.float32, m)
     inv = np.frombuffer(blob[128 + k * 64 + 8 * 64:].tobytes(), np.float32)[:k]
     u_ref, s_ref = orc.quantize(x, inv)
