@@ -9,15 +9,28 @@ working set (about 0.8 GB) exceeds the 256 MB MALL.  Weights are prepacked
 once at load, outside the timed region.
 
 Printed: one JSON line with the headline TOPS, the GEMM kernel's roofline
-(HIP events around every GEMM launch inside the timed region), the M=1 decode
+(per-kernel averages from graph replays of back-to-back launches), the M=1 decode
 HBM bandwidth (K=4096, N=14336) and a CPU baseline (the oracle, multithreaded,
 on a bounded row sample of the same workload).
 
     python bench.py [--steps 200] [--warmup 20] [--config headline|all] [--no-cpu]
+
+Profiling helpers (their output is what profiles/ holds):
+    python bench.py --traffic-probe        a plain 256 MiB copy, then 12 headline
+                                           GEMM launches: the workload of the
+                                           FETCH_SIZE / WRITE_SIZE rocprofv3 passes
+    python bench.py --profile-summary DIR  markdown summary of the rocprofv3 CSV
+                                           output under DIR (kernel stats and/or
+                                           per-dispatch counters)
 """
 import argparse
+import csv
+import glob
 import json
 import os
+import platform
+import re
+import statistics
 import sys
 import time
 
@@ -31,6 +44,9 @@ import htp_ops as hip  # noqa: E402
 METRIC = "W8A8 INT8 TOPS & %MFMA peak (M=4096,K=1536,N=6144); M=1 decode HBM GB/s"
 PEAK_INT8_TOPS = 5000.0   # MI355X dense INT8 MFMA
 PEAK_HBM_GBPS = 8000.0    # MI355X HBM3E
+HEADLINE = (4096, 1536, 6144)
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "w8a8_gemm_tiles_4096x1536x6144_traffic.md")
+COPY_PROBE_BYTES = 256 << 20
 
 
 def w8a8_bytes(m, k, n):
@@ -70,65 +86,153 @@ class W8A8Set:
 
 
 def run_w8a8(m, k, n, steps, warmup, rotate, outliers=0.0, scale=(1e-4, 1e-3)):
+    """Times `steps` opcode-15 steps replayed from one HIP graph (no host
+    launch cost inside the timed region), then the same number of GEMM-only
+    and quantize-only launches, each from its own graph, for per-kernel
+    averages (HIP events on the library stream that runs the kernels)."""
     lib = hip.lib()
     stream = hip.default_stream()
     sets = [W8A8Set(m, k, n, seed, outliers, *scale) for seed in range(rotate)]
-    ev = [(hip.Event(), hip.Event()) for _ in range(steps)]
 
-    def step(i, events=None):
-        st = sets[i % rotate]
+    def quant(st):
         hip.check(lib.hb_w8a8_quantize(st.q.ptr, st.s.ptr, st.x.ptr, st.inv_ptr, m, k, stream), "quantize")
-        if events:
-            events[0].record(stream)
+
+    def gemm(st):
         hip.check(lib.hb_w8a8_gemm(st.y.ptr, n, st.q.ptr, st.s.ptr, st.packed.ptr, m, k, n, hip.EPI_SCALE,
                                    stream), "gemm")
-        if events:
-            events[1].record(stream)
 
-    for i in range(warmup):
-        step(i)
-    hip.check(lib.hb_stream_sync(stream), "sync")
-    hip.sync()
-    t_begin, t_end = hip.Event(), hip.Event()
+    def step(st):
+        quant(st)
+        gemm(st)
+
+    def capture(fn, count):
+        with hip.Graph.capture(stream) as g:
+            for i in range(count):
+                fn(sets[i % rotate])
+        return g
+
+    def synced():
+        hip.check(lib.hb_stream_sync(stream), "sync")
+        hip.sync()
+
+    def timed(graph):
+        a, b = hip.Event(), hip.Event()
+        synced()
+        a.record(stream)
+        graph.launch(stream)
+        b.record(stream)
+        synced()
+        return a.elapsed_ms(b)
+
+    for st in sets:  # eager pass: every set quantized once before graphs reuse q
+        step(st)
+    synced()
+    g_warm = capture(step, max(warmup, 1))
+    g_steps = capture(step, steps)
+    g_gemm = capture(gemm, steps)
+    g_quant = capture(quant, steps)
+    g_warm.launch(stream)
     wall0 = time.perf_counter()
-    t_begin.record(stream)
-    for i in range(steps):
-        step(i, ev[i])
-    t_end.record(stream)
-    hip.check(lib.hb_stream_sync(stream), "sync")
-    hip.sync()
+    total_ms = timed(g_steps)
     wall = time.perf_counter() - wall0
-    total_ms = t_begin.elapsed_ms(t_end)
-    gemm_ms = np.array([a.elapsed_ms(b) for a, b in ev])
-    return {"ms_per_step": total_ms / steps, "wall_ms_per_step": wall * 1e3 / steps,
-            "gemm_ms_mean": float(gemm_ms.mean()), "gemm_ms_median": float(np.median(gemm_ms)),
-            "sets": sets}
+    gemm_ms = timed(g_gemm) / steps
+    quant_ms = timed(g_quant) / steps
+    return {"ms_per_step": total_ms / steps, "wall_ms_per_step": wall * 1e3 / steps, "gemm_ms_mean": gemm_ms,
+            "quant_ms_mean": quant_ms, "sets": sets}
 
 
-def cpu_baseline(m, k, n, target_s=10.0):
-    """Oracle (portable C, pthreads) on a row sample of the same workload."""
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(m, k, n, target_s=12.0, min_reps=5):
+    """Oracle (portable C11, pthreads, -O2 -march=x86-64-v3 -ffp-contract=off)
+    on the same workload: the full opcode-15 semantics (quantize, int32
+    accumulate, scale epilogue).  Rows are sampled only if one full pass would
+    exceed target_s / min_reps; the median over the repetitions is reported."""
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     import oracle
 
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or os.cpu_count() or 1
-    threads = max(1, min(threads, os.cpu_count() or 1))
+    online = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or online
+    threads = max(1, min(threads, online))
     rng = np.random.default_rng(1234)
     w = rng.integers(-127, 128, (n, k), dtype=np.int8)
     blob = oracle.pack_blob(w, rng.uniform(1e-4, 1e-3, n).astype(np.float32))
 
-    def timed(rows):
-        x = rng.standard_normal((rows, k), dtype=np.float32)
+    def timed(x):
         t0 = time.perf_counter()
         oracle.linear(x, blob, k, n, nthreads=threads)
         return time.perf_counter() - t0
 
-    probe_rows = max(threads, 16)
-    t = timed(probe_rows)
-    rows = int(min(m, max(probe_rows, probe_rows * target_s / max(t, 1e-6))))
-    t = timed(rows)
-    tops = 2.0 * rows * n * k / t / 1e12
+    probe_rows = min(m, max(threads, 16))
+    t_probe = timed(rng.standard_normal((probe_rows, k), dtype=np.float32))
+    per_row = max(t_probe / probe_rows, 1e-9)
+    rows = int(min(m, max(probe_rows, target_s / min_reps / per_row)))
+    x = rng.standard_normal((rows, k), dtype=np.float32)
+    # the probe carries fixed costs (thread start-up): re-estimate once at size
+    t_first = timed(x)
+    grown = int(min(m, rows * (target_s / min_reps) / max(t_first, 1e-9)))
+    if grown > rows * 1.2:
+        rows = grown
+        x = rng.standard_normal((rows, k), dtype=np.float32)
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < min_reps or (time.perf_counter() - t_start < target_s and len(times) < 200):
+        times.append(timed(x))
+    med = statistics.median(times)
+    tops = 2.0 * rows * n * k / med / 1e12
     return {"value": round(tops, 4), "unit": "TOPS", "cores": threads, "kind": "port",
-            "sample": f"{rows} of {m} rows x K={k} x N={n} (full opcode-15 semantics), {t:.1f} s"}
+            "sample": f"{rows} of {m} rows x K={k} x N={n} (full opcode-15 semantics), median of {len(times)} "
+                      f"reps, {med * 1e3:.1f} ms each, {time.perf_counter() - t_start:.1f} s total",
+            "cpu_model": cpu_model(), "online_cores": online}
+
+
+def e2e_opcode15(m, k, n, reps=10):
+    """Opcode 15 through execute_op_simple (the executor's validation, weight
+    cache lookup, launch and stream sync), on rpcmem buffers in HBM and on
+    pinned host buffers (the latter adds the H2D of x and the D2H of y)."""
+    rng = np.random.default_rng(99)
+    x = rng.standard_normal((m, k), dtype=np.float32)
+    w = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    blob = hip.pack_constants(w, rng.uniform(1e-4, 1e-3, n).astype(np.float32))
+    out = {}
+    for where, device in (("device_rpcmem", True), ("host_rpcmem", False)):
+        bufs = [hip.RpcBuffer(m * n * 4, device=device), hip.RpcBuffer(m * k * 4, device=device),
+                hip.RpcBuffer(blob.nbytes, device=device)]
+        bufs[1].write(x)
+        bufs[2].write(blob)
+        payload = hip.w8a8_params((bufs[0].fd, 0), (bufs[1].fd, 0), (bufs[2].fd, 0), m, k, n)
+        times = []
+        for i in range(reps + 2):
+            t0 = time.perf_counter()
+            rc, after = hip.execute(hip.OP_MAT_MUL_NATIVE_W8A8, payload)
+            if rc != 0:
+                raise RuntimeError(f"opcode 15 returned {rc}: {hip.last_error()}")
+            if i >= 2:
+                times.append(time.perf_counter() - t0)
+        elapsed_us = int.from_bytes(after[36:40], "little", signed=True)
+        out[where] = {"ms_median": round(statistics.median(times) * 1e3, 4), "elapsed_us_field": elapsed_us}
+        for b in bufs:
+            b.free()
+    return out
+
+
+def read_traffic():
+    """HBM bytes per headline GEMM launch from the committed PMC summary."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            match = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", f.read(), re.M)
+    except OSError:
+        return None
+    return int(match.group(1)) if match else None
 
 
 def decode_case(m, k, n, steps, warmup, rotate):
@@ -139,7 +243,7 @@ def decode_case(m, k, n, steps, warmup, rotate):
             "frac_hbm": round(op_bytes / (r["ms_per_step"] * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
             "gemm_us": round(r["gemm_ms_mean"] * 1e3, 3),
             "gemm_gbps": round(gemm_bytes(m, k, n) / (r["gemm_ms_mean"] * 1e-3) / 1e9, 1),
-            "rotated_sets": rotate}
+            "quant_us": round(r["quant_ms_mean"] * 1e3, 3), "rotated_sets": rotate}
 
 
 def all_configs(steps, warmup):
@@ -160,6 +264,59 @@ def all_configs(steps, warmup):
     return out
 
 
+def traffic_probe(steps=12):
+    """Workload of the FETCH_SIZE / WRITE_SIZE passes: a plain elementwise
+    copy of COPY_PROBE_BYTES (torch's unary kernel, reads and writes each byte
+    once) for calibration, then the headline GEMM on rotated sets."""
+    import torch
+
+    src = torch.empty(COPY_PROBE_BYTES // 4, dtype=torch.float32, device="cuda:0").normal_()
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
+    torch.cuda.empty_cache()
+    hip.init(0)
+    m, k, n = HEADLINE
+    r = run_w8a8(m, k, n, steps, 2, 6, outliers=0.01)
+    print(f"traffic probe done: gemm {r['gemm_ms_mean'] * 1e3:.2f} us", flush=True)
+
+
+def _short(name):
+    name = name.replace("(anonymous namespace)::", "")
+    return name if len(name) <= 110 else name[:107] + "..."
+
+
+def profile_summary(directory):
+    """Markdown summary of the rocprofv3 CSV files under directory."""
+    lines = []
+    for path in sorted(glob.glob(os.path.join(directory, "**", "*kernel_stats.csv"), recursive=True)):
+        lines.append(f"### kernel stats ({os.path.relpath(path, directory)})\n")
+        lines.append("| kernel | calls | average us | min us | max us | % time |")
+        lines.append("|---|---|---|---|---|---|")
+        with open(path) as f:
+            for row in csv.DictReader(f):
+                lines.append(f"| `{_short(row['Name'])}` | {row['Calls']} | {float(row['AverageNs']) / 1e3:.3f} | "
+                             f"{float(row['MinNs']) / 1e3:.3f} | {float(row['MaxNs']) / 1e3:.3f} | "
+                             f"{float(row['Percentage']):.2f} |")
+        lines.append("")
+    counters = {}
+    for path in sorted(glob.glob(os.path.join(directory, "**", "*counter_collection.csv"), recursive=True)):
+        with open(path) as f:
+            for row in csv.DictReader(f):
+                key = (_short(row["Kernel_Name"]), row["Counter_Name"])
+                counters.setdefault(key, []).append(float(row["Counter_Value"]))
+    if counters:
+        lines.append("### counters, mean per dispatch\n")
+        lines.append("| kernel | counter | mean | dispatches |")
+        lines.append("|---|---|---|---|")
+        for (kernel, counter), vals in sorted(counters.items()):
+            lines.append(f"| `{kernel}` | {counter} | {statistics.fmean(vals):.1f} | {len(vals)} |")
+        lines.append("")
+    print("\n".join(lines))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -168,15 +325,23 @@ def main():
     ap.add_argument("--rotate", type=int, default=6)
     ap.add_argument("--config", default="headline", choices=["headline", "all"])
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--traffic-probe", action="store_true")
+    ap.add_argument("--profile-summary", metavar="DIR")
     args = ap.parse_args()
+    if args.profile_summary:
+        profile_summary(args.profile_summary)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the path is single-GPU; "
               "multi-GPU sharding is design-only). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     rank = int(os.environ.get("RANK", "0"))
+    if args.traffic_probe:
+        traffic_probe()
+        return
 
     hip.init(0)
-    m, k, n = 4096, 1536, 6144
+    m, k, n = HEADLINE
     r = run_w8a8(m, k, n, args.steps, args.warmup, args.rotate, outliers=0.01)
     ops = 2.0 * m * n * k
     tops = ops / (r["ms_per_step"] * 1e-3) / 1e12
@@ -199,15 +364,17 @@ def main():
                    "m": m, "k": k, "n": n, "rotated_sets": args.rotate},
         "mfma_frac_full_op": round(tops / PEAK_INT8_TOPS, 4),
         "hbm_gbps_full_op": round(w8a8_bytes(m, k, n) / (r["ms_per_step"] * 1e-3) / 1e9, 1),
+        "quant_us": round(r["quant_ms_mean"] * 1e3, 3),
         "roofline": {"kernel": "w8a8_gemm_tiles", "bound": "mfma", "achieved": round(gemm_tops, 2),
                      "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s", "frac": round(gemm_tops / PEAK_INT8_TOPS, 4),
-                     "traffic": None, "gemm_us": round(r["gemm_ms_mean"] * 1e3, 3),
+                     "traffic": read_traffic(), "gemm_us": round(r["gemm_ms_mean"] * 1e3, 3),
                      "gemm_gbps": round(gemm_bytes(m, k, n) / (r["gemm_ms_mean"] * 1e-3) / 1e9, 1),
                      "algorithmic_ops_per_launch": ops,
                      "algorithmic_bytes_per_launch": gemm_bytes(m, k, n)},
     }
     del r
     line["decode_m1"] = decode_case(1, 4096, 14336, args.steps, args.warmup, 6)
+    line["e2e_opcode15"] = e2e_opcode15(m, k, n)
     if args.config == "all":
         line["configs"] = all_configs(args.steps, args.warmup)
     if not args.no_cpu and rank == 0:

@@ -185,4 +185,43 @@ int hb_event_elapsed_ms(float *ms, hb_event start, hb_event stop) {
   return err == hipSuccess ? HB_OK : hb_fail(err, "hipEventElapsedTime");
 }
 
+// Stream capture into a HIP graph (relaxed mode: host-side library calls
+// made while capturing, such as attribute queries, stay legal).
+int hb_graph_begin(hb_stream s) {
+  hipStream_t st = hb_resolve_stream(s);
+  if (st == nullptr) return hb_invalid("hb_graph_begin stream");
+  hipError_t err = hipStreamBeginCapture(st, hipStreamCaptureModeRelaxed);
+  return err == hipSuccess ? HB_OK : hb_fail(err, "hipStreamBeginCapture");
+}
+
+int hb_graph_end(hb_graph *g, hb_stream s) {
+  if (g == nullptr) return hb_invalid("hb_graph_end out");
+  *g = nullptr;
+  hipGraph_t graph = nullptr;
+  hipError_t err = hipStreamEndCapture(hb_resolve_stream(s), &graph);
+  if (err != hipSuccess) return hb_fail(err, "hipStreamEndCapture");
+  hipGraphExec_t exec = nullptr;
+  err = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  hipError_t derr = hipGraphDestroy(graph);
+  if (err != hipSuccess) return hb_fail(err, "hipGraphInstantiate");
+  if (derr != hipSuccess) {
+    (void)hipGraphExecDestroy(exec);
+    return hb_fail(derr, "hipGraphDestroy");
+  }
+  *g = (hb_graph)exec;
+  return HB_OK;
+}
+
+int hb_graph_launch(hb_graph g, hb_stream s) {
+  if (g == nullptr) return hb_invalid("hb_graph_launch graph");
+  hipError_t err = hipGraphLaunch((hipGraphExec_t)g, hb_resolve_stream(s));
+  return err == hipSuccess ? HB_OK : hb_fail(err, "hipGraphLaunch");
+}
+
+int hb_graph_destroy(hb_graph g) {
+  if (g == nullptr) return HB_OK;
+  hipError_t err = hipGraphExecDestroy((hipGraphExec_t)g);
+  return err == hipSuccess ? HB_OK : hb_fail(err, "hipGraphExecDestroy");
+}
+
 }  // extern "C"

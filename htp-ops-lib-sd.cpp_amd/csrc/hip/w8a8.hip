@@ -11,6 +11,7 @@
 // which equals acc - (sums << 7) modulo 2^32 for every input.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdint>
 #include <cstdlib>
 
@@ -493,38 +494,63 @@ __global__ __launch_bounds__(256) void w8a8_planes(uint8_t *__restrict__ out, co
 // Host-side dispatch.
 // ---------------------------------------------------------------------------
 
-// Candidate tile shapes; occ = workgroups resident per CU (LDS / register bound).
+// Candidate tile shapes in order of preference when the cost model ties;
+// occ = workgroups resident per CU (LDS / register bound).  Two resident
+// workgroups let one's epilogue stores overlap the other's MFMA loop, which
+// is why 128x192 leads (measured at 4096x1536x6144: 128x192 57 us,
+// 128x128 62 us, 256x192 64 us, 256x256 73 us).
+// eff = measured MAC throughput of a full round of that shape relative to
+// 128x192 (LDS traffic per MAC grows as tiles shrink; 64x64 is an estimate).
 struct TileShape {
-  int bm, bn, occ;
+  int bm, bn, occ, eff;
 };
-constexpr TileShape kTileShapes[] = {{256, 256, 1}, {256, 192, 1}, {128, 192, 2}, {128, 128, 2}, {64, 64, 4}};
+constexpr TileShape kTileShapes[] = {
+    {128, 192, 2, 100}, {256, 192, 1, 90}, {128, 128, 2, 92}, {256, 256, 1, 100}, {64, 64, 4, 60}};
 constexpr int kNumShapes = 5;
-constexpr int kCUs = 256;
 
-// HTP_OPS_AMD_W8A8_TILE=<index into kTileShapes> pins the tile shape (tuning sweeps).
+// -1: automatic.  Set by hb_w8a8_force_tile; HTP_OPS_AMD_W8A8_TILE gives
+// the initial value.
+std::atomic<int> g_forced_tile{-2};
+
 int forced_tile_shape() {
-  static int forced = -2;
+  int forced = g_forced_tile.load(std::memory_order_relaxed);
   if (forced == -2) {
     const char *v = getenv("HTP_OPS_AMD_W8A8_TILE");
     forced = (v && *v) ? atoi(v) : -1;
-    if (forced >= kNumShapes) forced = -1;
+    if (forced < -1 || forced >= kNumShapes) forced = -1;
+    int expected = -2;
+    if (!g_forced_tile.compare_exchange_strong(expected, forced)) forced = expected;
   }
   return forced;
 }
 
+int compute_units() {
+  static std::atomic<int> cus{0};
+  int v = cus.load(std::memory_order_relaxed);
+  if (v == 0) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
+      v = 256;
+    cus.store(v, std::memory_order_relaxed);
+  }
+  return v;
+}
+
 // Picks the shape minimising (rounds of resident workgroups) x (work per
-// round per CU); ties go to the larger tile (less operand traffic).
+// round per CU) / eff; ties go to the earlier entry of kTileShapes.
 int pick_tile_shape(int m, int n) {
   const int forced = forced_tile_shape();
   if (forced >= 0 && (kTileShapes[forced].bn != 192 || n % 192 == 0)) return forced;
+  const int cus = compute_units();
   int best = 0;
   long long best_cost = -1;
   for (int i = 0; i < kNumShapes; ++i) {
     const TileShape t = kTileShapes[i];
     if (t.bn == 192 && n % 192 != 0) continue;
     const long long tiles = (long long)((m + t.bm - 1) / t.bm) * ((n + t.bn - 1) / t.bn);
-    const long long slots = (long long)kCUs * t.occ;
-    const long long cost = (tiles + slots - 1) / slots * t.bm * t.bn * t.occ;
+    const long long slots = (long long)cus * t.occ;
+    const long long cost = (tiles + slots - 1) / slots * t.bm * t.bn * t.occ * 100 / t.eff;
     if (best_cost < 0 || cost < best_cost) {
       best_cost = cost;
       best = i;
@@ -541,7 +567,7 @@ int launch_tiles(void *y, int ldy, const int8_t *q, const float *scales, const i
   const int grid = ((m + t.bm - 1) / t.bm) * ((n + t.bn - 1) / t.bn);
   switch (shape) {
     case 0:
-      hipLaunchKernelGGL((w8a8_gemm_tiles<256, 256, 2, 2, 4, EPI>), dim3(grid), dim3(256), 0, st, y, ldy, q, scales,
+      hipLaunchKernelGGL((w8a8_gemm_tiles<128, 192, 2, 2, 4, EPI>), dim3(grid), dim3(256), 0, st, y, ldy, q, scales,
                          wpack, sw, corr, m, n, kp);
       break;
     case 1:
@@ -549,11 +575,11 @@ int launch_tiles(void *y, int ldy, const int8_t *q, const float *scales, const i
                          wpack, sw, corr, m, n, kp);
       break;
     case 2:
-      hipLaunchKernelGGL((w8a8_gemm_tiles<128, 192, 2, 2, 4, EPI>), dim3(grid), dim3(256), 0, st, y, ldy, q, scales,
+      hipLaunchKernelGGL((w8a8_gemm_tiles<128, 128, 2, 2, 4, EPI>), dim3(grid), dim3(256), 0, st, y, ldy, q, scales,
                          wpack, sw, corr, m, n, kp);
       break;
     case 3:
-      hipLaunchKernelGGL((w8a8_gemm_tiles<128, 128, 2, 2, 4, EPI>), dim3(grid), dim3(256), 0, st, y, ldy, q, scales,
+      hipLaunchKernelGGL((w8a8_gemm_tiles<256, 256, 2, 2, 4, EPI>), dim3(grid), dim3(256), 0, st, y, ldy, q, scales,
                          wpack, sw, corr, m, n, kp);
       break;
     default:
@@ -705,6 +731,12 @@ int hb_w8a8_linear(float *d_y, const float *d_x, const void *d_packed, int m, in
   int rc = hb_w8a8_quantize(q, scales, d_x, inv, m, k, s);
   if (rc) return rc;
   return hb_w8a8_gemm(d_y, n, q, scales, d_packed, m, k, n, epilogue, s);
+}
+
+int hb_w8a8_force_tile(int index) {
+  if (index < -1 || index >= kNumShapes) return hb_invalid("hb_w8a8_force_tile index");
+  forced_tile_shape();  // settle the environment default first
+  return g_forced_tile.exchange(index);
 }
 
 int hb_w8a8_planes_from_raw(uint8_t *d_out, const int32_t *d_raw, int m, int n, hb_stream s) {

@@ -54,6 +54,10 @@ _SIGNATURES = {
     "hb_event_record": (_c_int, [_c_void_p, _c_void_p]),
     "hb_event_sync": (_c_int, [_c_void_p]),
     "hb_event_elapsed_ms": (_c_int, [ctypes.POINTER(ctypes.c_float), _c_void_p, _c_void_p]),
+    "hb_graph_begin": (_c_int, [_c_void_p]),
+    "hb_graph_end": (_c_int, [ctypes.POINTER(_c_void_p), _c_void_p]),
+    "hb_graph_launch": (_c_int, [_c_void_p, _c_void_p]),
+    "hb_graph_destroy": (_c_int, [_c_void_p]),
     # W8A8
     "hb_w8a8_packed_bytes": (_c_size_t, [_c_int, _c_int]),
     "hb_w8a8_packed_offset": (_c_size_t, [_c_int, _c_int, _c_int]),
@@ -65,6 +69,7 @@ _SIGNATURES = {
     "hb_w8a8_linear": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_void_p,
                                 _c_size_t, _c_void_p]),
     "hb_w8a8_planes_from_raw": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
+    "hb_w8a8_force_tile": (_c_int, [_c_int]),
     # F16
     "hb_f16_packed_bytes": (_c_size_t, [_c_int, _c_int]),
     "hb_f16_prepack": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
@@ -295,6 +300,18 @@ def w8a8_linear(y_dev, x_dev, packed, m, k, n, workspace, epilogue=EPI_SCALE, st
                                workspace.nbytes, stream), "hb_w8a8_linear")
 
 
+W8A8_TILE_SHAPES = ((128, 192), (256, 192), (128, 128), (256, 256), (64, 64))
+
+
+def w8a8_force_tile(index):
+    """Pins the tiled W8A8 kernel's shape (index into W8A8_TILE_SHAPES, -1 =
+    automatic); returns the previous setting."""
+    prev = lib().hb_w8a8_force_tile(index)
+    if prev < -1:
+        check(prev, "hb_w8a8_force_tile")
+    return prev
+
+
 def w8a8_planes_from_raw(out_dev, raw_dev, m, n):
     check(lib().hb_w8a8_planes_from_raw(out_dev.ptr, raw_dev.ptr, m, n, None), "hb_w8a8_planes_from_raw")
 
@@ -337,6 +354,45 @@ class Event:
             lib().hb_event_destroy(self.ptr)
         except Exception:
             pass
+
+
+class Graph:
+    """Work captured from a stream: `with Graph.capture(stream) as g:` enqueue
+    library calls on stream, then g.launch(stream) replays them."""
+
+    def __init__(self):
+        self.ptr = None
+
+    @classmethod
+    def capture(cls, stream):
+        return _GraphCapture(cls(), stream)
+
+    def launch(self, stream=None):
+        check(lib().hb_graph_launch(self.ptr, stream), "hb_graph_launch")
+
+    def __del__(self):
+        try:
+            if self.ptr:
+                lib().hb_graph_destroy(self.ptr)
+        except Exception:
+            pass
+
+
+class _GraphCapture:
+    def __init__(self, graph, stream):
+        self.graph, self.stream = graph, stream
+
+    def __enter__(self):
+        check(lib().hb_graph_begin(self.stream), "hb_graph_begin")
+        return self.graph
+
+    def __exit__(self, exc_type, exc, tb):
+        g = ctypes.c_void_p()
+        rc = lib().hb_graph_end(ctypes.byref(g), self.stream)
+        self.graph.ptr = g.value
+        if exc_type is None:
+            check(rc, "hb_graph_end")
+        return False
 
 
 def default_stream():

@@ -37,6 +37,7 @@ extern "C" {
 
 typedef void *hb_stream; /* a hipStream_t */
 typedef void *hb_event;  /* a hipEvent_t */
+typedef void *hb_graph;  /* an instantiated hipGraphExec_t */
 
 /* ---- runtime ------------------------------------------------------------- */
 int hb_device_count(void);
@@ -60,6 +61,13 @@ int hb_event_destroy(hb_event e);
 int hb_event_record(hb_event e, hb_stream s);
 int hb_event_sync(hb_event e);
 int hb_event_elapsed_ms(float *ms, hb_event start, hb_event stop);
+/* Graph capture of the work enqueued on s between begin and end (kernel
+ * launches of this library only: no memset or copy is captured by it); the
+ * instantiated graph replays that work on any stream. */
+int hb_graph_begin(hb_stream s);
+int hb_graph_end(hb_graph *g, hb_stream s);
+int hb_graph_launch(hb_graph g, hb_stream s);
+int hb_graph_destroy(hb_graph g);
 
 /* ---- W8A8 (opcode 15) ----------------------------------------------------- */
 
@@ -107,6 +115,13 @@ enum {
  * (elements, >= n, a multiple of 4). */
 int hb_w8a8_gemm(void *d_y, int ldy, const int8_t *d_q, const float *d_scales, const void *d_packed, int m, int k,
                  int n, int epilogue, hb_stream s);
+
+/* Tuning and test hook: pins the tiled kernel's shape for every later call
+ * (index into 128x192, 256x192, 128x128, 256x256, 64x64; shapes 192 wide
+ * apply only when n % 192 == 0) or restores automatic choice with -1.
+ * Returns the previous setting.  Results are identical for every shape.
+ * The environment variable HTP_OPS_AMD_W8A8_TILE gives the initial value. */
+int hb_w8a8_force_tile(int index);
 
 /* Full opcode-15 computation: quantize + GEMM + epilogue (workspace from hb_w8a8_workspace_bytes). */
 int hb_w8a8_linear(float *d_y, const float *d_x, const void *d_packed, int m, int k, int n, int epilogue,

@@ -87,10 +87,11 @@ GEMM_SHAPES = [
     (16, 1024, 2048),  # decode, full 16 rows
     (16, 14336, 256),  # decode, K beyond the reference envelope
     (1, 96, 64),       # decode, K % 64 == 32
-    (300, 1536, 768),  # 64x64 tiles
-    (2048, 128, 2048),  # 128x128 tiles
-    (4096, 64, 4096),  # 256x256 tiles
-    (1000, 96, 4096),  # 256x256 tiles with M tail and K % 64 == 32
+    (300, 1536, 768),  # tiled kernels (automatic shape choice from here on)
+    (2048, 128, 2048),
+    (4096, 64, 4096),
+    (1000, 96, 4096),  # M tail and K % 64 == 32
+    (4096, 1536, 6144),  # headline shape
 ]
 
 
@@ -119,6 +120,32 @@ def test_w8a8_linear_bit_exact(hip, orc, m, k, n):
     y = hip.DeviceBuffer(m * n * 4)
     hip.w8a8_linear(y, xd, packed, m, k, n, ws)
     hip.sync()
+    ref = orc.linear(x, blob, k, n)
+    got = y.read(np.float32, m * n).reshape(m, n)
+    np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("tile", range(5))
+@pytest.mark.parametrize("m,k,n", [(261, 224, 960), (300, 1536, 576)])
+def test_w8a8_every_tile_shape_bit_exact(hip, orc, tile, m, k, n):
+    """Each tiled kernel instantiation, pinned in turn, with M, N and K tails
+    (n = 960 is a multiple of 192 but not of 128 or 256)."""
+    x, _, blob = make_w8a8(orc, m, k, n, seed=tile * 31 + m, inv_kind="uniform", sums_kind="random")
+    packed = hip.w8a8_prepack(upload_blob(hip, blob), k, n)
+    xd = hip.DeviceBuffer.from_array(x)
+    q, s = hip.w8a8_quantize(xd, packed.ptr + hip.w8a8_packed_offset(k, n, hip.SECTION_INV), m, k)
+    raw = hip.DeviceBuffer(m * n * 4)
+    y = hip.DeviceBuffer(m * n * 4)
+    prev = hip.w8a8_force_tile(tile)
+    try:
+        hip.w8a8_gemm(raw, q, s, packed, m, k, n, hip.EPI_RAW)
+        hip.w8a8_gemm(y, q, s, packed, m, k, n, hip.EPI_SCALE)
+        hip.sync()
+    finally:
+        hip.w8a8_force_tile(prev)
+    inv = np.frombuffer(blob[128 + k * n + 8 * n:].tobytes(), np.float32)[:k]
+    u, _ = orc.quantize(x, inv)
+    np.testing.assert_array_equal(raw.read(np.int32, m * n).reshape(m, n), orc.accumulate(u, blob, k, n))
     ref = orc.linear(x, blob, k, n)
     got = y.read(np.float32, m * n).reshape(m, n)
     np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
@@ -206,3 +233,30 @@ def test_f16_all_ones_gives_k(hip, orc):
     hip.f16_gemm(y, hip.DeviceBuffer.from_array(x), packed, None, m, k, n, n, 0)
     hip.sync()
     assert (y.read(np.float32, m * n) == k).all()
+
+
+@pytest.mark.parametrize("m,k,n", [(300, 256, 576), (1, 4096, 1024)])
+def test_graph_replays_match_eager(hip, orc, m, k, n):
+    """hb_w8a8_linear captured into a graph: every replay, with other eager
+    work on the same workspace between replays, equals the eager result."""
+    x, _, blob = make_w8a8(orc, m, k, n, seed=5, inv_kind="uniform", sums_kind="random")
+    x2 = orc.normal(m * k, 0.0, 3.0, 6).reshape(m, k)
+    packed = hip.w8a8_prepack(upload_blob(hip, blob), k, n)
+    xd, x2d = hip.DeviceBuffer.from_array(x), hip.DeviceBuffer.from_array(x2)
+    ws = hip.DeviceBuffer(hip.w8a8_workspace_bytes(m, k))
+    y_eager, y_graph, y_other = (hip.DeviceBuffer(m * n * 4) for _ in range(3))
+    stream = hip.default_stream()
+    hip.w8a8_linear(y_eager, xd, packed, m, k, n, ws, stream=stream)
+    hip.sync()
+    eager = y_eager.read(np.uint32, m * n)
+    np.testing.assert_array_equal(eager.view(np.float32).reshape(m, n).view(np.uint32),
+                                  orc.linear(x, blob, k, n).view(np.uint32))
+    with hip.Graph.capture(stream) as graph:
+        hip.w8a8_linear(y_graph, xd, packed, m, k, n, ws, stream=stream)
+    for _ in range(4):
+        y_graph.zero()
+        hip.w8a8_linear(y_other, x2d, packed, m, k, n, ws, stream=stream)  # overwrites the workspace
+        hip.sync()
+        graph.launch(stream)
+        hip.sync()
+        np.testing.assert_array_equal(y_graph.read(np.uint32, m * n), eager)
