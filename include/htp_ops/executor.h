@@ -23,8 +23,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
-#include "htp_ops/message.h"
-#include "htp_ops/op_reg.h"
+#include "message.h"
+#include "op_reg.h"
 
 #ifdef __cplusplus
 extern "C" {

@@ -10,7 +10,7 @@
 
 #include <stdint.h>
 
-#include "htp_ops/session.h"
+#include "session.h"
 
 #ifdef __cplusplus
 extern "C" {

@@ -17,7 +17,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
-#include "htp_ops/message.h"
+#include "message.h"
 
 #ifdef __cplusplus
 extern "C" {

@@ -10,7 +10,7 @@
 
 #include <stdint.h>
 
-#include "htp_ops/htp_ops.h"
+#include "htp_ops.h"
 
 #ifdef __cplusplus
 extern "C" {

@@ -11,6 +11,32 @@
  * conversion; the bit-level QFloat rounding is not observable from the
  * reference's own tests, so the reference contract is defined as IEEE per
  * operation (see the per-function notes in htp_oracle.c).
+ *
+ * Parity status of each function (what pins it; tests/test_oracle.py,
+ * tests/test_abi.py, tests/test_golden.py):
+ *   f32<->f16                 pinned: exhaustive against numpy's binary16.
+ *   blob pack/unpack/offset,  pinned: the reference's address formula
+ *   check_header                (linear_w8a8.c:453,482,486-488, study_dsp.c:82-84),
+ *                               bijection, one-hot and round-trip tests, the
+ *                               header rule of op_executor.cc:331-335.
+ *   accumulate                pinned: int64 brute force, one-hot, the boundary
+ *                               targets of integer_tests.c:97, the study data
+ *                               expectation of study_host.c:11-15.
+ *   quantize_value(s),        pinned to the IEEE-per-operation definition:
+ *   quantize, output, linear    closed forms, ties-to-even and clamp special
+ *                               cases, exhaustive rintf comparison, numpy float32
+ *                               restatements.  Parity unpinned against the
+ *                               reference hardware's QFloat rounding (no test of
+ *                               the reference observes it).
+ *   planes                    pinned: reassembly of the byte planes into the
+ *                               accumulator (layout of linear_w8a8.c:209-227).
+ *   gelu_tanh, quick_gelu     pinned to the closed forms in double within the
+ *                               2e-3 bound; parity unpinned against the
+ *                               reference's HVX exp2 polynomial (hvx_math.h:526-613).
+ *   f16_permute/_index        pinned: the writer formula of test.c:551-556, one-hot.
+ *   f16_gemm_epilogue         pinned: float64 brute force, all-ones gives K,
+ *                               one-hot; parity unpinned against the HMX FP16
+ *                               accumulation order and precision (mat_mul.c:724-748).
  */
 #ifndef HTP_ORACLE_H
 #define HTP_ORACLE_H

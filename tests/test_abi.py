@@ -106,6 +106,8 @@ def test_layout_validation_matches_reference(own, ref):
 def declared_functions():
     names = set()
     for fname in os.listdir(INCLUDE):
+        if not fname.endswith(".h"):
+            continue  # include-path shims under host/ only forward
         text = open(os.path.join(INCLUDE, fname)).read()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
         text = re.sub(r"static inline[^{]*\{.*?\n\}", "", text, flags=re.S)
@@ -154,3 +156,14 @@ def test_wire_helpers_sizes():
     assert len(h.f16_epilogue_params((1, 0), (2, 0), (3, 0), (-1, 0), 1, 32, 32, 32, 0)) == 56
     assert len(h.matmul_params((1, 0), (2, 0), (3, 0), 1, 32, 32)) == 92
     assert len(h.matmul_params((1, 0), (2, 0), (3, 0), 1, 32, 32, True)) == 96
+
+
+def test_reference_style_caller_compiles_and_links(tmp_path):
+    """tests/dropin_caller.c keeps the reference host's include lines
+    ("host/session.h", <remote.h>, <rpcmem.h>, "htp_ops.h", "message.h",
+    "op_reg.h"); with -I include/htp_ops it builds against libhtp_ops.so alone."""
+    exe = tmp_path / "dropin"
+    subprocess.run(["gcc", "-std=gnu11", "-Wall", "-Werror", "-I", INCLUDE, os.path.join(REPO, "tests", "dropin_caller.c"),
+                    "-L", PKG, "-lhtp_ops", f"-Wl,-rpath,{PKG}", "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()
+    assert out == ["40", "56", "15", "1"]
