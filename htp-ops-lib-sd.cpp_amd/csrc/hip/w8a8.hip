@@ -184,6 +184,58 @@ __global__ __launch_bounds__(256) void w8a8_quant_rows_any(int8_t *__restrict__ 
   }
 }
 
+// One 512-thread workgroup per row: for few rows (a single wave per row is
+// latency bound there) and for rows longer than the register path holds.
+// Loads are unconditional with the index clamped into the row, so they all
+// issue before the first use; out-of-row values never reach the maximum.
+constexpr int kRowThreads = 512;
+
+template <int VX>
+__global__ __launch_bounds__(kRowThreads) void w8a8_quant_rows_wg(int8_t *__restrict__ q, float *__restrict__ scales,
+                                                                  const float *__restrict__ x,
+                                                                  const float *__restrict__ inv, int k, int kp) {
+  __shared__ float red[kRowThreads / 64];
+  const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const float4 *xr = (const float4 *)(x + (size_t)row * k);
+  const float4 *iv = (const float4 *)inv;
+  const int nvec = k / 4;
+  float4 a[VX], b[VX];
+#pragma unroll
+  for (int j = 0; j < VX; ++j) {
+    const int idx = min(tid + kRowThreads * j, nvec - 1);
+    a[j] = xr[idx];
+    b[j] = iv[idx];
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < VX; ++j) {
+    a[j] = make_float4(__fmul_rn(a[j].x, b[j].x), __fmul_rn(a[j].y, b[j].y), __fmul_rn(a[j].z, b[j].z),
+                       __fmul_rn(a[j].w, b[j].w));
+    if (tid + kRowThreads * j < nvec)
+      amax = fmaxf(amax, fmaxf(fmaxf(fabsf(a[j].x), fabsf(a[j].y)), fmaxf(fabsf(a[j].z), fabsf(a[j].w))));
+  }
+  amax = wave_max(amax);
+  if (lane == 0) red[wave] = amax;
+  __syncthreads();
+  amax = red[0];
+#pragma unroll
+  for (int w = 1; w < kRowThreads / 64; ++w) amax = fmaxf(amax, red[w]);
+  const float s = fmaxf(__fdiv_rn(amax, 127.0f), 1e-12f);
+  const float r = __fdiv_rn(1.0f, s);
+  if (tid == 0) scales[row] = s;
+  const int qvec = kp / 4;
+#pragma unroll
+  for (int j = 0; j < VX; ++j) {
+    const int idx = tid + kRowThreads * j;
+    if (idx < nvec) {
+      *q_word(q, kp, row, 4 * idx) = quantize_byte(a[j].x, r) | (quantize_byte(a[j].y, r) << 8) |
+                                    (quantize_byte(a[j].z, r) << 16) | (quantize_byte(a[j].w, r) << 24);
+    } else if (idx < qvec) {
+      *q_word(q, kp, row, 4 * idx) = 0u;
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Output epilogue shared by both GEMM kernels.
 // ---------------------------------------------------------------------------
@@ -466,6 +518,100 @@ __global__ __launch_bounds__(64 * WAVES) void w8a8_gemm_decode(void *__restrict_
 }
 
 // ---------------------------------------------------------------------------
+// Single-row decode with the quantization fused in (m == 1).  One workgroup
+// per 16-column block.  Each workgroup first requests the activation row and
+// the smoothing vector, then every packed weight tile of its block (wave w
+// owns tiles [w*VW, w*VW + VW), held in registers), so the row's
+// quantization runs while the weight stream is in flight; the quantized row
+// goes to LDS in the A-operand order and the tiles are consumed by MFMA.
+// The arithmetic is the quantization kernels' and the decode GEMM's, step for
+// step, so results are identical to the two-kernel path.
+// ---------------------------------------------------------------------------
+
+constexpr int kFusedWaves = 8;
+constexpr int kFusedThreads = 64 * kFusedWaves;
+
+template <int VW, int EPI>
+__global__ __launch_bounds__(kFusedThreads) void w8a8_decode_fused(void *__restrict__ y, const float *__restrict__ x,
+                                                                  const float *__restrict__ inv,
+                                                                  const int8_t *__restrict__ wpack,
+                                                                  const float *__restrict__ sw,
+                                                                  const int32_t *__restrict__ corr, int k, int kp) {
+  constexpr int VX = VW / 4;  // float4 per thread: VX * 512 * 4 = VW * 512 = the largest kp served
+  __shared__ __attribute__((aligned(16))) int8_t qs[VW * kFusedThreads];  // [kt][k/16 group][16 bytes]
+  __shared__ float red[kFusedWaves];
+  __shared__ hb_i32x4 part[kFusedWaves][64];
+  const int nb = blockIdx.x;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, tid = threadIdx.x;
+  const int kc = kp / kKStep, nvec = k / 4;
+  // 1. activation row and smoothing vector (clamped, unconditional loads)
+  float4 a[VX], iv[VX];
+#pragma unroll
+  for (int j = 0; j < VX; ++j) {
+    const int v = min(tid + kFusedThreads * j, nvec - 1);
+    a[j] = ((const float4 *)x)[v];
+    iv[j] = ((const float4 *)inv)[v];
+  }
+  const int col = nb * 16 + (lane & 15);
+  const int32_t cc = corr[col];
+  const float sc = sw[col];
+  // 2. this wave's weight tiles (indices clamped into the block: the extra
+  //    loads repeat the block's last tile and are never multiplied)
+  const int8_t *wb = wpack + (size_t)nb * kc * kFragBytes + lane * 16;
+  hb_i32x4 b[VW];
+#pragma unroll
+  for (int i = 0; i < VW; ++i)
+    b[i] = __builtin_nontemporal_load((const hb_i32x4 *)(wb + (size_t)min(wave * VW + i, kc - 1) * kFragBytes));
+  __builtin_amdgcn_sched_barrier(0);
+  // 3. row absmax of t = x * inv, then the quantized row into LDS
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < VX; ++j) {
+    a[j] = make_float4(__fmul_rn(a[j].x, iv[j].x), __fmul_rn(a[j].y, iv[j].y), __fmul_rn(a[j].z, iv[j].z),
+                       __fmul_rn(a[j].w, iv[j].w));
+    if (tid + kFusedThreads * j < nvec)
+      amax = fmaxf(amax, fmaxf(fmaxf(fabsf(a[j].x), fabsf(a[j].y)), fmaxf(fabsf(a[j].z), fabsf(a[j].w))));
+  }
+  amax = wave_max(amax);
+  if (lane == 0) red[wave] = amax;
+  __syncthreads();
+  amax = red[0];
+#pragma unroll
+  for (int w = 1; w < kFusedWaves; ++w) amax = fmaxf(amax, red[w]);
+  const float s = fmaxf(__fdiv_rn(amax, 127.0f), 1e-12f);
+  const float r = __fdiv_rn(1.0f, s);
+#pragma unroll
+  for (int j = 0; j < VX; ++j) {
+    const int v = tid + kFusedThreads * j;
+    if (v < kp / 4) {
+      const uint32_t word = v < nvec ? (quantize_byte(a[j].x, r) | (quantize_byte(a[j].y, r) << 8) |
+                                        (quantize_byte(a[j].z, r) << 16) | (quantize_byte(a[j].w, r) << 24))
+                                     : 0u;
+      *(uint32_t *)(qs + 4 * v) = word;  // byte k at k: [kt][group][16] is k's natural order for one row
+    }
+  }
+  __syncthreads();
+  // 4. MFMA: lanes of row 0 (lane % 16 == 0) carry the row, the others zeros
+  const bool has_row = (lane & 15) == 0;
+  hb_i32x4 acc = {0, 0, 0, 0};
+#pragma unroll
+  for (int i = 0; i < VW; ++i) {
+    const int kt = wave * VW + i;
+    if (kt < kc) {
+      const hb_i32x4 av = has_row ? *(const hb_i32x4 *)(qs + kt * kKStep + (lane >> 4) * 16) : hb_i32x4{0, 0, 0, 0};
+      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b[i], acc, 0, 0, 0);
+    }
+  }
+  part[wave][lane] = acc;
+  __syncthreads();
+  if (wave != 0 || lane >= 16) return;
+  int32_t tot = part[0][lane][0];
+#pragma unroll
+  for (int w = 1; w < kFusedWaves; ++w) tot = (int32_t)((uint32_t)tot + (uint32_t)part[w][lane][0]);
+  __builtin_nontemporal_store(epilogue_bits<EPI>(tot, cc, sc, s), (uint32_t *)y + col);
+}
+
+// ---------------------------------------------------------------------------
 // Raw accumulator -> byte-plane export of the CPU-control variant.
 // One thread per output byte position (row, 32-column half, byte in 128).
 // ---------------------------------------------------------------------------
@@ -618,6 +764,23 @@ int launch_gemm(void *y, int ldy, const int8_t *q, const float *scales, const in
 
 bool aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
+// Rows up to which quantization runs one workgroup per row.
+constexpr int kWgRowsMax = 64;
+
+template <int EPI>
+int launch_decode_fused(void *y, const float *x, const float *inv, const int8_t *wpack, const float *sw,
+                        const int32_t *corr, int k, int n, int kp, hipStream_t st) {
+  const dim3 grid(n / 16), block(kFusedThreads);
+  if (kp <= 8 * kFusedThreads) {
+    hipLaunchKernelGGL((w8a8_decode_fused<8, EPI>), grid, block, 0, st, y, x, inv, wpack, sw, corr, k, kp);
+  } else if (kp <= 16 * kFusedThreads) {
+    hipLaunchKernelGGL((w8a8_decode_fused<16, EPI>), grid, block, 0, st, y, x, inv, wpack, sw, corr, k, kp);
+  } else {
+    hipLaunchKernelGGL((w8a8_decode_fused<32, EPI>), grid, block, 0, st, y, x, inv, wpack, sw, corr, k, kp);
+  }
+  return hb_check_launch("w8a8_decode_fused");
+}
+
 }  // namespace
 
 extern "C" {
@@ -680,7 +843,21 @@ int hb_w8a8_quantize(int8_t *d_q, float *d_scales, const float *d_x, const float
   const int kp = (int)kp_of(k);
   const dim3 grid((m + 3) / 4), block(256);
   const bool vec = aligned(d_x, 16) && aligned(d_inv, 16);
-  if (vec && k <= 256 * 2) {
+  // Few rows, or rows too long for one wave's registers: a workgroup per row.
+  if (vec && (m <= kWgRowsMax || k > 256 * 24) && k <= kRowThreads * 4 * 16) {
+    const dim3 rows(m), threads(kRowThreads);
+    if (k <= kRowThreads * 4 * 1) {
+      hipLaunchKernelGGL(w8a8_quant_rows_wg<1>, rows, threads, 0, st, d_q, d_scales, d_x, d_inv, k, kp);
+    } else if (k <= kRowThreads * 4 * 2) {
+      hipLaunchKernelGGL(w8a8_quant_rows_wg<2>, rows, threads, 0, st, d_q, d_scales, d_x, d_inv, k, kp);
+    } else if (k <= kRowThreads * 4 * 4) {
+      hipLaunchKernelGGL(w8a8_quant_rows_wg<4>, rows, threads, 0, st, d_q, d_scales, d_x, d_inv, k, kp);
+    } else if (k <= kRowThreads * 4 * 8) {
+      hipLaunchKernelGGL(w8a8_quant_rows_wg<8>, rows, threads, 0, st, d_q, d_scales, d_x, d_inv, k, kp);
+    } else {
+      hipLaunchKernelGGL(w8a8_quant_rows_wg<16>, rows, threads, 0, st, d_q, d_scales, d_x, d_inv, k, kp);
+    }
+  } else if (vec && k <= 256 * 2) {
     hipLaunchKernelGGL(w8a8_quant_rows_reg<2>, grid, block, 0, st, d_q, d_scales, d_x, d_inv, m, k, kp);
   } else if (vec && k <= 256 * 6) {
     hipLaunchKernelGGL(w8a8_quant_rows_reg<6>, grid, block, 0, st, d_q, d_scales, d_x, d_inv, m, k, kp);
@@ -728,6 +905,20 @@ int hb_w8a8_linear(float *d_y, const float *d_x, const void *d_packed, int m, in
   int8_t *q = (int8_t *)d_workspace;
   float *scales = (float *)((uint8_t *)d_workspace + hb_round_up(mp_of(m) * kp_of(k), 256));
   const float *inv = (const float *)((const uint8_t *)d_packed + hb_w8a8_packed_offset(k, n, HB_W8A8_INV));
+  // One row: quantization fused into the weight-streaming kernel.
+  const int kp = (int)kp_of(k);
+  if (m == 1 && kp <= 32 * kFusedThreads && k >= 32 && k % 32 == 0 && n >= 16 && n % 16 == 0 && d_y && d_x &&
+      aligned(d_x, 16) && (epilogue == HB_W8A8_EPI_SCALE || epilogue == HB_W8A8_EPI_SCALE_GELU)) {
+    if (!aligned(d_packed, 256)) return hb_invalid("hb_w8a8_linear alignment");
+    const uint8_t *base = (const uint8_t *)d_packed;
+    const int8_t *wpack = (const int8_t *)(base + hb_w8a8_packed_offset(k, n, HB_W8A8_WEIGHTS));
+    const float *sw = (const float *)(base + hb_w8a8_packed_offset(k, n, HB_W8A8_SW));
+    const int32_t *delta = (const int32_t *)(base + hb_w8a8_packed_offset(k, n, HB_W8A8_DELTA));
+    hipStream_t st = hb_resolve_stream(s);
+    return epilogue == HB_W8A8_EPI_SCALE
+               ? launch_decode_fused<HB_W8A8_EPI_SCALE>(d_y, d_x, inv, wpack, sw, delta, k, n, kp, st)
+               : launch_decode_fused<HB_W8A8_EPI_SCALE_GELU>(d_y, d_x, inv, wpack, sw, delta, k, n, kp, st);
+  }
   int rc = hb_w8a8_quantize(q, scales, d_x, inv, m, k, s);
   if (rc) return rc;
   return hb_w8a8_gemm(d_y, n, q, scales, d_packed, m, k, n, epilogue, s);

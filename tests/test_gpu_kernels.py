@@ -37,7 +37,11 @@ def upload_blob(hip, blob):
 
 
 @pytest.mark.parametrize("m,k,inv_kind", [(77, 768, "ones"), (77, 768, "uniform"), (1, 96, "ones"), (5, 32, "uniform"),
-                                          (33, 6144, "uniform"), (4, 14336, "ones"), (130, 1536, "uniform")])
+                                          (33, 6144, "uniform"), (4, 14336, "ones"), (130, 1536, "uniform"),
+                                          # one workgroup per row: few rows (<= 64) or rows past 6144
+                                          (64, 1536, "uniform"), (65, 1536, "uniform"), (2, 2080, "uniform"),
+                                          (3, 8192, "uniform"), (1, 16416, "ones"), (70, 14336, "uniform"),
+                                          (2, 32768, "uniform")])
 def test_quantize_bit_exact(hip, orc, m, k, inv_kind):
     x, _, blob = make_w8a8(orc, m, k, 64, seed=m + k, inv_kind=inv_kind)
     x[0, :] = 0.0  # zero row: s = 1e-12, u = 128
@@ -151,7 +155,53 @@ def test_w8a8_every_tile_shape_bit_exact(hip, orc, tile, m, k, n):
     np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
 
 
-@pytest.mark.parametrize("m,k,n", [(77, 768, 3072), (4, 1536, 1024), (1000, 96, 4096)])
+# One row: hb_w8a8_linear quantizes inside the weight-streaming kernel
+# (one variant per kp range: <= 4096, <= 8192, <= 16384).
+DECODE_FUSED_SHAPES = [
+    (1, 32, 64),       # smallest K (k % 64 == 32)
+    (1, 4096, 14336),  # BASELINE decode gate/up shape
+    (1, 14336, 4096),  # BASELINE decode down shape
+    (1, 4160, 256),    # just past the first variant
+    (1, 8192, 512),
+    (1, 16384, 128),
+    (1, 1568, 1024),   # k % 64 == 32 with clamped tail tiles
+]
+
+
+@pytest.mark.parametrize("m,k,n", DECODE_FUSED_SHAPES)
+def test_w8a8_decode_fused_bit_exact(hip, orc, m, k, n):
+    x, _, blob = make_w8a8(orc, m, k, n, seed=k + n, inv_kind="uniform", sums_kind="random", outliers=0.01,
+                           scale_lo=5e-5, scale_hi=5e-4)
+    packed = hip.w8a8_prepack(upload_blob(hip, blob), k, n)
+    xd = hip.DeviceBuffer.from_array(x)
+    ws = hip.DeviceBuffer(hip.w8a8_workspace_bytes(m, k))
+    y = hip.DeviceBuffer(m * n * 4)
+    hip.w8a8_linear(y, xd, packed, m, k, n, ws)
+    hip.sync()
+    ref = orc.linear(x, blob, k, n)
+    np.testing.assert_array_equal(y.read(np.uint32, m * n).reshape(m, n), ref.view(np.uint32))
+
+
+def test_w8a8_decode_fused_special_rows(hip, orc):
+    """Zero row (s = 1e-12, u = 128), a row whose absmax is exactly 127
+    (s = 1, so u = rint(t + 128)), and halves that round to even."""
+    k, n = 256, 128
+    _, _, blob = make_w8a8(orc, 1, k, n, seed=17, sums_kind="random")
+    packed = hip.w8a8_prepack(upload_blob(hip, blob), k, n)
+    ws = hip.DeviceBuffer(hip.w8a8_workspace_bytes(1, k))
+    rows = [np.zeros(k, np.float32),
+            np.linspace(-127.0, 127.0, k, dtype=np.float32),
+            np.where(np.arange(k) % 3 == 0, 0.5, np.where(np.arange(k) % 3 == 1, 1.5, 2.5)).astype(np.float32)]
+    rows[2][0] = 127.0
+    for row in rows:
+        x = row.reshape(1, k)
+        y = hip.DeviceBuffer(n * 4)
+        hip.w8a8_linear(y, hip.DeviceBuffer.from_array(x), packed, 1, k, n, ws)
+        hip.sync()
+        np.testing.assert_array_equal(y.read(np.uint32, n), orc.linear(x, blob, k, n).view(np.uint32).ravel())
+
+
+@pytest.mark.parametrize("m,k,n", [(77, 768, 3072), (4, 1536, 1024), (1000, 96, 4096), (1, 4096, 2048)])
 def test_w8a8_gelu_epilogue(hip, orc, m, k, n):
     x, _, blob = make_w8a8(orc, m, k, n, seed=11, scale_lo=1e-3, scale_hi=1e-2)
     packed = hip.w8a8_prepack(upload_blob(hip, blob), k, n)
