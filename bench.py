@@ -267,6 +267,62 @@ def all_configs(steps, warmup):
     for m in (1, 4, 16):
         for k, n in ((4096, 14336), (14336, 4096)):
             out[f"C5_M{m}_{k}x{n}"] = decode_case(m, k, n, steps, warmup, 6)
+    out["C2_f16_text_mlp_77x768x3072x768"] = f16_mlp_case(steps, warmup)
+    return out
+
+
+def f16_mlp_case(steps, warmup, m=77, k=768, n=3072, rotate=6):
+    """opcode-16 F16 GEMM 77x768 -> 3072 with bias +
+    QuickGELU, then 3072 -> 768 with bias (text-encoder MLP block); FP32
+    activations, FP16 weights prepacked once, HBM-resident.  Each layer's
+    graph-replayed mean is reported with its algorithmic bytes
+    (4MK + 2NK + 4N + 4MN) and flops (2MNK)."""
+    lib = hip.lib()
+    stream = hip.default_stream()
+    rng = np.random.default_rng(2)
+    layers = []
+    for (kk, nn, mode) in ((k, n, 2), (n, k, 0)):
+        sets = []
+        for _ in range(rotate):
+            w = (rng.standard_normal((kk, nn), dtype=np.float32) * 0.02).astype(np.float16)
+            perm = hip.permute_f16(w.view(np.uint16))
+            pd = hip.DeviceBuffer.from_array(perm)
+            packed = hip.f16_prepack(pd, kk, nn)
+            pd.free()
+            bias = hip.DeviceBuffer.from_array((rng.standard_normal(nn, dtype=np.float32) * 0.02))
+            sets.append((packed, bias))
+        layers.append((kk, nn, mode, sets))
+    x = hip.DeviceBuffer.from_array(rng.standard_normal((m, k), dtype=np.float32))
+    h = hip.DeviceBuffer(m * n * 4)
+    y = hip.DeviceBuffer(m * k * 4)
+    ios = [(x, h), (h, y)]
+    out = {}
+    for li, (kk, nn, mode, sets) in enumerate(layers):
+        src, dst = ios[li]
+        ws = hip.DeviceBuffer(max(hip.f16_workspace_bytes(m, kk, nn), 256))
+
+        def launch(i):
+            packed, bias = sets[i % rotate]
+            hip.check(lib.hb_f16_gemm_ws(dst.ptr, src.ptr, packed.ptr, bias.ptr, m, kk, nn, nn, mode, ws.ptr,
+                                         ws.nbytes, stream), "hb_f16_gemm_ws")
+
+        for i in range(max(warmup, 1)):
+            launch(i)
+        with hip.Graph.capture(stream) as g:
+            for i in range(steps):
+                launch(i)
+        a, b = hip.Event(), hip.Event()
+        hip.check(lib.hb_stream_sync(stream), "sync")
+        a.record(stream)
+        g.launch(stream)
+        b.record(stream)
+        hip.check(lib.hb_stream_sync(stream), "sync")
+        us = a.elapsed_ms(b) * 1e3 / steps
+        nbytes = 4 * m * kk + 2 * nn * kk + 4 * nn + 4 * m * nn
+        out["layer1_quickgelu" if li == 0 else "layer2_bias"] = {
+            "shape": f"M={m} K={kk} N={nn} mode={mode}", "us": round(us, 3),
+            "tflops": round(2 * m * nn * kk / us * 1e-6, 2), "gbps": round(nbytes / us * 1e-3, 1),
+            "frac_hbm": round(nbytes / us * 1e-3 / PEAK_HBM_GBPS, 4)}
     return out
 
 

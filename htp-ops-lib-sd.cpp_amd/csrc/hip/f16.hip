@@ -200,7 +200,173 @@ __global__ __launch_bounds__(64 * WM *WN) void f16_gemm_tiles(float *__restrict_
   }
 }
 
+// ---------------------------------------------------------------------------
+// Few rows (m <= 128): split-K.  Workgroup (g, s) computes all rows x 32
+// columns (col-group g) over the s-th range of 32-k blocks; its 4 waves take
+// the range's blocks round robin and are summed in LDS in wave order, then
+// the partial tile goes to workspace slice s.  A second kernel sums the
+// slices in order (so results do not depend on scheduling), rounds to fp16
+// (the readout step) and applies bias and activation.  Operands are read
+// straight from memory in MFMA lane order: W from the packed image (one 1 KB
+// tile per 16 columns x 32 k), A as 8 fp32 per lane converted to fp16 (RNE).
+// ---------------------------------------------------------------------------
+
+constexpr int kSkinnyWaves = 4;
+
+// RF row fragments (16 rows each) x CF column fragments per workgroup; each
+// wave owns KPW consecutive 32-k blocks of the split, whose operands it
+// requests all at once before the first MFMA.
+template <int RF, int CF, int KPW>
+__global__ __launch_bounds__(64 * kSkinnyWaves) void f16_skinny_partial(float *__restrict__ ws,
+                                                                        const float *__restrict__ x,
+                                                                        const uint16_t *__restrict__ packed, int m,
+                                                                        int k, int n) {
+  __shared__ hb_f32x4 red[kSkinnyWaves - 1][RF * CF][64];
+  const int g = blockIdx.x, s = blockIdx.y;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int kblocks = k / 32;
+  const int kb0 = (s * kSkinnyWaves + wave) * KPW;
+  // operands (block indices clamped into range; blocks past the end are not multiplied)
+  hb_f16x8 b[KPW][CF];
+  float4 alo[KPW][RF], ahi[KPW][RF];
+#pragma unroll
+  for (int t = 0; t < KPW; ++t) {
+    const int kb = min(kb0 + t, kblocks - 1);
+#pragma unroll
+    for (int j = 0; j < CF; ++j)
+      b[t][j] = *(const hb_f16x8 *)(packed + ((size_t)(g * CF + j) * kblocks + kb) * 512u + lane * 8);
+#pragma unroll
+    for (int i = 0; i < RF; ++i) {
+      const float *xr = x + (size_t)min(16 * i + (lane & 15), m - 1) * k + kb * 32 + 8 * (lane >> 4);
+      alo[t][i] = *(const float4 *)xr;
+      ahi[t][i] = *(const float4 *)(xr + 4);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);  // every load is in flight before the first use
+  hb_f32x4 acc[RF][CF];
+#pragma unroll
+  for (int i = 0; i < RF; ++i)
+#pragma unroll
+    for (int j = 0; j < CF; ++j) acc[i][j] = hb_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int t = 0; t < KPW; ++t) {
+    if (kb0 + t < kblocks) {
+#pragma unroll
+      for (int i = 0; i < RF; ++i) {
+        const hb_f16x8 a = {(_Float16)alo[t][i].x, (_Float16)alo[t][i].y, (_Float16)alo[t][i].z,
+                            (_Float16)alo[t][i].w, (_Float16)ahi[t][i].x, (_Float16)ahi[t][i].y,
+                            (_Float16)ahi[t][i].z, (_Float16)ahi[t][i].w};
+        // W as the A operand: lane l holds 4 consecutive columns of row l % 16
+#pragma unroll
+        for (int j = 0; j < CF; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(b[t][j], a, acc[i][j], 0, 0, 0);
+      }
+    }
+  }
+  if (wave != 0) {
+#pragma unroll
+    for (int i = 0; i < RF; ++i)
+#pragma unroll
+      for (int j = 0; j < CF; ++j) red[wave - 1][i * CF + j][lane] = acc[i][j];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  // 16-byte stores through a buffer resource covering the slice: rows past
+  // mp fall outside it and are dropped by the hardware (no branches)
+  const int mp = (m + 15) / 16 * 16;
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(ws + (size_t)s * mp * n, 0, mp * n * 4, 0x00020000);
+#pragma unroll
+  for (int i = 0; i < RF; ++i) {
+#pragma unroll
+    for (int j = 0; j < CF; ++j) {
+      hb_f32x4 t = acc[i][j];
+#pragma unroll
+      for (int w = 1; w < kSkinnyWaves; ++w) t += red[w - 1][i * CF + j][lane];
+      const int row = 16 * i + (lane & 15), col = (g * CF + j) * 16 + 4 * (lane >> 4);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(hb_u32x4, t), rs, (uint32_t)(row * n + col) * 4u, 0,
+                                             0);
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void f16_skinny_epilogue(float *__restrict__ y, const float *__restrict__ ws,
+                                                          const float *__restrict__ bias, int m, int n,
+                                                          int channels, int mode, int splits) {
+  const int limit = mode == 3 ? channels : n;
+  const size_t total = (size_t)m * limit;
+  const int mp = (m + 15) / 16 * 16;
+  for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += (size_t)gridDim.x * blockDim.x) {
+    const int row = (int)(idx / (size_t)limit), col = (int)(idx % (size_t)limit);
+    // slices are summed in order; loads go out eight at a time
+    const float *p = ws + (size_t)row * n + col;
+    const size_t slice = (size_t)mp * n;
+    float acc = 0.0f;
+    for (int s0 = 0; s0 < splits; s0 += 8) {
+      float v8[8];
+#pragma unroll
+      for (int t = 0; t < 8; ++t) v8[t] = p[(size_t)min(s0 + t, splits - 1) * slice];
+#pragma unroll
+      for (int t = 0; t < 8; ++t)
+        if (s0 + t < splits) acc += v8[t];
+    }
+    const float v = (float)(_Float16)acc;
+    const float z = bias ? __fadd_rn(v, bias[col]) : v;
+    if (mode == 3) {
+      y[(size_t)col * m + row] = z;
+    } else {
+      y[(size_t)row * n + col] = apply_mode(z, mode);
+    }
+  }
+}
+
 bool aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+int compute_units() {
+  int dev = 0, v = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      v <= 0)
+    v = 256;
+  return v;
+}
+
+// Columns per workgroup, split count and blocks per split for the few-rows
+// path: 64 columns when n allows (each A element is then re-read by a
+// quarter as many workgroups), about one workgroup per CU, at least 4
+// k-blocks (one per wave) per split.
+int skinny_cols(int n) { return n % 64 == 0 ? 64 : 32; }
+
+// k-blocks per wave: two when the k-blocks cover at least one workgroup per
+// CU that way, else one.
+void skinny_plan(int k, int n, int &splits, int &kpw) {
+  const int kblocks = k / 32, groups = n / skinny_cols(n);
+  const int per_wg2 = kSkinnyWaves * 2;
+  kpw = (long long)groups * ((kblocks + per_wg2 - 1) / per_wg2) >= compute_units() ? 2 : 1;
+  const int per_wg = kSkinnyWaves * kpw;
+  splits = (kblocks + per_wg - 1) / per_wg;
+}
+
+template <int CF, int KPW>
+void launch_skinny_k(int rf, dim3 grid, dim3 block, hipStream_t st, float *ws, const float *x, const uint16_t *packed,
+                     int m, int k, int n) {
+  if (rf <= 1) {
+    hipLaunchKernelGGL((f16_skinny_partial<1, CF, KPW>), grid, block, 0, st, ws, x, packed, m, k, n);
+  } else if (rf <= 2) {
+    hipLaunchKernelGGL((f16_skinny_partial<2, CF, KPW>), grid, block, 0, st, ws, x, packed, m, k, n);
+  } else if (rf <= 4) {
+    hipLaunchKernelGGL((f16_skinny_partial<4, CF, KPW>), grid, block, 0, st, ws, x, packed, m, k, n);
+  } else if (rf <= 6) {
+    hipLaunchKernelGGL((f16_skinny_partial<6, CF, KPW>), grid, block, 0, st, ws, x, packed, m, k, n);
+  } else {
+    hipLaunchKernelGGL((f16_skinny_partial<8, CF, KPW>), grid, block, 0, st, ws, x, packed, m, k, n);
+  }
+}
+
+template <int CF>
+void launch_skinny(int rf, int kpw, dim3 grid, dim3 block, hipStream_t st, float *ws, const float *x,
+                   const uint16_t *packed, int m, int k, int n) {
+  if (kpw == 2) launch_skinny_k<CF, 2>(rf, grid, block, st, ws, x, packed, m, k, n);
+  else launch_skinny_k<CF, 1>(rf, grid, block, st, ws, x, packed, m, k, n);
+}
 
 }  // namespace
 
@@ -222,8 +388,15 @@ int hb_f16_prepack(uint16_t *d_packed, const uint16_t *d_permuted, int k, int n,
   return hb_check_launch("f16_prepack");
 }
 
-int hb_f16_gemm(float *d_y, const float *d_x, const uint16_t *d_packed, const float *d_bias, int m, int k, int n,
-                int channels, int mode, hb_stream s) {
+size_t hb_f16_workspace_bytes(int m, int k, int n) {
+  if (m < 1 || m > 128 || k < 32 || n < 32) return 0;
+  // splits <= ceil(kblocks / 4) (one k-block per wave at the least)
+  const int max_splits = (k / 32 + kSkinnyWaves - 1) / kSkinnyWaves;
+  return (size_t)max_splits * (size_t)((m + 15) / 16 * 16) * (size_t)n * 4u;
+}
+
+int hb_f16_gemm_ws(float *d_y, const float *d_x, const uint16_t *d_packed, const float *d_bias, int m, int k, int n,
+                   int channels, int mode, void *d_workspace, size_t workspace_bytes, hb_stream s) {
   if (!d_y || !d_x || !d_packed) return hb_invalid("hb_f16_gemm null pointer");
   if (m < 1 || k < 32 || k % 32 || n < 32 || n % 32 || channels < 1 || channels > n || mode < 0 || mode > 3 ||
       (mode != 3 && channels != n))
@@ -231,6 +404,26 @@ int hb_f16_gemm(float *d_y, const float *d_x, const uint16_t *d_packed, const fl
   if (!aligned(d_x, 16) || !aligned(d_packed, 16) || !aligned(d_y, 4) || (d_bias && !aligned(d_bias, 4)))
     return hb_invalid("hb_f16_gemm alignment");
   hipStream_t st = hb_resolve_stream(s);
+  const size_t need = hb_f16_workspace_bytes(m, k, n);
+  const long long tiled_wgs = ((m + 31) / 32) * (long long)((n + 31) / 32);
+  if (d_workspace && need && workspace_bytes >= need && aligned(d_workspace, 16) &&
+      tiled_wgs < compute_units()) {
+    int splits = 1, kpw = 1;
+    skinny_plan(k, n, splits, kpw);
+    const int cols = skinny_cols(n);
+    const dim3 grid(n / cols, splits), block(64 * kSkinnyWaves);
+    float *ws = (float *)d_workspace;
+    const int rf = (m + 15) / 16;
+    if (cols == 64) launch_skinny<4>(rf, kpw, grid, block, st, ws, d_x, d_packed, m, k, n);
+    else launch_skinny<2>(rf, kpw, grid, block, st, ws, d_x, d_packed, m, k, n);
+    int rc = hb_check_launch("f16_skinny_partial");
+    if (rc) return rc;
+    const size_t outs = (size_t)m * (size_t)(mode == 3 ? channels : n);
+    const int eg = (int)((outs + 255) / 256 < 4096 ? (outs + 255) / 256 : 4096);
+    hipLaunchKernelGGL(f16_skinny_epilogue, dim3(eg), dim3(256), 0, st, d_y, ws, d_bias, m, n, channels, mode,
+                       splits);
+    return hb_check_launch("f16_skinny_epilogue");
+  }
   const long long big = ((m + 127) / 128) * (long long)((n + 127) / 128);
   const long long mid = ((m + 63) / 64) * (long long)((n + 63) / 64);
   if (big >= 256) {
@@ -245,6 +438,11 @@ int hb_f16_gemm(float *d_y, const float *d_x, const uint16_t *d_packed, const fl
                        k, n, channels, mode);
   }
   return hb_check_launch("f16_gemm_tiles");
+}
+
+int hb_f16_gemm(float *d_y, const float *d_x, const uint16_t *d_packed, const float *d_bias, int m, int k, int n,
+                int channels, int mode, hb_stream s) {
+  return hb_f16_gemm_ws(d_y, d_x, d_packed, d_bias, m, k, n, channels, mode, nullptr, 0, s);
 }
 
 }  // extern "C"

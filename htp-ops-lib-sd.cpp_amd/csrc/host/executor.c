@@ -28,8 +28,11 @@
 #define QTIMER_HZ 19200000.0
 
 static pthread_mutex_t g_exec_lock = PTHREAD_MUTEX_INITIALIZER;
-static void *g_scratch[4];
-static size_t g_scratch_size[4];
+/* Device scratch slots: 0 W8A8 workspace, 1 raw accumulators or a realigned
+ * bias, 2 realigned activations, 3 realigned output, 4 F16 split-K partials. */
+enum { kScratchSlots = 5 };
+static void *g_scratch[kScratchSlots];
+static size_t g_scratch_size[kScratchSlots];
 static __thread int t_device_ready = 0;
 
 int htp_executor_ensure_device(void) {
@@ -43,7 +46,7 @@ int htp_executor_ensure_device(void) {
 hb_stream htp_executor_stream(void) { return hb_default_stream(); }
 
 void *htp_executor_scratch(int slot, size_t bytes) {
-  if (slot < 0 || slot >= 4) return NULL;
+  if (slot < 0 || slot >= kScratchSlots) return NULL;
   if (bytes == 0) bytes = 256;
   if (g_scratch_size[slot] < bytes) {
     if (g_scratch[slot]) hb_free(g_scratch[slot]);
@@ -338,8 +341,15 @@ static int run_f16(htp_view *out, htp_view *act, htp_view *wgt, htp_view *bias, 
     events_close(&ev);
     return -5;
   }
+  /* Few rows: the split-K path, with its partial sums in executor scratch. */
+  const size_t ws_bytes = hb_f16_workspace_bytes(m, k, n);
+  void *ws = ws_bytes ? htp_executor_scratch(4, ws_bytes) : NULL;
+  if (ws_bytes && !ws) {
+    events_close(&ev);
+    return -5;
+  }
   int hrc = hb_event_record(ev.e[0], s);
-  if (!hrc) hrc = hb_f16_gemm(y, x, (const uint16_t *)packed, b, m, k, n, channels, mode, s);
+  if (!hrc) hrc = hb_f16_gemm_ws(y, x, (const uint16_t *)packed, b, m, k, n, channels, mode, ws, ws_bytes, s);
   if (!hrc) hrc = hb_event_record(ev.e[1], s);
   if (!hrc && (void *)y != (void *)out->dev) hrc = hb_memcpy_d2d(out->dev, y, out_bytes, s);
   if (!hrc) hrc = hb_stream_sync(s);

@@ -75,6 +75,9 @@ _SIGNATURES = {
     "hb_f16_prepack": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
     "hb_f16_gemm": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int,
                              _c_void_p]),
+    "hb_f16_workspace_bytes": (_c_size_t, [_c_int, _c_int, _c_int]),
+    "hb_f16_gemm_ws": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                _c_void_p, _c_size_t, _c_void_p]),
 }
 
 # Host-library symbols (session, executor, registry); bound when present.
@@ -325,9 +328,19 @@ def f16_prepack(permuted_dev, k, n):
     return packed
 
 
-def f16_gemm(y_dev, x_dev, packed, bias_dev, m, k, n, channels, mode, stream=None):
-    check(lib().hb_f16_gemm(y_dev.ptr, x_dev.ptr, packed.ptr, bias_dev.ptr if bias_dev else None, m, k, n,
-                            channels, mode, stream), "hb_f16_gemm")
+def f16_workspace_bytes(m, k, n):
+    return lib().hb_f16_workspace_bytes(m, k, n)
+
+
+def f16_gemm(y_dev, x_dev, packed, bias_dev, m, k, n, channels, mode, stream=None, workspace=None):
+    """hb_f16_gemm, or hb_f16_gemm_ws when a workspace buffer is given (the
+    split-K path for m <= 128)."""
+    if workspace is None:
+        check(lib().hb_f16_gemm(y_dev.ptr, x_dev.ptr, packed.ptr, bias_dev.ptr if bias_dev else None, m, k, n,
+                                channels, mode, stream), "hb_f16_gemm")
+    else:
+        check(lib().hb_f16_gemm_ws(y_dev.ptr, x_dev.ptr, packed.ptr, bias_dev.ptr if bias_dev else None, m, k, n,
+                                   channels, mode, workspace.ptr, workspace.nbytes, stream), "hb_f16_gemm_ws")
 
 
 # ---- events ----------------------------------------------------------------

@@ -146,6 +146,18 @@ int hb_f16_prepack(uint16_t *d_packed, const uint16_t *d_permuted, int k, int n,
 int hb_f16_gemm(float *d_y, const float *d_x, const uint16_t *d_packed, const float *d_bias, int m, int k, int n,
                 int channels, int mode, hb_stream s);
 
+/* Workspace for the few-rows (m <= 128) split-K path of hb_f16_gemm_ws; 0
+ * when the shape takes the tiled path (no workspace needed). */
+size_t hb_f16_workspace_bytes(int m, int k, int n);
+
+/* hb_f16_gemm with a workspace: for m <= 128, a workspace of at least
+ * hb_f16_workspace_bytes, and a shape whose 32x32 output tiles number fewer
+ * than the device's CUs, K is split across workgroups and the partial sums
+ * are added in a fixed order before the fp16 readout rounding and the
+ * epilogue (two kernels); otherwise identical to hb_f16_gemm. */
+int hb_f16_gemm_ws(float *d_y, const float *d_x, const uint16_t *d_packed, const float *d_bias, int m, int k, int n,
+                   int channels, int mode, void *d_workspace, size_t workspace_bytes, hb_stream s);
+
 #ifdef __cplusplus
 }
 #endif

@@ -247,8 +247,17 @@ def f16_case(orc, m, k, n, seed, bias=True):
     (300, 256, 512, 3, 480, True),    # channel-major store, channels < n
     (1024, 256, 4096, 0, 4096, True), # 128x128 tiles
     (1, 128, 32, 2, 32, True),
+    (128, 3072, 768, 3, 704, True),   # eight row fragments, channel-major, split-K
+    (17, 1024, 96, 1, 96, False),     # two row fragments, a single split
+    (48, 4096, 2048, 2, 2048, True),  # three row fragments -> four-fragment variant
 ])
-def test_f16_gemm_epilogue(hip, orc, m, k, n, mode, channels, bias):
+@pytest.mark.parametrize("split_k", [False, True])
+def test_f16_gemm_epilogue(hip, orc, m, k, n, mode, channels, bias, split_k):
+    """Tiled path, and (split_k) the few-rows split-K path of hb_f16_gemm_ws
+    where the shape allows it (m <= 128)."""
+    ws_bytes = hip.f16_workspace_bytes(m, k, n)
+    if split_k and not ws_bytes:
+        pytest.skip("m > 128: hb_f16_gemm_ws takes the tiled path")
     x, w, perm, b = f16_case(orc, m, k, n, seed=m + n + mode, bias=bias)
     permd = hip.DeviceBuffer.from_array(perm)
     packed = hip.f16_prepack(permd, k, n)
@@ -256,7 +265,8 @@ def test_f16_gemm_epilogue(hip, orc, m, k, n, mode, channels, bias):
     bd = hip.DeviceBuffer.from_array(b[:channels] if b is not None else np.zeros(1, np.float32)) if bias else None
     out_elems = m * (channels if mode == 3 else n)
     y = hip.DeviceBuffer(out_elems * 4)
-    hip.f16_gemm(y, xd, packed, bd, m, k, n, channels, mode)
+    ws = hip.DeviceBuffer(ws_bytes) if split_k else None
+    hip.f16_gemm(y, xd, packed, bd, m, k, n, channels, mode, workspace=ws)
     hip.sync()
     got = y.read(np.float32, out_elems)
     ref = orc.f16_gemm_epilogue(x, perm, None if b is None else b[:channels].copy() if mode == 3 else b, m, k, n,
