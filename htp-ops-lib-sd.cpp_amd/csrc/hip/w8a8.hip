@@ -84,7 +84,9 @@ __global__ __launch_bounds__(256) void w8a8_prepack_columns(float *__restrict__ 
 }
 
 // ---------------------------------------------------------------------------
-// Activation quantization: one wave per row, four rows per workgroup.
+// Activation quantization: blocks of 8 or 16 rows (a wave per row) for many
+// rows, a workgroup per row for few or long rows, a two-pass fallback for
+// unaligned rows.
 // ---------------------------------------------------------------------------
 
 __device__ inline float wave_max(float v) {
@@ -113,52 +115,6 @@ __device__ inline uint32_t *q_word(int8_t *q, int kp, int row, int k) {
   return (uint32_t *)(q + off);
 }
 
-// NV float4 vectors per lane stay in registers (row length k <= 256*NV).
-template <int NV>
-__global__ __launch_bounds__(256) void w8a8_quant_rows_reg(int8_t *__restrict__ q, float *__restrict__ scales,
-                                                          const float *__restrict__ x,
-                                                          const float *__restrict__ inv, int m, int k, int kp) {
-  const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= m) return;
-  const float4 *xr = (const float4 *)(x + (size_t)row * k);
-  const float4 *iv = (const float4 *)inv;
-  const int nvec = k / 4;
-  // Loads are unconditional (index clamped into the row) so all 2*NV of them
-  // issue back to back; lanes past the row end contribute nothing.
-  float4 a[NV], b[NV];
-#pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    const int idx = min(lane + 64 * j, nvec - 1);
-    a[j] = xr[idx];
-    b[j] = iv[idx];
-  }
-  float4 t[NV];
-  float amax = 0.0f;
-#pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    t[j] = make_float4(__fmul_rn(a[j].x, b[j].x), __fmul_rn(a[j].y, b[j].y), __fmul_rn(a[j].z, b[j].z),
-                       __fmul_rn(a[j].w, b[j].w));
-    if (lane + 64 * j < nvec)
-      amax = fmaxf(amax, fmaxf(fmaxf(fabsf(t[j].x), fabsf(t[j].y)), fmaxf(fabsf(t[j].z), fabsf(t[j].w))));
-  }
-  amax = wave_max(amax);
-  const float s = fmaxf(__fdiv_rn(amax, 127.0f), 1e-12f);
-  const float r = __fdiv_rn(1.0f, s);
-  if (lane == 0) scales[row] = s;
-  const int qvec = kp / 4;
-#pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    const int idx = lane + 64 * j;
-    if (idx < nvec) {
-      *q_word(q, kp, row, 4 * idx) = quantize_byte(t[j].x, r) | (quantize_byte(t[j].y, r) << 8) |
-                                    (quantize_byte(t[j].z, r) << 16) | (quantize_byte(t[j].w, r) << 24);
-    } else if (idx < qvec) {
-      *q_word(q, kp, row, 4 * idx) = 0u;
-    }
-  }
-}
-
 // Any row length and 4-byte aligned pointers: two passes over the row
 // (the second pass re-reads x from cache and recomputes the same t).
 __global__ __launch_bounds__(256) void w8a8_quant_rows_any(int8_t *__restrict__ q, float *__restrict__ scales,
@@ -181,6 +137,67 @@ __global__ __launch_bounds__(256) void w8a8_quant_rows_any(int8_t *__restrict__ 
       for (int e = 0; e < 4; ++e) word |= quantize_byte(__fmul_rn(xr[i + e], inv[i + e]), r) << (8 * e);
     }
     *q_word(q, kp, row, i) = word;
+  }
+}
+
+// Many rows: one workgroup per block of ROWS rows (8 or 16), one wave per
+// row with its NV float4 per lane in registers.  The block's quantized bytes
+// are assembled in LDS and written out as whole 128-byte lines (a tile holds
+// 16 rows x 64 k; rows r..r+7 of one 16-k group are 128 contiguous bytes), so
+// no output line is shared between workgroups.  Rows past m inside the block
+// are written as zeros.
+template <int NV, int ROWS>
+__global__ __launch_bounds__(64 * ROWS) void w8a8_quant_block(int8_t *__restrict__ q, float *__restrict__ scales,
+                                                              const float *__restrict__ x,
+                                                              const float *__restrict__ inv, int m, int k, int kp) {
+  static_assert(ROWS == 8 || ROWS == 16, "a block is half or all of a tile's rows");
+  extern __shared__ uint4 stage[];  // ROWS * kp bytes: [tile][16-k group][row][16 bytes]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int row0 = blockIdx.x * ROWS, row = row0 + wave;
+  const bool live = row < m;
+  const int nvec = k / 4;
+  // x is read once (non-temporal loads keep it from displacing the smoothing
+  // vector and the quantized output in the caches); inv is shared by all rows.
+  const hb_f32x4 *xr = (const hb_f32x4 *)(x + (size_t)min(row, m - 1) * k);
+  const float4 *iv = (const float4 *)inv;
+  float4 a[NV], b[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int idx = min(lane + 64 * j, nvec - 1);
+    const hb_f32x4 v = __builtin_nontemporal_load(xr + idx);
+    a[j] = make_float4(v.x, v.y, v.z, v.w);
+    b[j] = iv[idx];
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    a[j] = make_float4(__fmul_rn(a[j].x, b[j].x), __fmul_rn(a[j].y, b[j].y), __fmul_rn(a[j].z, b[j].z),
+                       __fmul_rn(a[j].w, b[j].w));
+    if (lane + 64 * j < nvec)
+      amax = fmaxf(amax, fmaxf(fmaxf(fabsf(a[j].x), fabsf(a[j].y)), fmaxf(fabsf(a[j].z), fabsf(a[j].w))));
+  }
+  amax = wave_max(amax);
+  const float s = fmaxf(__fdiv_rn(amax, 127.0f), 1e-12f);
+  const float r = __fdiv_rn(1.0f, s);
+  if (live && lane == 0) scales[row] = s;
+  uint32_t *sw = (uint32_t *)stage;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int idx = lane + 64 * j;
+    if (idx < kp / 4) {
+      const int kk = 4 * idx;
+      const uint32_t word = (live && idx < nvec) ? (quantize_byte(a[j].x, r) | (quantize_byte(a[j].y, r) << 8) |
+                                                    (quantize_byte(a[j].z, r) << 16) | (quantize_byte(a[j].w, r) << 24))
+                                                 : 0u;
+      sw[((kk / kKStep) * 4 * ROWS + ((kk % kKStep) / 16) * ROWS + wave) * 4 + (kk % 16) / 4] = word;
+    }
+  }
+  __syncthreads();
+  // rows row0..row0+ROWS-1 sit at row offset row0 % 16 of tile row row0 / 16
+  int8_t *base = q + (size_t)(row0 / 16) * (size_t)kp * 16u + (size_t)(row0 % 16) * 16u;
+  for (int v = tid; v < ROWS * kp / 16; v += 64 * ROWS) {
+    const int tile = v / (4 * ROWS), g = (v / ROWS) % 4, rr = v % ROWS;
+    *(uint4 *)(base + (size_t)tile * kFragBytes + (size_t)(g * 16 + rr) * 16u) = stage[v];
   }
 }
 
@@ -767,6 +784,14 @@ bool aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
 // Rows up to which quantization runs one workgroup per row.
 constexpr int kWgRowsMax = 64;
 
+template <int NV, int ROWS>
+void launch_quant_block(int8_t *d_q, float *d_scales, const float *d_x, const float *d_inv, int m, int k, int kp,
+                        hipStream_t st) {
+  const dim3 blocks((m + ROWS - 1) / ROWS), threads(64 * ROWS);
+  hipLaunchKernelGGL((w8a8_quant_block<NV, ROWS>), blocks, threads, (size_t)ROWS * (size_t)kp, st, d_q, d_scales, d_x,
+                     d_inv, m, k, kp);
+}
+
 template <int EPI>
 int launch_decode_fused(void *y, const float *x, const float *inv, const int8_t *wpack, const float *sw,
                         const int32_t *corr, int k, int n, int kp, hipStream_t st) {
@@ -843,7 +868,7 @@ int hb_w8a8_quantize(int8_t *d_q, float *d_scales, const float *d_x, const float
   const int kp = (int)kp_of(k);
   const dim3 grid((m + 3) / 4), block(256);
   const bool vec = aligned(d_x, 16) && aligned(d_inv, 16);
-  // Few rows, or rows too long for one wave's registers: a workgroup per row.
+  // Few rows, or rows longer than the block kernel holds: a workgroup per row.
   if (vec && (m <= kWgRowsMax || k > 256 * 24) && k <= kRowThreads * 4 * 16) {
     const dim3 rows(m), threads(kRowThreads);
     if (k <= kRowThreads * 4 * 1) {
@@ -857,14 +882,29 @@ int hb_w8a8_quantize(int8_t *d_q, float *d_scales, const float *d_x, const float
     } else {
       hipLaunchKernelGGL(w8a8_quant_rows_wg<16>, rows, threads, 0, st, d_q, d_scales, d_x, d_inv, k, kp);
     }
-  } else if (vec && k <= 256 * 2) {
-    hipLaunchKernelGGL(w8a8_quant_rows_reg<2>, grid, block, 0, st, d_q, d_scales, d_x, d_inv, m, k, kp);
-  } else if (vec && k <= 256 * 6) {
-    hipLaunchKernelGGL(w8a8_quant_rows_reg<6>, grid, block, 0, st, d_q, d_scales, d_x, d_inv, m, k, kp);
-  } else if (vec && k <= 256 * 16) {
-    hipLaunchKernelGGL(w8a8_quant_rows_reg<16>, grid, block, 0, st, d_q, d_scales, d_x, d_inv, m, k, kp);
   } else if (vec && k <= 256 * 24) {
-    hipLaunchKernelGGL(w8a8_quant_rows_reg<24>, grid, block, 0, st, d_q, d_scales, d_x, d_inv, m, k, kp);
+    // 8-row blocks (a workgroup per 128-byte output line), 16-row blocks
+    // (whole 1 KB tiles) for short rows when there are enough of them; the
+    // staging buffer is ROWS x kp bytes of LDS (at most 48 KB).
+    const bool whole_tiles = m >= 2048;
+    if (k <= 256 * 2) {
+      whole_tiles ? launch_quant_block<2, 16>(d_q, d_scales, d_x, d_inv, m, k, kp, st)
+                  : launch_quant_block<2, 8>(d_q, d_scales, d_x, d_inv, m, k, kp, st);
+    } else if (k <= 256 * 4) {
+      whole_tiles ? launch_quant_block<4, 16>(d_q, d_scales, d_x, d_inv, m, k, kp, st)
+                  : launch_quant_block<4, 8>(d_q, d_scales, d_x, d_inv, m, k, kp, st);
+    } else if (k <= 256 * 6) {
+      whole_tiles ? launch_quant_block<6, 16>(d_q, d_scales, d_x, d_inv, m, k, kp, st)
+                  : launch_quant_block<6, 8>(d_q, d_scales, d_x, d_inv, m, k, kp, st);
+    } else if (k <= 256 * 8) {
+      launch_quant_block<8, 8>(d_q, d_scales, d_x, d_inv, m, k, kp, st);
+    } else if (k <= 256 * 12) {
+      launch_quant_block<12, 8>(d_q, d_scales, d_x, d_inv, m, k, kp, st);
+    } else if (k <= 256 * 16) {
+      launch_quant_block<16, 8>(d_q, d_scales, d_x, d_inv, m, k, kp, st);
+    } else {
+      launch_quant_block<24, 8>(d_q, d_scales, d_x, d_inv, m, k, kp, st);
+    }
   } else {
     hipLaunchKernelGGL(w8a8_quant_rows_any, grid, block, 0, st, d_q, d_scales, d_x, d_inv, m, k, kp);
   }

@@ -41,7 +41,11 @@ def upload_blob(hip, blob):
                                           # one workgroup per row: few rows (<= 64) or rows past 6144
                                           (64, 1536, "uniform"), (65, 1536, "uniform"), (2, 2080, "uniform"),
                                           (3, 8192, "uniform"), (1, 16416, "ones"), (70, 14336, "uniform"),
-                                          (2, 32768, "uniform")])
+                                          (2, 32768, "uniform"),
+                                          # 16-row and 8-row blocks (m > 64, k <= 6144), ragged m and k % 64 == 32
+                                          (100, 480, "uniform"), (97, 1024, "ones"), (72, 2048, "uniform"),
+                                          (81, 3040, "uniform"), (90, 4096, "uniform"), (75, 6144, "uniform"),
+                                          (129, 5152, "uniform")])
 def test_quantize_bit_exact(hip, orc, m, k, inv_kind):
     x, _, blob = make_w8a8(orc, m, k, 64, seed=m + k, inv_kind=inv_kind)
     x[0, :] = 0.0  # zero row: s = 1e-12, u = 128
