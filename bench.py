@@ -45,6 +45,7 @@ METRIC = "W8A8 INT8 TOPS & %MFMA peak (M=4096,K=1536,N=6144); M=1 decode HBM GB/
 PEAK_INT8_TOPS = 5000.0   # MI355X dense INT8 MFMA
 PEAK_HBM_GBPS = 8000.0    # MI355X HBM3E
 HEADLINE = (4096, 1536, 6144)
+SETTLE_MS = 80.0          # untimed GPU time before each timed sequence (clock ramp)
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "w8a8_gemm_tiles_4096x1536x6144_traffic.md")
 COPY_PROBE_BYTES = 256 << 20
 
@@ -88,10 +89,13 @@ class W8A8Set:
 
 
 def run_w8a8(m, k, n, steps, warmup, rotate, outliers=0.0, scale=(1e-4, 1e-3)):
-    """Times `steps` opcode-15 steps replayed from one HIP graph (no host
-    launch cost inside the timed region), then the same number of GEMM-only
-    and quantize-only launches, each from its own graph, for per-kernel
-    averages (HIP events on the library stream that runs the kernels)."""
+    """Times `steps` opcode-15 steps launched in stream order (the library's
+    own launches, as a caller issues them; the host enqueues ahead of the
+    GPU), then the same number of GEMM-only and quantize-only launches, for
+    per-kernel averages (HIP events on the library stream that runs the
+    kernels).  The same three sequences are also replayed from HIP graphs
+    and reported beside them.  Each timed sequence starts after at least
+    SETTLE_MS of untimed load (the GPU clocks ramp over tens of ms)."""
     lib = hip.lib()
     stream = hip.default_stream()
     sets = [W8A8Set(m, k, n, seed, outliers, *scale) for seed in range(rotate)]
@@ -119,7 +123,17 @@ def run_w8a8(m, k, n, steps, warmup, rotate, outliers=0.0, scale=(1e-4, 1e-3)):
         hip.check(lib.hb_stream_sync(stream), "sync")
         hip.sync()
 
-    def timed(graph):
+    def timed_stream(fn, count):
+        a, b = hip.Event(), hip.Event()
+        synced()
+        a.record(stream)
+        for i in range(count):
+            fn(sets[i % rotate])
+        b.record(stream)
+        synced()
+        return a.elapsed_ms(b)
+
+    def timed_graph(graph):
         a, b = hip.Event(), hip.Event()
         synced()
         a.record(stream)
@@ -128,22 +142,38 @@ def run_w8a8(m, k, n, steps, warmup, rotate, outliers=0.0, scale=(1e-4, 1e-3)):
         synced()
         return a.elapsed_ms(b)
 
-    for st in sets:  # eager pass: every set quantized once before graphs reuse q
+    def settle(min_steps):
+        # GPU clocks ramp up over tens of milliseconds of load: run at least
+        # min_steps untimed steps and keep going, 100 at a time, until 80 ms
+        # of GPU time has passed.
+        done, gpu_ms = 0, 0.0
+        while done < min_steps or gpu_ms < SETTLE_MS:
+            a, b = hip.Event(), hip.Event()
+            a.record(stream)
+            for i in range(100):
+                step(sets[(done + i) % rotate])
+            b.record(stream)
+            synced()
+            done, gpu_ms = done + 100, gpu_ms + a.elapsed_ms(b)
+
+    for st in sets:  # eager pass: every set quantized once
         quant(st)
         step(st)
     synced()
-    g_warm = capture(step, max(warmup, 1))
-    g_steps = capture(step, steps)
-    g_gemm = capture(gemm, steps)
-    g_quant = capture(quant, steps)
-    g_warm.launch(stream)
+    settle(warmup)
     wall0 = time.perf_counter()
-    total_ms = timed(g_steps)
+    total_ms = timed_stream(step, steps)
     wall = time.perf_counter() - wall0
-    gemm_ms = timed(g_gemm) / steps
-    quant_ms = timed(g_quant) / steps
+    gemm_ms = timed_stream(gemm, steps) / steps
+    quant_ms = timed_stream(quant, steps) / steps
+    graphs = {name: capture(fn, steps) for name, fn in (("step", step), ("gemm", gemm), ("quant", quant))}
+    graph_ms = {}
+    for name, g in graphs.items():
+        settle(0)
+        graph_ms[name] = timed_graph(g) / steps
     return {"ms_per_step": total_ms / steps, "wall_ms_per_step": wall * 1e3 / steps, "gemm_ms_mean": gemm_ms,
-            "quant_ms_mean": quant_ms, "sets": sets}
+            "quant_ms_mean": quant_ms, "graph_ms_per_step": graph_ms["step"], "graph_gemm_ms_mean": graph_ms["gemm"],
+            "graph_quant_ms_mean": graph_ms["quant"], "sets": sets}
 
 
 def cpu_model():
@@ -249,7 +279,8 @@ def decode_case(m, k, n, steps, warmup, rotate):
             "frac_hbm": round(op_bytes / (r["ms_per_step"] * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
             "gemm_us": round(r["gemm_ms_mean"] * 1e3, 3),
             "gemm_gbps": round(gemm_bytes(m, k, n) / (r["gemm_ms_mean"] * 1e-3) / 1e9, 1),
-            "quant_us": round(r["quant_ms_mean"] * 1e3, 3), "rotated_sets": rotate}
+            "quant_us": round(r["quant_ms_mean"] * 1e3, 3), "rotated_sets": rotate,
+            "graph_us_per_call": round(r["graph_ms_per_step"] * 1e3, 3)}
 
 
 def all_configs(steps, warmup):
@@ -382,8 +413,8 @@ def profile_summary(directory):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--rotate", type=int, default=6)
     ap.add_argument("--config", default="headline", choices=["headline", "all"])
     ap.add_argument("--no-cpu", action="store_true")
@@ -427,6 +458,8 @@ def main():
         "mfma_frac_full_op": round(tops / PEAK_INT8_TOPS, 4),
         "hbm_gbps_full_op": round(w8a8_bytes(m, k, n) / (r["ms_per_step"] * 1e-3) / 1e9, 1),
         "quant_us": round(r["quant_ms_mean"] * 1e3, 3),
+        "timing": "stream-ordered launches between HIP events; graph replay of the same steps: "
+                  f"{r['graph_ms_per_step'] * 1e3:.3f} us/step, GEMM {r['graph_gemm_ms_mean'] * 1e3:.3f} us",
         "roofline": {"kernel": "w8a8_gemm_tiles", "bound": "mfma", "achieved": round(gemm_tops, 2),
                      "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s", "frac": round(gemm_tops / PEAK_INT8_TOPS, 4),
                      "traffic": read_traffic(), "gemm_us": round(r["gemm_ms_mean"] * 1e3, 3),
