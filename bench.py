@@ -88,14 +88,14 @@ class W8A8Set:
         self.host_x, self.host_blob = (x, blob) if seed == 0 else (None, None)
 
 
-def run_w8a8(m, k, n, steps, warmup, rotate, outliers=0.0, scale=(1e-4, 1e-3)):
+def run_w8a8(m, k, n, steps, warmup, rotate, outliers=0.0, scale=(1e-4, 1e-3), settle_ms=SETTLE_MS):
     """Times `steps` opcode-15 steps launched in stream order (the library's
     own launches, as a caller issues them; the host enqueues ahead of the
     GPU), then the same number of GEMM-only and quantize-only launches, for
     per-kernel averages (HIP events on the library stream that runs the
     kernels).  The same three sequences are also replayed from HIP graphs
     and reported beside them.  Each timed sequence starts after at least
-    SETTLE_MS of untimed load (the GPU clocks ramp over tens of ms)."""
+    settle_ms of untimed load (the GPU clocks ramp over tens of ms)."""
     lib = hip.lib()
     stream = hip.default_stream()
     sets = [W8A8Set(m, k, n, seed, outliers, *scale) for seed in range(rotate)]
@@ -147,7 +147,7 @@ def run_w8a8(m, k, n, steps, warmup, rotate, outliers=0.0, scale=(1e-4, 1e-3)):
         # min_steps untimed steps and keep going, 100 at a time, until 80 ms
         # of GPU time has passed.
         done, gpu_ms = 0, 0.0
-        while done < min_steps or gpu_ms < SETTLE_MS:
+        while done < min_steps or gpu_ms < settle_ms:
             a, b = hip.Event(), hip.Event()
             a.record(stream)
             for i in range(100):
@@ -365,9 +365,11 @@ def f16_mlp_case(steps, warmup, m=77, k=768, n=3072, rotate=6):
 
 
 def traffic_probe(steps=12):
-    """Workload of the FETCH_SIZE / WRITE_SIZE passes: a plain elementwise
-    copy of COPY_PROBE_BYTES (torch's unary kernel, reads and writes each byte
-    once) for calibration, then the headline GEMM on rotated sets."""
+    """Workload of the counter passes (FETCH_SIZE, WRITE_SIZE, MFMA busy
+    cycles): a plain elementwise copy of COPY_PROBE_BYTES (torch's unary
+    kernel, reads and writes each byte once) for calibration, then the
+    headline opcode-15 steps and the M=1 decode calls on rotated sets, without
+    the clock-settling runs (every dispatch is serialized under counters)."""
     import torch
 
     src = torch.empty(COPY_PROBE_BYTES // 4, dtype=torch.float32, device="cuda:0").normal_()
@@ -378,12 +380,11 @@ def traffic_probe(steps=12):
     del src, dst
     torch.cuda.empty_cache()
     hip.init(0)
-    if args.config == "c2":
-        print(json.dumps({"C2_f16_text_mlp_77x768x3072x768": f16_mlp_case(args.steps, args.warmup)}), flush=True)
-        return
     m, k, n = HEADLINE
-    r = run_w8a8(m, k, n, steps, 2, 6, outliers=0.01)
-    print(f"traffic probe done: gemm {r['gemm_ms_mean'] * 1e3:.2f} us", flush=True)
+    r = run_w8a8(m, k, n, steps, 2, 6, outliers=0.01, settle_ms=0.0)
+    del r
+    r = run_w8a8(1, 4096, 14336, steps, 2, 6, scale=(5e-5, 5e-4), settle_ms=0.0)
+    print(f"counter probe done: decode {r['ms_per_step'] * 1e3:.2f} us", flush=True)
 
 
 def _short(name):
