@@ -299,6 +299,73 @@ def all_configs(steps, warmup):
         for k, n in ((4096, 14336), (14336, 4096)):
             out[f"C5_M{m}_{k}x{n}"] = decode_case(m, k, n, steps, warmup, 6)
     out["C2_f16_text_mlp_77x768x3072x768"] = f16_mlp_case(steps, warmup)
+    out["opcode19_aux"] = aux_cases(steps, warmup)
+    return out
+
+
+def aux_cases(steps, warmup, rotate=4):
+    """Opcode-19 model auxiliary ops at DiT/VAE shapes (hb_model_aux on HBM
+    tensors, rotated copies, stream-ordered after clock settling).  Bytes are
+    the algorithmic ones: every input value read once, every output written
+    once."""
+    lib = hip.lib()
+    stream = hip.default_stream()
+    rng = np.random.default_rng(5)
+    tok, width, ff, heads, dim = 4096, 1536, 6144, 24, 64
+    cases = {
+        # name: (kw, input floats, weight floats, bias floats, output floats)
+        "ln_modulation_4096x1536": (dict(mode=9, count=tok * width, width=width, spatial=tok, batch=1,
+                                         other_count=width, eps=1e-6), tok * width, width, width, tok * width),
+        "rms_norm_4096x1536": (dict(mode=1, count=tok * width, width=width, other_count=width, eps=1e-6),
+                               tok * width, width, 0, tok * width),
+        "group_norm_512ch_64x64": (dict(mode=2, count=512 * 4096, width=4096, channels=512, spatial=4096, groups=32,
+                                        batch=1, other_count=512, eps=1e-6), 512 * 4096, 512, 512, 512 * 4096),
+        "swiglu_4096x6144": (dict(mode=12, count=tok * ff, width=ff, channels=2 * ff, spatial=tok, activation=1),
+                             tok * 2 * ff, 0, 0, tok * ff),
+        "gelu_4096x6144": (dict(mode=6, count=tok * ff, width=ff), tok * ff, 0, 0, tok * ff),
+        "rope_4096tok_24x64": (dict(mode=11, count=tok * heads * dim, width=dim, channels=heads, spatial=tok,
+                                    groups=1, batch=1, other_count=2 * dim * tok), tok * heads * dim, 2 * dim * tok, 0,
+                               tok * heads * dim),
+        "transpose_512x4096": (dict(mode=8, count=512 * 4096, width=512, spatial=4096, batch=1), 512 * 4096, 0, 0,
+                               512 * 4096),
+    }
+    out = {}
+    for name, (kw, nx, nw, nb, ny) in cases.items():
+        sets = []
+        for _ in range(rotate):
+            x = hip.DeviceBuffer.from_array(rng.standard_normal(nx, dtype=np.float32))
+            w = hip.DeviceBuffer.from_array(rng.standard_normal(nw, dtype=np.float32) * 0.1) if nw else None
+            b = hip.DeviceBuffer.from_array(rng.standard_normal(nb, dtype=np.float32) * 0.1) if nb else None
+            y = hip.DeviceBuffer(ny * 4)
+            sets.append((x, w, b, y))
+
+        def launch(i):
+            x, w, b, y = sets[i % rotate]
+            hip.model_aux(y, x, w, b, stream=stream, **kw)
+
+        done, gpu_ms = 0, 0.0
+        while done < max(warmup, 1) or gpu_ms < SETTLE_MS:
+            a, e = hip.Event(), hip.Event()
+            a.record(stream)
+            for i in range(100):
+                launch(done + i)
+            e.record(stream)
+            hip.check(lib.hb_stream_sync(stream), "sync")
+            done, gpu_ms = done + 100, gpu_ms + a.elapsed_ms(e)
+        a, e = hip.Event(), hip.Event()
+        a.record(stream)
+        for i in range(steps):
+            launch(i)
+        e.record(stream)
+        hip.check(lib.hb_stream_sync(stream), "sync")
+        us = a.elapsed_ms(e) * 1e3 / steps
+        nbytes = 4 * (nx + nw + nb + ny)
+        out[name] = {"mode": kw["mode"], "us": round(us, 2), "gbps": round(nbytes / us * 1e-3, 1),
+                     "frac_hbm": round(nbytes / us * 1e-3 / PEAK_HBM_GBPS, 4)}
+        for st in sets:
+            for buf in st:
+                if buf is not None:
+                    buf.free()
     return out
 
 
@@ -427,8 +494,9 @@ def main():
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--rotate", type=int, default=6)
-    ap.add_argument("--config", default="headline", choices=["headline", "all", "c2"],
-                    help="c2: only the F16 text-MLP case (a profiling aid; prints that case alone)")
+    ap.add_argument("--config", default="headline", choices=["headline", "all", "c2", "aux"],
+                    help="c2 / aux: only the F16 text-MLP case / the opcode-19 cases (profiling aids; "
+                         "print those cases alone)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--traffic-probe", action="store_true")
     ap.add_argument("--profile-summary", metavar="DIR")
@@ -448,6 +516,9 @@ def main():
     hip.init(0)
     if args.config == "c2":
         print(json.dumps({"C2_f16_text_mlp_77x768x3072x768": f16_mlp_case(args.steps, args.warmup)}), flush=True)
+        return
+    if args.config == "aux":
+        print(json.dumps({"opcode19_aux": aux_cases(args.steps, args.warmup)}), flush=True)
         return
     m, k, n = HEADLINE
     r = run_w8a8(m, k, n, args.steps, args.warmup, args.rotate, outliers=0.01)

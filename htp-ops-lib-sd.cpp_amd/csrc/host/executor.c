@@ -1,5 +1,5 @@
 /*
- * Request executor for opcodes 1, 15 and 16.
+ * Request executor for opcodes 1, 15, 16 and 19.
  *
  * Validation order and return codes follow the reference dispatcher
  * (reference src/dsp/op_executor.cc:274-540) and its kernels' argument checks
@@ -9,6 +9,7 @@
  * device mirrors, HBM-resident tensors are used in place, and outputs are
  * host-visible when the call returns.
  */
+#include <math.h>
 #include <pthread.h>
 #include <stdlib.h>
 #include <string.h>
@@ -437,6 +438,105 @@ int htp_exec_matmul_w16a32(const struct MatMulParams *p, int32_t *elapsed_us, ui
   return rc;
 }
 
+/* ---- opcode 19 ------------------------------------------------------------------- */
+
+/* A device pointer with 4-byte alignment for an optional input view (NULL view: NULL). */
+static const float *aux_input(const htp_view *v, int slot, hb_stream s, int *failed) {
+  if (!v) return NULL;
+  if (stage_in(v, s)) {
+    *failed = 1;
+    return NULL;
+  }
+  const float *p = (const float *)aligned_input(v, 4, slot, s);
+  if (!p) *failed = 1;
+  return p;
+}
+
+static int exec_model_aux(uint8_t *payload, size_t payload_size) {
+  /* reference src/dsp/op_executor.cc:371-404, src/dsp/ops/mat_mul.c:2488-2501 */
+  if (payload_size != sizeof(struct NativeAuxParams)) return -1;
+  struct NativeAuxParams p;
+  memcpy(&p, payload, sizeof(p));
+  if (p.count <= 0 || p.mode < 0 || p.mode > 13 || p.width <= 0 || p.channels <= 0 || p.spatial <= 0 ||
+      p.batch <= 0)
+    return -1;
+  const int64_t wsb = (int64_t)p.width * p.spatial * p.batch;
+  const int has_w = p.weight.fd >= 0, has_b = p.bias.fd >= 0;
+  if (p.mode == 8 && wsb != p.count) return -1;
+  if (p.mode == 2 && (p.groups <= 0 || p.channels % p.groups)) return -1;
+  if (p.mode == 12 && (wsb != p.count || has_w || has_b || p.channels < (int64_t)2 * p.width ||
+                       (p.activation != 0 && p.activation != 1)))
+    return -1;
+  if (p.mode == 13 && (p.groups <= 0 || !has_w || has_b ||
+                       ((int64_t)p.width + p.groups) * p.spatial * p.batch != p.count ||
+                       (int64_t)p.groups * p.spatial * p.batch != p.other_count ||
+                       p.channels < (int64_t)2 * p.width || (p.activation != 0 && p.activation != 1)))
+    return -1;
+  if ((p.mode == 9 || p.mode == 10) &&
+      (wsb != p.count || !has_w || !has_b ||
+       (p.other_count != p.width && p.other_count != (int64_t)p.width * p.batch) ||
+       (p.mode == 9 && (!isfinite(p.eps) || p.eps < 0))))
+    return -1;
+  if (p.mode == 11 && (p.width % 2 || (int64_t)p.width * p.channels * p.spatial * p.batch != p.count || !has_w ||
+                       has_b || (p.groups != 1 && p.groups != p.batch) ||
+                       p.other_count != (int64_t)2 * p.width * p.spatial * p.groups))
+    return -1;
+  const int n = p.mode == 2 ? p.channels : p.mode == 9 ? p.other_count : p.mode == 10 ? p.count : p.width;
+  if (p.mode <= 2 && has_w && p.other_count != n) return -1;
+  if ((p.mode == 3 || p.mode == 4) && (p.other_count <= 0 || p.count % p.other_count || !has_w)) return -1;
+  size_t input_bytes = (size_t)p.count * 4u;
+  if (p.mode == 12 || p.mode == 13)
+    input_bytes = ((size_t)p.spatial * (size_t)p.batch - 1u) * (size_t)p.channels * 4u + (size_t)2 * p.width * 4u;
+  htp_view out, in, wgt, bias;
+  int rc = resolve(&p.output, (size_t)p.count * 4u, &out, -1);
+  if (!rc) rc = resolve(&p.input, input_bytes, &in, -1);
+  if (!rc && has_w) rc = resolve(&p.weight, (size_t)p.other_count * 4u, &wgt, -1);
+  if (!rc && has_b) rc = resolve(&p.bias, (size_t)n * 4u, &bias, -1);
+  if (rc) return rc;
+  /* The reference's worker pool refuses a call with no task (mat_mul.c:2491). */
+  if ((p.mode <= 1 || p.mode == 9) && p.count / p.width == 0) return -40;
+  if (htp_executor_ensure_device() != 0) return -5;
+  if (materialize(&out) || materialize(&in) || (has_w && materialize(&wgt)) || (has_b && materialize(&bias)))
+    return -5;
+  hb_stream s = htp_executor_stream();
+  int failed = 0;
+  const float *x = aux_input(&in, 2, s, &failed);
+  const float *w = aux_input(has_w ? &wgt : NULL, 0, s, &failed);
+  const float *b = aux_input(has_b ? &bias : NULL, 1, s, &failed);
+  if (failed) return -5;
+  float *y = ((uintptr_t)out.dev % 4u) == 0 ? (float *)out.dev : (float *)htp_executor_scratch(3, out.bytes);
+  if (!y) return -5;
+  /* Values a mode does not write keep their contents: the norms cover whole
+   * rows (modes 0/1) or groups (mode 2) only. */
+  int64_t covered = p.count;
+  if (p.mode <= 1) covered = (int64_t)(p.count / p.width) * p.width;
+  if (p.mode == 2) covered = (int64_t)p.batch * p.spatial * p.channels;
+  if (covered < p.count) {
+    if (stage_in(&out, s)) return -5;
+    if ((void *)y != (void *)out.dev && hb_memcpy_d2d(y, out.dev, out.bytes, s) != HB_OK) return -5;
+  }
+  event_set ev;
+  if (events_open(&ev, 2)) {
+    events_close(&ev);
+    return -5;
+  }
+  int hrc = hb_event_record(ev.e[0], s);
+  if (!hrc)
+    hrc = hb_model_aux(y, x, w, b, p.mode, p.count, p.width, p.channels, p.spatial, p.groups, p.batch, p.other_count,
+                       p.activation, p.eps, s);
+  if (!hrc) hrc = hb_event_record(ev.e[1], s);
+  if (!hrc && (void *)y != (void *)out.dev) hrc = hb_memcpy_d2d(out.dev, y, out.bytes, s);
+  if (!hrc) hrc = hb_stream_sync(s);
+  const double ms = hrc ? 0.0 : event_ms(&ev, 0, 1);
+  events_close(&ev);
+  if (hrc) return hrc == HB_E_INVAL ? -1 : -5;
+  if (stage_out(&out, s)) return -5;
+  htp_registry_touch(out.fd);
+  const int32_t elapsed = (int32_t)(ms * 1e3);
+  memcpy(payload + offsetof(struct NativeAuxParams, elapsed_us), &elapsed, sizeof(elapsed));
+  return 0;
+}
+
 /* ---- dispatcher ---------------------------------------------------------------- */
 
 int execute_op_simple(struct OpComputeRequest *req, size_t req_size) {
@@ -451,6 +551,7 @@ int execute_op_simple(struct OpComputeRequest *req, size_t req_size) {
     case HTP_OPS_MAT_MUL_NATIVE_W8A8: rc = exec_w8a8(payload, payload_size); break;
     case HTP_OPS_MAT_MUL_F16_EPILOGUE: rc = exec_f16_epilogue(payload, payload_size); break;
     case HTP_OPS_MAT_MUL_PERMUTED_W16A32: rc = exec_matmul(payload, payload_size); break;
+    case HTP_OPS_MODEL_AUX_F32: rc = exec_model_aux(payload, payload_size); break;
     default: rc = HTP_OPS_E_UNSUPPORTED; break;
   }
   pthread_mutex_unlock(&g_exec_lock);

@@ -78,6 +78,8 @@ _SIGNATURES = {
     "hb_f16_workspace_bytes": (_c_size_t, [_c_int, _c_int, _c_int]),
     "hb_f16_gemm_ws": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int,
                                 _c_void_p, _c_size_t, _c_void_p]),
+    "hb_model_aux": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p] + [_c_int] * 9 + [ctypes.c_float,
+                                                                                         _c_void_p]),
 }
 
 # Host-library symbols (session, executor, registry); bound when present.
@@ -491,6 +493,21 @@ def unpack_w8a8_profile(raw):
 def f16_epilogue_params(out, act, wgt, bias, m, k, n, channels, mode, elapsed=0):
     """F16EpilogueParams (56 bytes)."""
     return _struct.pack("<8i6i", *out, *act, *wgt, *bias, m, k, n, channels, mode, elapsed)
+
+
+def aux_params(out, inp, wgt, bias, mode, count, width, channels, spatial, groups, batch, other_count, activation,
+               eps, elapsed=0):
+    """NativeAuxParams (76 bytes, opcode 19); a buffer (-1, 0) is absent."""
+    return _struct.pack("<8i9ifi", *out, *inp, *wgt, *bias, mode, count, width, channels, spatial, groups, batch,
+                        other_count, activation, eps, elapsed)
+
+
+def model_aux(y_dev, x_dev, w_dev, b_dev, mode, count, width, channels=1, spatial=1, groups=1, batch=1,
+              other_count=0, activation=0, eps=0.0, stream=None):
+    """hb_model_aux on device buffers (w_dev / b_dev may be None)."""
+    check(lib().hb_model_aux(y_dev.ptr, x_dev.ptr, w_dev.ptr if w_dev else None, b_dev.ptr if b_dev else None, mode,
+                             count, width, channels, spatial, groups, batch, other_count, activation, eps, stream),
+          "hb_model_aux")
 
 
 def matmul_params(out, act, wgt, m, k, n, with_elapsed=False):

@@ -158,6 +158,27 @@ size_t hb_f16_workspace_bytes(int m, int k, int n);
 int hb_f16_gemm_ws(float *d_y, const float *d_x, const uint16_t *d_packed, const float *d_bias, int m, int k, int n,
                    int channels, int mode, void *d_workspace, size_t workspace_bytes, hb_stream s);
 
+/*
+ * Opcode 19 model auxiliary ops on f32 tensors (replaces hvx_model_aux_f32,
+ * reference src/dsp/ops/mat_mul.c:2488-2501; argument meaning as in
+ * NativeAuxParams, op_reg.h).  d_w / d_b may be NULL where the mode allows.
+ *   0 LayerNorm rows of width (+w[i], +b[i]); 1 RMSNorm rows; 9 LayerNorm rows
+ *   then v += v*w, v += b (per batch unless other_count == width); 2 GroupNorm
+ *   over spatial*channels/groups values with per-channel w/b; for 0/1/2/9 a
+ *   nonzero activation applies SiLU;  3/4 x + / * w[i % other_count];
+ *   5/6/7 SiLU / GELU-tanh / QuickGELU;  8 transpose [batch][width][spatial]
+ *   -> [batch][spatial][width];  10 x*w[batch-or-0][i % width] + b[i];
+ *   11 rotary embedding, x [batch][token][head][width], 2x2 matrices w per
+ *   (batch-or-0, token, pair), y [batch][head][token][width];  12 SiLU(gate)*up
+ *   from rows of `channels` values (activation 0: [up | gate], 1: [gate | up]);
+ *   13 as 12, each output row prefixed by `groups` attention values from w.
+ * The caller validates shapes as opcode 19 does; this checks only what the
+ * kernels index with.
+ */
+int hb_model_aux(float *d_y, const float *d_x, const float *d_w, const float *d_b, int mode, int count, int width,
+                 int channels, int spatial, int groups, int batch, int other_count, int activation, float eps,
+                 hb_stream s);
+
 #ifdef __cplusplus
 }
 #endif

@@ -173,6 +173,18 @@ struct F16EpilogueParams {
 } __attribute__((packed));
 
 HTP_OPS_STATIC_ASSERT(sizeof(struct F16EpilogueParams) == 56, "F16 epilogue ABI");
+
+/* Opcode 19 payload (reference include/op_reg.h:503-507): model auxiliary f32
+ * ops.  weight.fd / bias.fd < 0 mean "absent".  Modes 0-13 as in
+ * src/dsp/ops/mat_mul.c:2356-2486 (see hb_model_aux in hb.h). */
+struct NativeAuxParams {
+  struct RpcmemBufAddr output, input, weight, bias;
+  int32_t mode, count, width, channels, spatial, groups, batch, other_count, activation;
+  float eps;
+  int32_t elapsed_us;
+} __attribute__((packed));
+
+HTP_OPS_STATIC_ASSERT(sizeof(struct NativeAuxParams) == 76, "native auxiliary ABI");
 HTP_OPS_STATIC_ASSERT(sizeof(struct RpcmemBufAddr) == 8, "RpcmemBufAddr ABI");
 
 #ifdef __cplusplus

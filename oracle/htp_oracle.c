@@ -453,6 +453,142 @@ void oracle_gelu_tanh_inplace(float *y, size_t count) {
 }
 
 /* ------------------------------------------------------------------------ */
+/* Opcode 19 model auxiliary ops, reference src/dsp/ops/mat_mul.c:2356-2486 */
+/* (task decomposition :2489).  Row sums accumulate in double, as the       */
+/* reference's cross-lane sum does (:2352-2355); every float step is one    */
+/* IEEE operation in the reference's order.  Activation ids: 1 GELU-tanh,   */
+/* 2 QuickGELU, 4 and 5 SiLU (x*sigmoid(x)).                                */
+/* ------------------------------------------------------------------------ */
+
+float oracle_silu(float z) { return z * stable_sigmoid(z); }
+
+static float aux_activate(float v, int act) {
+  if (act == 1) return oracle_gelu_tanh(v);
+  if (act == 2) return oracle_quick_gelu(v);
+  if (act == 4 || act == 5) return oracle_silu(v);
+  return v;
+}
+
+int oracle_model_aux(float *y, const float *x, const float *w, const float *b, int mode, int count, int width,
+                     int channels, int spatial, int groups, int batch, int other_count, int activation, float eps) {
+  if (count <= 0 || width <= 0 || channels <= 0 || spatial <= 0 || batch <= 0) return -1;
+  if (mode <= 2 || mode == 9) {
+    int tasks, len;
+    if (mode == 2) {
+      if (groups <= 0 || channels % groups) return -1;
+      tasks = groups * batch;
+      len = spatial * (channels / groups);
+    } else {
+      tasks = count / width;
+      len = width;
+    }
+    for (int task = 0; task < tasks; ++task) {
+      const size_t offset = (size_t)task * (size_t)len;
+      const float *xr = x + offset;
+      float mean = 0.0f;
+      if (mode != 1) {
+        double sum = 0.0;
+        for (int i = 0; i < len; ++i) sum += (double)xr[i];
+        mean = (float)(sum / (double)len);
+      }
+      double sq = 0.0;
+      for (int i = 0; i < len; ++i) {
+        const double v = (double)(xr[i] - mean);
+        sq += v * v;
+      }
+      const float inv = 1.0f / sqrtf((float)(sq / (double)len + (double)eps));
+      const size_t pbase = (mode == 9 && other_count != width) ? (size_t)(task / spatial) * (size_t)width : 0;
+      for (int i = 0; i < len; ++i) {
+        float v = (xr[i] - mean) * inv;
+        if (mode == 0 || mode == 1) {
+          if (w) v = v * w[i];
+          if (b) v = v + b[i];
+        } else if (mode == 2) {
+          const int ch = (int)(((offset + (size_t)i) / (size_t)spatial) % (size_t)channels);
+          if (w) v = v * w[ch];
+          if (b) v = v + b[ch];
+        } else {
+          v = v + v * w[pbase + (size_t)i];
+          v = v + b[pbase + (size_t)i];
+        }
+        if (activation) v = aux_activate(v, 4);
+        y[offset + (size_t)i] = v;
+      }
+    }
+    return 0;
+  }
+  switch (mode) {
+    case 3:
+    case 4:
+      if (!w || other_count <= 0) return -1;
+      for (int64_t i = 0; i < count; ++i)
+        y[i] = mode == 3 ? x[i] + w[i % other_count] : x[i] * w[i % other_count];
+      return 0;
+    case 5:
+    case 6:
+    case 7:
+      for (int64_t i = 0; i < count; ++i) y[i] = aux_activate(x[i], mode == 5 ? 4 : mode == 6 ? 1 : 2);
+      return 0;
+    case 8:
+      if ((int64_t)width * spatial * batch != count) return -1;
+      for (int bt = 0; bt < batch; ++bt)
+        for (int r = 0; r < width; ++r)
+          for (int c = 0; c < spatial; ++c)
+            y[((size_t)bt * spatial + c) * width + r] = x[((size_t)bt * width + r) * spatial + c];
+      return 0;
+    case 10:
+      if (!w || !b) return -1;
+      for (int64_t i = 0; i < count; ++i) {
+        const int64_t channel = i % width, bt = i / ((int64_t)width * spatial);
+        const int64_t pb = other_count == width ? 0 : bt;
+        y[i] = x[i] * w[pb * width + channel] + b[i];
+      }
+      return 0;
+    case 11: {
+      if (!w || width % 2 || (groups != 1 && groups != batch)) return -1;
+      for (int bt = 0; bt < batch; ++bt)
+        for (int token = 0; token < spatial; ++token) {
+          const float *pe = w + ((size_t)(groups == 1 ? 0 : bt) * spatial + token) * (size_t)width * 2;
+          for (int head = 0; head < channels; ++head) {
+            const float *xs = x + (((size_t)bt * spatial + token) * channels + head) * width;
+            float *ys = y + (((size_t)bt * channels + head) * spatial + token) * width;
+            for (int e = 0; e < width; e += 2) {
+              const float *m = pe + 2 * e;
+              const float x0 = xs[e], x1 = xs[e + 1];
+              ys[e] = x0 * m[0] + x1 * m[1];
+              ys[e + 1] = x1 * m[3] + x0 * m[2];
+            }
+          }
+        }
+      return 0;
+    }
+    case 12:
+      if (channels < 2 * width) return -1;
+      for (int64_t i = 0; i < count; ++i) {
+        const int64_t column = i % width, row = i / width;
+        const float *a = x + row * channels + column;
+        const float gate = a[activation ? 0 : width], up = a[activation ? width : 0];
+        y[i] = aux_activate(gate, 5) * up;
+      }
+      return 0;
+    case 13:
+      if (!w || groups <= 0 || channels < 2 * width) return -1;
+      for (int64_t r = 0; r < (int64_t)spatial * batch; ++r) {
+        float *dst = y + r * (width + groups);
+        for (int i = 0; i < groups; ++i) dst[i] = w[r * groups + i];
+        const float *xr = x + r * channels;
+        for (int i = 0; i < width; ++i) {
+          const float gate = xr[i + (activation ? 0 : width)], up = xr[i + (activation ? width : 0)];
+          dst[groups + i] = aux_activate(gate, 5) * up;
+        }
+      }
+      return 0;
+    default:
+      return -1;
+  }
+}
+
+/* ------------------------------------------------------------------------ */
 /* Packed F16 GEMM with epilogue (opcodes 1/16)                             */
 /* layout: reference src/host/test.c:547-558 (writer);                      */
 /* semantics: reference src/dsp/ops/mat_mul.c:937-1049                      */

@@ -78,6 +78,11 @@ void oracle_w8a8_planes(uint8_t *out, const int32_t *acc, int m, int n);
 float oracle_gelu_tanh(float z);
 float oracle_quick_gelu(float z);
 void oracle_gelu_tanh_inplace(float *y, size_t count);
+float oracle_silu(float z);
+
+/* ---- opcode 19 model auxiliary ops ---------------------------------------- */
+int oracle_model_aux(float *y, const float *x, const float *w, const float *b, int mode, int count, int width,
+                     int channels, int spatial, int groups, int batch, int other_count, int activation, float eps);
 
 /* ---- packed F16 GEMM -------------------------------------------------------- */
 size_t oracle_f16_permuted_index(int k_total, int k_idx, int n_idx);

@@ -36,6 +36,8 @@ _SIGS = {
     "oracle_gelu_tanh": (ctypes.c_float, [ctypes.c_float]),
     "oracle_quick_gelu": (ctypes.c_float, [ctypes.c_float]),
     "oracle_gelu_tanh_inplace": (None, [_P, _S]),
+    "oracle_silu": (ctypes.c_float, [ctypes.c_float]),
+    "oracle_model_aux": (_I, [_P, _P, _P, _P] + [_I] * 9 + [ctypes.c_float]),
     "oracle_f16_permuted_index": (_S, [_I, _I, _I]),
     "oracle_f16_permute": (None, [_P, _P, _I, _I]),
     "oracle_f16_gemm_epilogue": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I]),
@@ -215,6 +217,27 @@ def quick_gelu(z):
 def gelu_tanh_array(y):
     y = np.array(y, np.float32, copy=True)
     lib().oracle_gelu_tanh_inplace(_ptr(y), y.size)
+    return y
+
+
+def silu(z):
+    return lib().oracle_silu(float(z))
+
+
+# ---- opcode 19 ---------------------------------------------------------------
+
+def model_aux(x, w, b, mode, count, width, channels=1, spatial=1, groups=1, batch=1, other_count=0, activation=0,
+              eps=0.0, out=None):
+    """Opcode-19 restatement; `out` (float32, count values) supplies the values a
+    mode leaves untouched (rows past count/width), zeros when omitted."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = None if w is None else np.ascontiguousarray(w, np.float32)
+    b = None if b is None else np.ascontiguousarray(b, np.float32)
+    y = np.zeros(count, np.float32) if out is None else np.array(out, np.float32, copy=True)
+    rc = lib().oracle_model_aux(_ptr(y), _ptr(x), _ptr(w), _ptr(b), mode, count, width, channels, spatial, groups,
+                                batch, other_count, activation, float(eps))
+    if rc:
+        raise ValueError(f"oracle_model_aux rejected mode {mode}")
     return y
 
 

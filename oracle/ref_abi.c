@@ -32,6 +32,7 @@ size_t ref_abi_size(int which) {
     case 13: return sizeof(struct RpcmemMapEntryV2);
     case 14: return sizeof(struct RpcmemMapRequestV2);
     case 15: return sizeof(struct W8A8CpuBatch);
+    case 16: return sizeof(struct NativeAuxParams);
     default: return 0;
   }
 }
@@ -52,6 +53,9 @@ size_t ref_abi_offset(int which) {
     case 11: return offsetof(struct NativeW8A8CpuParams, control);
     case 12: return offsetof(struct RpcmemMapRequestV2, entries);
     case 13: return offsetof(struct W8A8Header, inverse_offset);
+    case 14: return offsetof(struct NativeAuxParams, mode);
+    case 15: return offsetof(struct NativeAuxParams, eps);
+    case 16: return offsetof(struct NativeAuxParams, elapsed_us);
     default: return (size_t)-1;
   }
 }
@@ -64,6 +68,7 @@ int ref_opcode(int which) {
     case 3: return HTP_OPS_COUNT;
     case 4: return REQUEST_TYPE_OP_COMPUTE;
     case 5: return REQUEST_TYPE_RPCMEM_MAP;
+    case 6: return HTP_OPS_MODEL_AUX_F32;
     default: return -1;
   }
 }

@@ -43,7 +43,7 @@ def ref(orc):
 
 
 EXPECTED_SIZES = {0: 16, 1: 8, 2: 4, 3: 8, 4: 128, 5: 40, 6: 64, 7: 104, 8: 17536, 9: 48, 10: 92, 11: 56,
-                  12: 8, 13: 32, 14: 24, 15: 16}
+                  12: 8, 13: 32, 14: 24, 15: 16, 16: 76}
 
 
 def test_sizes_match_reference(own, ref):
@@ -52,14 +52,15 @@ def test_sizes_match_reference(own, ref):
 
 
 def test_offsets_match_reference(own, ref):
-    for which in range(14):
+    for which in range(17):
         assert own.own_abi_offset(which) == ref.ref_abi_offset(which), which
 
 
 def test_opcodes_match_reference(own, ref):
-    for which in range(6):
+    for which in range(7):
         assert own.own_opcode(which) == ref.ref_opcode(which), which
     assert own.own_opcode(1) == 15 and own.own_opcode(2) == 16 and own.own_opcode(0) == 1
+    assert own.own_opcode(6) == 19
 
 
 def _validate(lib, fn, raw, capacity):
