@@ -320,6 +320,9 @@ def aux_cases(steps, warmup, rotate=4):
                                tok * width, width, 0, tok * width),
         "group_norm_512ch_64x64": (dict(mode=2, count=512 * 4096, width=4096, channels=512, spatial=4096, groups=32,
                                         batch=1, other_count=512, eps=1e-6), 512 * 4096, 512, 512, 512 * 4096),
+        "group_norm_128ch_512x512": (dict(mode=2, count=128 * 262144, width=262144, channels=128, spatial=262144,
+                                          groups=32, batch=1, other_count=128, eps=1e-6), 128 * 262144, 128, 128,
+                                     128 * 262144),
         "swiglu_4096x6144": (dict(mode=12, count=tok * ff, width=ff, channels=2 * ff, spatial=tok, activation=1),
                              tok * 2 * ff, 0, 0, tok * ff),
         "gelu_4096x6144": (dict(mode=6, count=tok * ff, width=ff), tok * ff, 0, 0, tok * ff),
@@ -339,9 +342,13 @@ def aux_cases(steps, warmup, rotate=4):
             y = hip.DeviceBuffer(ny * 4)
             sets.append((x, w, b, y))
 
+        wsb = hip.model_aux_workspace_bytes(kw["mode"], kw.get("channels", 1), kw.get("spatial", 1),
+                                            kw.get("groups", 1), kw.get("batch", 1))
+        ws = hip.DeviceBuffer(wsb) if wsb else None
+
         def launch(i):
             x, w, b, y = sets[i % rotate]
-            hip.model_aux(y, x, w, b, stream=stream, **kw)
+            hip.model_aux(y, x, w, b, stream=stream, workspace=ws, **kw)
 
         done, gpu_ms = 0, 0.0
         while done < max(warmup, 1) or gpu_ms < SETTLE_MS:

@@ -52,6 +52,7 @@ __device__ inline float activate(float x, int act) {
   return x;
 }
 
+template <int T = kAuxThreads>
 __device__ inline double block_sum(double v, double *red) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
@@ -61,49 +62,201 @@ __device__ inline double block_sum(double v, double *red) {
   __syncthreads();
   double t = 0.0;
 #pragma unroll
-  for (int w = 0; w < kAuxThreads / 64; ++w) t += red[w];
+  for (int w = 0; w < T / 64; ++w) t += red[w];
   return t;
 }
 
-// Modes 0, 1, 2, 9: one workgroup per task of `len` contiguous values.
+// Affine / modulation step of the norms for element i of the task (MODE as in aux_norm).
+// Mode 2: a task is one (batch, group) of channels/groups whole channels, so
+// the channel of element i is pbase + i / spatial with pbase = (task % groups)
+// * channels / groups (the reference's ((offset + i) / spatial) % channels).
 template <int MODE>
-__global__ __launch_bounds__(kAuxThreads) void aux_norm(float *__restrict__ y, const float *__restrict__ x,
-                                                        const float *__restrict__ w, const float *__restrict__ b,
-                                                        int len, int width, int channels, int spatial,
-                                                        int other_count, float eps, int act) {
-  __shared__ double red[kAuxThreads / 64];
+__device__ inline float norm_affine(float v, int i, const float *w, const float *b, size_t pbase, int spatial) {
+  if (MODE == 0 || MODE == 1) {
+    if (w) v = __fmul_rn(v, w[i]);
+    if (b) v = __fadd_rn(v, b[i]);
+  } else if (MODE == 2) {
+    const int ch = (int)pbase + (int)((unsigned)i / (unsigned)spatial);
+    if (w) v = __fmul_rn(v, w[ch]);
+    if (b) v = __fadd_rn(v, b[ch]);
+  } else {
+    v = __fadd_rn(v, __fmul_rn(v, w[pbase + i]));
+    v = __fadd_rn(v, b[pbase + i]);
+  }
+  return v;
+}
+
+// Modes 0, 1, 2, 9 with the task held in registers: T threads x NV float4,
+// len % 4 == 0 and 16-byte aligned rows; x is read once.
+template <int MODE, int NV, int T>
+__global__ __launch_bounds__(T) void aux_norm_reg(float *__restrict__ y, const float *__restrict__ x,
+                                                  const float *__restrict__ w, const float *__restrict__ b, int len,
+                                                  int width, int channels, int spatial, int groups, int other_count,
+                                                  float eps, int act) {
+  __shared__ double red[T / 64];
+  const size_t offset = (size_t)blockIdx.x * (size_t)len;
+  const float4 *xr = (const float4 *)(x + offset);
+  const int nv4 = len / 4;
+  float4 v[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) v[j] = xr[min((int)threadIdx.x + j * T, nv4 - 1)];
+  float mean = 0.0f;
+  if (MODE != 1) {
+    double s = 0.0;
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+      if ((int)threadIdx.x + j * T < nv4) s += (double)v[j].x + (double)v[j].y + (double)v[j].z + (double)v[j].w;
+    mean = (float)(block_sum<T>(s, red) / (double)len);
+  }
+  double q = 0.0;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    if ((int)threadIdx.x + j * T < nv4) {
+      const double d0 = __fsub_rn(v[j].x, mean), d1 = __fsub_rn(v[j].y, mean), d2 = __fsub_rn(v[j].z, mean),
+                   d3 = __fsub_rn(v[j].w, mean);
+      q += d0 * d0 + d1 * d1 + d2 * d2 + d3 * d3;
+    }
+  }
+  const float inv = __fdiv_rn(1.0f, __fsqrt_rn((float)(block_sum<T>(q, red) / (double)len + (double)eps)));
+  const size_t pbase = MODE == 9 ? (other_count != width ? (size_t)(blockIdx.x / spatial) * (size_t)width : 0)
+                      : MODE == 2 ? (size_t)(blockIdx.x % groups) * (size_t)(channels / groups)
+                                  : 0;
+  float4 *yr = (float4 *)(y + offset);
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int idx = (int)threadIdx.x + j * T;
+    if (idx < nv4) {
+      float o[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+      if (MODE == 2) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float t = norm_affine<MODE>(__fmul_rn(__fsub_rn(o[e], mean), inv), 4 * idx + e, w, b, pbase, spatial);
+          o[e] = act ? activate(t, 4) : t;
+        }
+      } else {
+        // the row's parameters are 16-byte aligned quads (width % 4 == 0)
+        const float4 wv = w ? ((const float4 *)(w + pbase))[idx] : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+        const float4 bv = b ? ((const float4 *)(b + pbase))[idx] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        const float wq[4] = {wv.x, wv.y, wv.z, wv.w}, bq[4] = {bv.x, bv.y, bv.z, bv.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float t = __fmul_rn(__fsub_rn(o[e], mean), inv);
+          if (MODE == 9) {
+            t = __fadd_rn(t, __fmul_rn(t, wq[e]));
+            t = __fadd_rn(t, bq[e]);
+          } else {
+            if (w) t = __fmul_rn(t, wq[e]);
+            if (b) t = __fadd_rn(t, bq[e]);
+          }
+          o[e] = act ? activate(t, 4) : t;
+        }
+      }
+      yr[idx] = make_float4(o[0], o[1], o[2], o[3]);
+    }
+  }
+}
+
+// Modes 0, 1, 2, 9, any task length: one workgroup of T threads per task of
+// `len` contiguous values, three passes (the later ones mostly from cache).
+template <int MODE, int T>
+__global__ __launch_bounds__(T) void aux_norm(float *__restrict__ y, const float *__restrict__ x,
+                                              const float *__restrict__ w, const float *__restrict__ b, int len,
+                                              int width, int channels, int spatial, int groups, int other_count,
+                                              float eps, int act) {
+  __shared__ double red[T / 64];
   const size_t offset = (size_t)blockIdx.x * (size_t)len;
   const float *xr = x + offset;
   float *yr = y + offset;
   float mean = 0.0f;
   if (MODE != 1) {
     double s = 0.0;
-    for (int i = threadIdx.x; i < len; i += kAuxThreads) s += (double)xr[i];
-    mean = (float)(block_sum(s, red) / (double)len);
+    for (int i = threadIdx.x; i < len; i += T) s += (double)xr[i];
+    mean = (float)(block_sum<T>(s, red) / (double)len);
   }
   double q = 0.0;
-  for (int i = threadIdx.x; i < len; i += kAuxThreads) {
+  for (int i = threadIdx.x; i < len; i += T) {
     const double v = (double)__fsub_rn(xr[i], mean);
     q += v * v;
   }
-  const float inv = __fdiv_rn(1.0f, __fsqrt_rn((float)(block_sum(q, red) / (double)len + (double)eps)));
-  // mode 9: per-batch parameters unless they are shared by all batches
-  const size_t pbase = (MODE == 9 && other_count != width) ? (size_t)(blockIdx.x / spatial) * (size_t)width : 0;
-  for (int i = threadIdx.x; i < len; i += kAuxThreads) {
+  const float inv = __fdiv_rn(1.0f, __fsqrt_rn((float)(block_sum<T>(q, red) / (double)len + (double)eps)));
+  // mode 9: per-batch parameters unless they are shared by all batches; mode 2: the group's first channel
+  const size_t pbase = MODE == 9 ? (other_count != width ? (size_t)(blockIdx.x / spatial) * (size_t)width : 0)
+                      : MODE == 2 ? (size_t)(blockIdx.x % groups) * (size_t)(channels / groups)
+                                  : 0;
+  for (int i = threadIdx.x; i < len; i += T) {
     float v = __fmul_rn(__fsub_rn(xr[i], mean), inv);
-    if (MODE == 0 || MODE == 1) {
-      if (w) v = __fmul_rn(v, w[i]);
-      if (b) v = __fadd_rn(v, b[i]);
-    } else if (MODE == 2) {
-      const int ch = (int)(((offset + (size_t)i) / (size_t)spatial) % (size_t)channels);
-      if (w) v = __fmul_rn(v, w[ch]);
-      if (b) v = __fadd_rn(v, b[ch]);
-    } else {
-      v = __fadd_rn(v, __fmul_rn(v, w[pbase + i]));
-      v = __fadd_rn(v, b[pbase + i]);
-    }
+    v = norm_affine<MODE>(v, i, w, b, pbase, spatial);
     if (act) v = activate(v, 4);
     yr[i] = v;
+  }
+}
+
+// Group norm over few long groups: each group is split into `chunks` pieces
+// of `chunk` values (a multiple of 4) handled by separate workgroups, in
+// three launches that keep the reference's two-pass statistics: the chunk
+// sums, then the centered sums of squares about the group's float mean, then
+// the output.  Every workgroup of a group adds the per-chunk partials in the
+// same order, so all of them derive the same mean and inv.
+// ws: double sum[tasks][chunks], then double sq[tasks][chunks].
+__device__ inline double ordered_total(const double *part, int chunks, double *red) {
+  // thread 0 adds the partials in chunk order; the block reads its result
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double t = 0.0;
+    for (int c = 0; c < chunks; ++c) t += part[c];
+    red[0] = t;
+  }
+  __syncthreads();
+  return red[0];
+}
+
+template <int PASS>
+__global__ __launch_bounds__(kAuxThreads) void aux_group_norm_chunk(float *__restrict__ y, const float *__restrict__ x,
+                                                                    const float *__restrict__ w,
+                                                                    const float *__restrict__ b, double *ws, int len,
+                                                                    int chunk, int chunks, int tasks, int channels,
+                                                                    int spatial, int groups, float eps, int act) {
+  __shared__ double red[kAuxThreads / 64];
+  const int c = blockIdx.x, task = blockIdx.y;
+  const size_t offset = (size_t)task * (size_t)len;
+  const int begin = c * chunk, end = min(begin + chunk, len);
+  const float4 *xr = (const float4 *)(x + offset);
+  double *sum = ws + (size_t)task * chunks, *sq = ws + (size_t)tasks * chunks + (size_t)task * chunks;
+  if (PASS == 0) {
+    double s = 0.0;
+    for (int i = begin / 4 + threadIdx.x; i < end / 4; i += kAuxThreads) {
+      const float4 v = xr[i];
+      s += (double)v.x + (double)v.y + (double)v.z + (double)v.w;
+    }
+    s = block_sum(s, red);
+    if (threadIdx.x == 0) sum[c] = s;
+    return;
+  }
+  const float mean = (float)(ordered_total(sum, chunks, red) / (double)len);
+  if (PASS == 1) {
+    double q = 0.0;
+    for (int i = begin / 4 + threadIdx.x; i < end / 4; i += kAuxThreads) {
+      const float4 v = xr[i];
+      const double d0 = __fsub_rn(v.x, mean), d1 = __fsub_rn(v.y, mean), d2 = __fsub_rn(v.z, mean),
+                   d3 = __fsub_rn(v.w, mean);
+      q += d0 * d0 + d1 * d1 + d2 * d2 + d3 * d3;
+    }
+    q = block_sum(q, red);
+    if (threadIdx.x == 0) sq[c] = q;
+    return;
+  }
+  const float inv = __fdiv_rn(1.0f, __fsqrt_rn((float)(ordered_total(sq, chunks, red) / (double)len + (double)eps)));
+  const size_t pbase = (size_t)(task % groups) * (size_t)(channels / groups);
+  float4 *yr = (float4 *)(y + offset);
+  for (int i = begin / 4 + threadIdx.x; i < end / 4; i += kAuxThreads) {
+    const float4 v = xr[i];
+    float o[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float t = norm_affine<2>(__fmul_rn(__fsub_rn(o[e], mean), inv), 4 * i + e, w, b, pbase, spatial);
+      o[e] = act ? activate(t, 4) : t;
+    }
+    yr[i] = make_float4(o[0], o[1], o[2], o[3]);
   }
 }
 
@@ -133,6 +286,52 @@ __global__ __launch_bounds__(kAuxThreads) void aux_elementwise(float *__restrict
       v = __fmul_rn(activate(gate, 5), up);
     }
     y[i] = v;
+  }
+}
+
+// The same modes, four consecutive values per thread with 16-byte loads and
+// stores (count % 4 == 0, x and y 16-byte aligned; mode 12 also needs width
+// and channels divisible by 4 so each quad of gate and up values is contiguous).
+template <int MODE>
+__global__ __launch_bounds__(kAuxThreads) void aux_elementwise4(float *__restrict__ y, const float *__restrict__ x,
+                                                                const float *__restrict__ w,
+                                                                const float *__restrict__ b, int64_t count4,
+                                                                int width, int channels, int spatial,
+                                                                int other_count, int act) {
+  const int64_t stride = (int64_t)gridDim.x * kAuxThreads;
+  for (int64_t q = (int64_t)blockIdx.x * kAuxThreads + threadIdx.x; q < count4; q += stride) {
+    const int64_t i0 = 4 * q;
+    float o[4];
+    if (MODE == 12) {
+      const int64_t column = i0 % width, row = i0 / width;
+      const float *a = x + row * channels + column;
+      const float4 g = *(const float4 *)(a + (act ? 0 : width)), u = *(const float4 *)(a + (act ? width : 0));
+      o[0] = __fmul_rn(activate(g.x, 5), u.x);
+      o[1] = __fmul_rn(activate(g.y, 5), u.y);
+      o[2] = __fmul_rn(activate(g.z, 5), u.z);
+      o[3] = __fmul_rn(activate(g.w, 5), u.w);
+    } else {
+      const float4 xv = ((const float4 *)x)[q];
+      const float xi[4] = {xv.x, xv.y, xv.z, xv.w};
+      const float4 bv = MODE == 10 ? ((const float4 *)b)[q] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      const float bi[4] = {bv.x, bv.y, bv.z, bv.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t i = i0 + e;
+        if (MODE == 3) {
+          o[e] = __fadd_rn(xi[e], w[i % other_count]);
+        } else if (MODE == 4) {
+          o[e] = __fmul_rn(xi[e], w[i % other_count]);
+        } else if (MODE == 5 || MODE == 6 || MODE == 7) {
+          o[e] = activate(xi[e], MODE == 5 ? 4 : MODE == 6 ? 1 : 2);
+        } else {  // 10
+          const int64_t channel = i % width, batch = i / ((int64_t)width * spatial);
+          const int64_t pb = other_count == width ? 0 : batch;
+          o[e] = __fadd_rn(__fmul_rn(xi[e], w[pb * width + channel]), bi[e]);
+        }
+      }
+    }
+    ((float4 *)y)[q] = make_float4(o[0], o[1], o[2], o[3]);
   }
 }
 
@@ -185,16 +384,93 @@ __global__ __launch_bounds__(kAuxThreads) void aux_swiglu_concat(float *__restri
   }
 }
 
+bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Register-resident tasks when they fit (256 threads up to 8192 values, 1024
+// threads up to 65536), else the three-pass kernel; few long tasks (group
+// norm) take 1024-thread workgroups.
+template <int MODE>
+void launch_norm(float *y, const float *x, const float *w, const float *b, int tasks, int len, int width,
+                 int channels, int spatial, int groups, int other_count, float eps, int act, bool vec,
+                 hipStream_t st) {
+  const dim3 grid(tasks);
+  const int nv4 = len / 4;
+  if (vec && nv4 <= 256 * 1) {
+    hipLaunchKernelGGL((aux_norm_reg<MODE, 1, 256>), grid, dim3(256), 0, st, y, x, w, b, len, width, channels,
+                       spatial, groups, other_count, eps, act);
+  } else if (vec && nv4 <= 256 * 2) {
+    hipLaunchKernelGGL((aux_norm_reg<MODE, 2, 256>), grid, dim3(256), 0, st, y, x, w, b, len, width, channels,
+                       spatial, groups, other_count, eps, act);
+  } else if (vec && nv4 <= 256 * 4) {
+    hipLaunchKernelGGL((aux_norm_reg<MODE, 4, 256>), grid, dim3(256), 0, st, y, x, w, b, len, width, channels,
+                       spatial, groups, other_count, eps, act);
+  } else if (vec && nv4 <= 256 * 8) {
+    hipLaunchKernelGGL((aux_norm_reg<MODE, 8, 256>), grid, dim3(256), 0, st, y, x, w, b, len, width, channels,
+                       spatial, groups, other_count, eps, act);
+  } else if (vec && nv4 <= 1024 * 16) {
+    hipLaunchKernelGGL((aux_norm_reg<MODE, 16, 1024>), grid, dim3(1024), 0, st, y, x, w, b, len, width, channels,
+                       spatial, groups, other_count, eps, act);
+  } else if (tasks < 1024) {
+    hipLaunchKernelGGL((aux_norm<MODE, 1024>), grid, dim3(1024), 0, st, y, x, w, b, len, width, channels, spatial,
+                       groups, other_count, eps, act);
+  } else {
+    hipLaunchKernelGGL((aux_norm<MODE, 256>), grid, dim3(256), 0, st, y, x, w, b, len, width, channels, spatial,
+                       groups, other_count, eps, act);
+  }
+}
+
+// Chunked group-norm plan: used when the groups alone would leave most CUs
+// idle and the values divide into float4 quads; 0 chunks means "not chunked".
+struct GroupPlan {
+  int chunks, chunk;
+};
+
+GroupPlan group_plan(int tasks, int len) {
+  GroupPlan p{0, 0};
+  if (tasks >= 512 || len % 4 || len < 8192) return p;
+  int chunks = (1024 + tasks - 1) / tasks;  // aim for about 1024 workgroups
+  if (chunks > len / 4096) chunks = len / 4096;
+  if (chunks < 2) return p;
+  int chunk = (len + chunks - 1) / chunks;
+  chunk = (chunk + 3) / 4 * 4;
+  p.chunks = (len + chunk - 1) / chunk;
+  p.chunk = chunk;
+  return p;
+}
+
 int elementwise_grid(int64_t count) {
   const int64_t blocks = (count + kAuxThreads - 1) / kAuxThreads;
   return (int)(blocks < 65536 ? blocks : 65536);
 }
 
+template <int MODE>
+void launch_elementwise(float *y, const float *x, const float *w, const float *b, int count, int width, int channels,
+                        int spatial, int other_count, int act, hipStream_t st) {
+  bool vec = count % 4 == 0 && aligned16(x) && aligned16(y) && (MODE != 10 || aligned16(b));
+  if (MODE == 12) vec = vec && width % 4 == 0 && channels % 4 == 0;
+  if (vec) {
+    const int64_t count4 = count / 4;
+    hipLaunchKernelGGL(aux_elementwise4<MODE>, dim3(elementwise_grid(count4)), dim3(kAuxThreads), 0, st, y, x, w, b,
+                       count4, width, channels, spatial, other_count, act);
+  } else {
+    hipLaunchKernelGGL(aux_elementwise<MODE>, dim3(elementwise_grid(count)), dim3(kAuxThreads), 0, st, y, x, w, b,
+                       (int64_t)count, width, channels, spatial, other_count, act);
+  }
+}
+
 }  // namespace
 
-extern "C" int hb_model_aux(float *d_y, const float *d_x, const float *d_w, const float *d_b, int mode, int count,
-                            int width, int channels, int spatial, int groups, int batch, int other_count,
-                            int activation, float eps, hb_stream s) {
+extern "C" size_t hb_model_aux_workspace_bytes(int mode, int channels, int spatial, int groups, int batch) {
+  if (mode != 2 || groups <= 0 || channels <= 0 || spatial <= 0 || batch <= 0 || channels % groups) return 0;
+  const int64_t len64 = (int64_t)spatial * (channels / groups), tasks64 = (int64_t)groups * batch;
+  if (len64 > INT32_MAX || tasks64 > INT32_MAX) return 0;
+  const GroupPlan p = group_plan((int)tasks64, (int)len64);
+  return p.chunks ? (size_t)tasks64 * (size_t)p.chunks * 2u * sizeof(double) : 0;
+}
+
+extern "C" int hb_model_aux_ws(float *d_y, const float *d_x, const float *d_w, const float *d_b, int mode, int count,
+                               int width, int channels, int spatial, int groups, int batch, int other_count,
+                               int activation, float eps, void *d_workspace, size_t workspace_bytes, hb_stream s) {
   if (!d_y || !d_x) return hb_invalid("hb_model_aux null pointer");
   if (count <= 0 || width <= 0 || channels <= 0 || spatial <= 0 || batch <= 0)
     return hb_invalid("hb_model_aux shape");
@@ -207,45 +483,55 @@ extern "C" int hb_model_aux(float *d_y, const float *d_x, const float *d_w, cons
       if (mode == 9 && (!d_w || !d_b)) return hb_invalid("hb_model_aux mode 9 parameters");
       const int rows = count / width;
       if (rows < 1) return hb_invalid("hb_model_aux rows");
+      const bool vec = width % 4 == 0 && aligned16(d_x) && aligned16(d_y) && aligned16(d_w) && aligned16(d_b);
       if (mode == 0)
-        hipLaunchKernelGGL(aux_norm<0>, dim3(rows), block, 0, st, d_y, d_x, d_w, d_b, width, width, channels, spatial,
-                           other_count, eps, activation);
+        launch_norm<0>(d_y, d_x, d_w, d_b, rows, width, width, channels, spatial, 1, other_count, eps, activation,
+                       vec, st);
       else if (mode == 1)
-        hipLaunchKernelGGL(aux_norm<1>, dim3(rows), block, 0, st, d_y, d_x, d_w, d_b, width, width, channels, spatial,
-                           other_count, eps, activation);
+        launch_norm<1>(d_y, d_x, d_w, d_b, rows, width, width, channels, spatial, 1, other_count, eps, activation,
+                       vec, st);
       else
-        hipLaunchKernelGGL(aux_norm<9>, dim3(rows), block, 0, st, d_y, d_x, d_w, d_b, width, width, channels, spatial,
-                           other_count, eps, activation);
+        launch_norm<9>(d_y, d_x, d_w, d_b, rows, width, width, channels, spatial, 1, other_count, eps, activation,
+                       vec, st);
       break;
     }
     case 2: {
       if (groups <= 0 || channels % groups) return hb_invalid("hb_model_aux groups");
       const int len = spatial * (channels / groups);
-      hipLaunchKernelGGL(aux_norm<2>, dim3(groups * batch), block, 0, st, d_y, d_x, d_w, d_b, len, width, channels,
-                         spatial, other_count, eps, activation);
+      const bool vec = len % 4 == 0 && aligned16(d_x) && aligned16(d_y);
+      const GroupPlan gp = group_plan(groups * batch, len);
+      const size_t need = hb_model_aux_workspace_bytes(mode, channels, spatial, groups, batch);
+      if (vec && gp.chunks && d_workspace && workspace_bytes >= need && ((uintptr_t)d_workspace & 7u) == 0) {
+        const dim3 grid(gp.chunks, groups * batch);
+        double *ws = (double *)d_workspace;
+        hipLaunchKernelGGL(aux_group_norm_chunk<0>, grid, block, 0, st, d_y, d_x, d_w, d_b, ws, len, gp.chunk,
+                           gp.chunks, groups * batch, channels, spatial, groups, eps, activation);
+        hipLaunchKernelGGL(aux_group_norm_chunk<1>, grid, block, 0, st, d_y, d_x, d_w, d_b, ws, len, gp.chunk,
+                           gp.chunks, groups * batch, channels, spatial, groups, eps, activation);
+        hipLaunchKernelGGL(aux_group_norm_chunk<2>, grid, block, 0, st, d_y, d_x, d_w, d_b, ws, len, gp.chunk,
+                           gp.chunks, groups * batch, channels, spatial, groups, eps, activation);
+        break;
+      }
+      launch_norm<2>(d_y, d_x, d_w, d_b, groups * batch, len, width, channels, spatial, groups, other_count, eps,
+                     activation, vec, st);
       break;
     }
     case 3:
     case 4:
       if (!d_w || other_count <= 0) return hb_invalid("hb_model_aux broadcast operand");
       if (mode == 3)
-        hipLaunchKernelGGL(aux_elementwise<3>, dim3(elementwise_grid(count)), block, 0, st, d_y, d_x, d_w, d_b,
-                           (int64_t)count, width, channels, spatial, other_count, activation);
+        launch_elementwise<3>(d_y, d_x, d_w, d_b, count, width, channels, spatial, other_count, activation, st);
       else
-        hipLaunchKernelGGL(aux_elementwise<4>, dim3(elementwise_grid(count)), block, 0, st, d_y, d_x, d_w, d_b,
-                           (int64_t)count, width, channels, spatial, other_count, activation);
+        launch_elementwise<4>(d_y, d_x, d_w, d_b, count, width, channels, spatial, other_count, activation, st);
       break;
     case 5:
-      hipLaunchKernelGGL(aux_elementwise<5>, dim3(elementwise_grid(count)), block, 0, st, d_y, d_x, d_w, d_b,
-                         (int64_t)count, width, channels, spatial, other_count, activation);
+      launch_elementwise<5>(d_y, d_x, d_w, d_b, count, width, channels, spatial, other_count, activation, st);
       break;
     case 6:
-      hipLaunchKernelGGL(aux_elementwise<6>, dim3(elementwise_grid(count)), block, 0, st, d_y, d_x, d_w, d_b,
-                         (int64_t)count, width, channels, spatial, other_count, activation);
+      launch_elementwise<6>(d_y, d_x, d_w, d_b, count, width, channels, spatial, other_count, activation, st);
       break;
     case 7:
-      hipLaunchKernelGGL(aux_elementwise<7>, dim3(elementwise_grid(count)), block, 0, st, d_y, d_x, d_w, d_b,
-                         (int64_t)count, width, channels, spatial, other_count, activation);
+      launch_elementwise<7>(d_y, d_x, d_w, d_b, count, width, channels, spatial, other_count, activation, st);
       break;
     case 8: {
       if ((int64_t)width * spatial * batch != count) return hb_invalid("hb_model_aux transpose shape");
@@ -255,8 +541,7 @@ extern "C" int hb_model_aux(float *d_y, const float *d_x, const float *d_w, cons
     }
     case 10:
       if (!d_w || !d_b) return hb_invalid("hb_model_aux mode 10 parameters");
-      hipLaunchKernelGGL(aux_elementwise<10>, dim3(elementwise_grid(count)), block, 0, st, d_y, d_x, d_w, d_b,
-                         (int64_t)count, width, channels, spatial, other_count, activation);
+      launch_elementwise<10>(d_y, d_x, d_w, d_b, count, width, channels, spatial, other_count, activation, st);
       break;
     case 11:
       if (!d_w || width % 2 || (groups != 1 && groups != batch)) return hb_invalid("hb_model_aux rope");
@@ -265,8 +550,7 @@ extern "C" int hb_model_aux(float *d_y, const float *d_x, const float *d_w, cons
       break;
     case 12:
       if (channels < 2 * width) return hb_invalid("hb_model_aux gated width");
-      hipLaunchKernelGGL(aux_elementwise<12>, dim3(elementwise_grid(count)), block, 0, st, d_y, d_x, d_w, d_b,
-                         (int64_t)count, width, channels, spatial, other_count, activation);
+      launch_elementwise<12>(d_y, d_x, d_w, d_b, count, width, channels, spatial, other_count, activation, st);
       break;
     case 13:
       if (!d_w || groups <= 0 || channels < 2 * width) return hb_invalid("hb_model_aux concat");
@@ -277,4 +561,11 @@ extern "C" int hb_model_aux(float *d_y, const float *d_x, const float *d_w, cons
       return hb_invalid("hb_model_aux mode");
   }
   return hb_check_launch("hb_model_aux");
+}
+
+extern "C" int hb_model_aux(float *d_y, const float *d_x, const float *d_w, const float *d_b, int mode, int count,
+                            int width, int channels, int spatial, int groups, int batch, int other_count,
+                            int activation, float eps, hb_stream s) {
+  return hb_model_aux_ws(d_y, d_x, d_w, d_b, mode, count, width, channels, spatial, groups, batch, other_count,
+                         activation, eps, nullptr, 0, s);
 }

@@ -29,8 +29,9 @@
 #define QTIMER_HZ 19200000.0
 
 static pthread_mutex_t g_exec_lock = PTHREAD_MUTEX_INITIALIZER;
-/* Device scratch slots: 0 W8A8 workspace, 1 raw accumulators or a realigned
- * bias, 2 realigned activations, 3 realigned output, 4 F16 split-K partials. */
+/* Device scratch slots: 0 W8A8 workspace (opcode 19: a realigned weight), 1 raw
+ * accumulators or a realigned bias, 2 realigned activations, 3 realigned
+ * output, 4 F16 split-K partials or opcode-19 group-norm partials. */
 enum { kScratchSlots = 5 };
 static void *g_scratch[kScratchSlots];
 static size_t g_scratch_size[kScratchSlots];
@@ -520,10 +521,17 @@ static int exec_model_aux(uint8_t *payload, size_t payload_size) {
     events_close(&ev);
     return -5;
   }
+  /* Group norms over few long groups split each group: partial sums in scratch. */
+  const size_t ws_bytes = hb_model_aux_workspace_bytes(p.mode, p.channels, p.spatial, p.groups, p.batch);
+  void *ws = ws_bytes ? htp_executor_scratch(4, ws_bytes) : NULL;
+  if (ws_bytes && !ws) {
+    events_close(&ev);
+    return -5;
+  }
   int hrc = hb_event_record(ev.e[0], s);
   if (!hrc)
-    hrc = hb_model_aux(y, x, w, b, p.mode, p.count, p.width, p.channels, p.spatial, p.groups, p.batch, p.other_count,
-                       p.activation, p.eps, s);
+    hrc = hb_model_aux_ws(y, x, w, b, p.mode, p.count, p.width, p.channels, p.spatial, p.groups, p.batch,
+                          p.other_count, p.activation, p.eps, ws, ws_bytes, s);
   if (!hrc) hrc = hb_event_record(ev.e[1], s);
   if (!hrc && (void *)y != (void *)out.dev) hrc = hb_memcpy_d2d(out.dev, y, out.bytes, s);
   if (!hrc) hrc = hb_stream_sync(s);

@@ -80,6 +80,9 @@ _SIGNATURES = {
                                 _c_void_p, _c_size_t, _c_void_p]),
     "hb_model_aux": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p] + [_c_int] * 9 + [ctypes.c_float,
                                                                                          _c_void_p]),
+    "hb_model_aux_workspace_bytes": (_c_size_t, [_c_int] * 5),
+    "hb_model_aux_ws": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p] + [_c_int] * 9 +
+                        [ctypes.c_float, _c_void_p, _c_size_t, _c_void_p]),
 }
 
 # Host-library symbols (session, executor, registry); bound when present.
@@ -502,12 +505,22 @@ def aux_params(out, inp, wgt, bias, mode, count, width, channels, spatial, group
                         other_count, activation, eps, elapsed)
 
 
+def model_aux_workspace_bytes(mode, channels, spatial, groups, batch):
+    return lib().hb_model_aux_workspace_bytes(mode, channels, spatial, groups, batch)
+
+
 def model_aux(y_dev, x_dev, w_dev, b_dev, mode, count, width, channels=1, spatial=1, groups=1, batch=1,
-              other_count=0, activation=0, eps=0.0, stream=None):
-    """hb_model_aux on device buffers (w_dev / b_dev may be None)."""
-    check(lib().hb_model_aux(y_dev.ptr, x_dev.ptr, w_dev.ptr if w_dev else None, b_dev.ptr if b_dev else None, mode,
-                             count, width, channels, spatial, groups, batch, other_count, activation, eps, stream),
-          "hb_model_aux")
+              other_count=0, activation=0, eps=0.0, stream=None, workspace=None):
+    """hb_model_aux on device buffers (w_dev / b_dev may be None), or
+    hb_model_aux_ws when a workspace buffer is given."""
+    w, b = (w_dev.ptr if w_dev else None), (b_dev.ptr if b_dev else None)
+    if workspace is None:
+        check(lib().hb_model_aux(y_dev.ptr, x_dev.ptr, w, b, mode, count, width, channels, spatial, groups, batch,
+                                 other_count, activation, eps, stream), "hb_model_aux")
+    else:
+        check(lib().hb_model_aux_ws(y_dev.ptr, x_dev.ptr, w, b, mode, count, width, channels, spatial, groups, batch,
+                                    other_count, activation, eps, workspace.ptr, workspace.nbytes, stream),
+              "hb_model_aux_ws")
 
 
 def matmul_params(out, act, wgt, m, k, n, with_elapsed=False):

@@ -179,6 +179,15 @@ int hb_model_aux(float *d_y, const float *d_x, const float *d_w, const float *d_
                  int channels, int spatial, int groups, int batch, int other_count, int activation, float eps,
                  hb_stream s);
 
+/* Workspace for hb_model_aux_ws: nonzero only for group norms (mode 2) with
+ * few long groups, which then split each group over many workgroups (three
+ * launches; the statistics are added in a fixed order, so the result does not
+ * depend on the split).  The workspace holds no state between calls. */
+size_t hb_model_aux_workspace_bytes(int mode, int channels, int spatial, int groups, int batch);
+int hb_model_aux_ws(float *d_y, const float *d_x, const float *d_w, const float *d_b, int mode, int count, int width,
+                    int channels, int spatial, int groups, int batch, int other_count, int activation, float eps,
+                    void *d_workspace, size_t workspace_bytes, hb_stream s);
+
 #ifdef __cplusplus
 }
 #endif

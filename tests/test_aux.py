@@ -265,14 +265,21 @@ def test_aux_validation_codes(bufs):
 # GPU parity
 # ---------------------------------------------------------------------------
 
-def run_aux(hip, x, w, b, out_init=None, **kw):
+def run_aux(hip, x, w, b, out_init=None, split=False, **kw):
+    """hb_model_aux (or, with split, hb_model_aux_ws with its workspace)."""
     count = kw["count"]
     xd = hip.DeviceBuffer.from_array(np.ascontiguousarray(x, np.float32))
     wd = None if w is None else hip.DeviceBuffer.from_array(np.ascontiguousarray(w, np.float32))
     bd = None if b is None else hip.DeviceBuffer.from_array(np.ascontiguousarray(b, np.float32))
     init = np.full(count, 3.5, np.float32) if out_init is None else out_init
     yd = hip.DeviceBuffer.from_array(init)
-    hip.model_aux(yd, xd, wd, bd, **kw)
+    ws = None
+    if split:
+        nbytes = hip.model_aux_workspace_bytes(kw["mode"], kw.get("channels", 1), kw.get("spatial", 1),
+                                               kw.get("groups", 1), kw.get("batch", 1))
+        assert nbytes > 0, kw
+        ws = hip.DeviceBuffer(nbytes)
+    hip.model_aux(yd, xd, wd, bd, workspace=ws, **kw)
     hip.sync()
     return yd.read(np.float32, count), init
 
@@ -286,6 +293,9 @@ NORM_CASES = [
     dict(mode=1, count=33 * 5, width=33, affine=False),
     dict(mode=2, batch=2, channels=64, groups=32, spatial=37, affine=True),
     dict(mode=2, batch=1, channels=128, groups=32, spatial=4096, affine=False, activation=1),
+    dict(mode=2, batch=1, channels=256, groups=32, spatial=16384, affine=True),  # 131072 per group: 3-pass kernel
+    dict(mode=0, count=8192 * 20, width=8192, affine=True),                    # 8 float4 per thread
+    dict(mode=1, count=2050 * 9, width=2050, affine=True),                     # width % 4 != 0
     dict(mode=9, batch=2, spatial=77, width=1536, per_batch=True),
     dict(mode=9, batch=1, spatial=300, width=3072, per_batch=False, activation=1),
 ]
@@ -326,6 +336,24 @@ def test_aux_norms_gpu(hip, orc, case):
     # untouched tail (partial rows) keeps its contents
     covered = (count // kw["width"]) * kw["width"] if mode <= 1 else count
     assert (got[covered:] == init[covered:]).all()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("batch,channels,groups,spatial,affine,act", [
+    (1, 512, 32, 4096, True, 0), (2, 128, 32, 16384, False, 1), (1, 256, 32, 16388, True, 0),
+    (1, 64, 8, 65536 * 2, True, 0)])
+def test_aux_group_norm_split_gpu(hip, orc, batch, channels, groups, spatial, affine, act):
+    """Group norm split over many workgroups per group (hb_model_aux_ws)."""
+    count = batch * channels * spatial
+    x = rng_normal(count, 150, 2.0) + 0.75
+    w = rng_normal(channels, 151) if affine else None
+    b = rng_normal(channels, 152) if affine else None
+    kw = dict(mode=2, count=count, width=spatial, channels=channels, spatial=spatial, groups=groups, batch=batch,
+              other_count=channels if affine else 0, activation=act, eps=1e-5)
+    got, init = run_aux(hip, x, w, b, split=True, **kw)
+    want = orc.model_aux(x, w, b, out=init, **kw)
+    rtol, atol = (ACT_RTOL, ACT_ATOL) if act else (NORM_RTOL, NORM_ATOL)
+    np.testing.assert_allclose(got, want, rtol=rtol, atol=atol)
 
 
 @pytest.mark.gpu
