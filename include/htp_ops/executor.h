@@ -6,6 +6,7 @@
  *     opcode 15 (W8A8)  reference src/dsp/op_executor.cc:314-353
  *     opcode 16 (F16+epilogue) reference src/dsp/op_executor.cc:446-471
  *     opcode 1  (F16)   reference src/dsp/op_executor.cc:473-540
+ *     opcode 19 (model auxiliary f32 ops) reference src/dsp/op_executor.cc:371-404
  *
  * Return codes (unchanged from the reference):
  *   opcode 15: -1 payload size / shape / profile mode, -2 unmapped buffer,
@@ -13,6 +14,8 @@
  *              -12 CPU-control batch overflow.
  *   opcode 16: -1 validation or unmapped buffer, -10/-11/-12 kernel argument errors.
  *   opcode 1:  -1 short payload, -2 unmapped buffer, -3 misaligned buffer (128 B).
+ *   opcode 19: -1 payload size / validation / unmapped buffer, -40 a norm with
+ *              no whole row (the reference's empty worker pool).
  *   other opcodes: HTP_OPS_E_UNSUPPORTED (the reference silently returns 0).
  *   A GPU runtime failure while executing a valid request returns -5.
  * All argument checks happen before any GPU work is queued.
