@@ -283,7 +283,7 @@ def decode_case(m, k, n, steps, warmup, rotate):
             "graph_us_per_call": round(r["graph_ms_per_step"] * 1e3, 3)}
 
 
-def all_configs(steps, warmup):
+def all_configs(steps, warmup, with_cpu=False):
     out = {}
     for name, (m, k, n, outl, sc) in {
             "C1_77x768x3072": (77, 768, 3072, 0.0, (1e-4, 1e-3)),
@@ -299,11 +299,11 @@ def all_configs(steps, warmup):
         for k, n in ((4096, 14336), (14336, 4096)):
             out[f"C5_M{m}_{k}x{n}"] = decode_case(m, k, n, steps, warmup, 6)
     out["C2_f16_text_mlp_77x768x3072x768"] = f16_mlp_case(steps, warmup)
-    out["opcode19_aux"] = aux_cases(steps, warmup)
+    out["opcode19_aux"] = aux_cases(steps, warmup, with_cpu=with_cpu)
     return out
 
 
-def aux_cases(steps, warmup, rotate=4):
+def aux_cases(steps, warmup, rotate=4, with_cpu=True):
     """Opcode-19 model auxiliary ops at DiT/VAE shapes (hb_model_aux on HBM
     tensors, rotated copies, stream-ordered after clock settling).  Bytes are
     the algorithmic ones: every input value read once, every output written
@@ -335,10 +335,15 @@ def aux_cases(steps, warmup, rotate=4):
     out = {}
     for name, (kw, nx, nw, nb, ny) in cases.items():
         sets = []
-        for _ in range(rotate):
-            x = hip.DeviceBuffer.from_array(rng.standard_normal(nx, dtype=np.float32))
-            w = hip.DeviceBuffer.from_array(rng.standard_normal(nw, dtype=np.float32) * 0.1) if nw else None
-            b = hip.DeviceBuffer.from_array(rng.standard_normal(nb, dtype=np.float32) * 0.1) if nb else None
+        for r in range(rotate):
+            hx = rng.standard_normal(nx, dtype=np.float32)
+            hw = rng.standard_normal(nw, dtype=np.float32) * 0.1 if nw else None
+            hb = rng.standard_normal(nb, dtype=np.float32) * 0.1 if nb else None
+            if r == 0:
+                host = (hx, hw, hb)
+            x = hip.DeviceBuffer.from_array(hx)
+            w = hip.DeviceBuffer.from_array(hw) if nw else None
+            b = hip.DeviceBuffer.from_array(hb) if nb else None
             y = hip.DeviceBuffer(ny * 4)
             sets.append((x, w, b, y))
 
@@ -369,6 +374,15 @@ def aux_cases(steps, warmup, rotate=4):
         nbytes = 4 * (nx + nw + nb + ny)
         out[name] = {"mode": kw["mode"], "us": round(us, 2), "gbps": round(nbytes / us * 1e-3, 1),
                      "frac_hbm": round(nbytes / us * 1e-3 / PEAK_HBM_GBPS, 4)}
+        if with_cpu:
+            # the oracle's single-threaded restatement on the same values, once
+            sys.path.insert(0, os.path.join(REPO, "oracle"))
+            import oracle
+            t0 = time.perf_counter()
+            oracle.model_aux(*host, **kw)
+            cpu_us = (time.perf_counter() - t0) * 1e6
+            out[name]["cpu_baseline"] = {"us": round(cpu_us, 1), "gbps": round(nbytes / cpu_us * 1e-3, 2),
+                                         "cores": 1, "kind": "port"}
         for st in sets:
             for buf in st:
                 if buf is not None:
@@ -525,7 +539,7 @@ def main():
         print(json.dumps({"C2_f16_text_mlp_77x768x3072x768": f16_mlp_case(args.steps, args.warmup)}), flush=True)
         return
     if args.config == "aux":
-        print(json.dumps({"opcode19_aux": aux_cases(args.steps, args.warmup)}), flush=True)
+        print(json.dumps({"opcode19_aux": aux_cases(args.steps, args.warmup, with_cpu=not args.no_cpu)}), flush=True)
         return
     m, k, n = HEADLINE
     r = run_w8a8(m, k, n, args.steps, args.warmup, args.rotate, outliers=0.01)
@@ -564,7 +578,7 @@ def main():
     line["decode_m1"] = decode_case(1, 4096, 14336, args.steps, args.warmup, 6)
     line["e2e_opcode15"] = e2e_opcode15(m, k, n)
     if args.config == "all":
-        line["configs"] = all_configs(args.steps, args.warmup)
+        line["configs"] = all_configs(args.steps, args.warmup, with_cpu=not args.no_cpu)
     if not args.no_cpu and rank == 0:
         line["cpu_baseline"] = cpu_baseline(m, k, n)
     else:
