@@ -497,6 +497,7 @@ extern "C" int hb_model_aux_ws(float *d_y, const float *d_x, const float *d_w, c
     }
     case 2: {
       if (groups <= 0 || channels % groups) return hb_invalid("hb_model_aux groups");
+      if ((int64_t)batch * channels * spatial > count) return hb_invalid("hb_model_aux group norm extent");
       const int len = spatial * (channels / groups);
       const bool vec = len % 4 == 0 && aligned16(d_x) && aligned16(d_y);
       const GroupPlan gp = group_plan(groups * batch, len);

@@ -465,6 +465,10 @@ static int exec_model_aux(uint8_t *payload, size_t payload_size) {
   const int has_w = p.weight.fd >= 0, has_b = p.bias.fd >= 0;
   if (p.mode == 8 && wsb != p.count) return -1;
   if (p.mode == 2 && (p.groups <= 0 || p.channels % p.groups)) return -1;
+  /* Deviation: the reference does not check that a group norm's batch x
+   * channels x spatial values lie inside `count` (its kernel would read past
+   * the input); such a request is rejected here. */
+  if (p.mode == 2 && (int64_t)p.batch * p.channels * p.spatial > p.count) return -1;
   if (p.mode == 12 && (wsb != p.count || has_w || has_b || p.channels < (int64_t)2 * p.width ||
                        (p.activation != 0 && p.activation != 1)))
     return -1;

@@ -225,6 +225,7 @@ def test_aux_validation_codes(bufs):
         dict(count=0), dict(mode=-1), dict(mode=14), dict(width=0), dict(channels=0), dict(spatial=0), dict(batch=0),
         dict(mode=8, count=63, width=8, spatial=8),
         dict(mode=2, groups=0), dict(mode=2, channels=6, groups=4),
+        dict(mode=2, count=64, channels=8, groups=4, spatial=16),  # 8 x 16 values > count (checked here only)
         dict(mode=12, count=64, width=16, spatial=4, channels=31),
         dict(mode=12, count=64, width=16, spatial=4, channels=32, activation=2),
         dict(mode=12, count=60, width=16, spatial=4, channels=32),
