@@ -160,10 +160,14 @@ def test_w8a8_every_tile_shape_bit_exact(hip, orc, tile, m, k, n):
 
 
 # One row: hb_w8a8_linear quantizes inside the weight-streaming kernel
-# (one variant per kp range: <= 4096, <= 8192, <= 16384).
+# (one variant per kp range: <= 4096, <= 8192, <= 16384; for kp <= 4096 and
+# at least one block per CU, two column blocks per workgroup).
 DECODE_FUSED_SHAPES = [
     (1, 32, 64),       # smallest K (k % 64 == 32)
-    (1, 4096, 14336),  # BASELINE decode gate/up shape
+    (1, 4096, 14336),  # BASELINE decode gate/up shape (two blocks per workgroup)
+    (1, 4064, 14272),  # two blocks per workgroup, row shorter than the threads
+    (1, 3104, 8192),   # two blocks per workgroup, 49 of 64 tiles per block present
+    (1, 4096, 12288),  # one block per workgroup (three per CU)
     (1, 14336, 4096),  # BASELINE decode down shape
     (1, 4160, 256),    # just past the first variant
     (1, 8192, 512),
