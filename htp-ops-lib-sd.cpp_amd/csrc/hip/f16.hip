@@ -46,6 +46,67 @@ __global__ __launch_bounds__(256) void f16_prepack(uint4 *__restrict__ packed, c
 }
 
 // ---------------------------------------------------------------------------
+// Dequantizing prepack (opcodes 2/3/4): Q4_0 / Q8_0 / IQ4_NL super-blocks of
+// 256 weights -> the same MFMA tile image as f16_prepack, so the GEMM is the
+// F16 one.  Super-block b holds positions [256b, 256b + 256) of the permuted
+// F16 layout (reference src/dsp/ops/mat_mul.c:1700-1712).  Position j uses
+// fp16 scale j/32.  Q8_0: quant byte j.  Q4_0 / IQ4_NL: the four 64-value
+// vectors of a super-block come from the low nibbles of the even bytes, the
+// low nibbles of the odd bytes, then the high nibbles of the even and of the
+// odd bytes (vlut16 splits even and odd source bytes, :401-427); Q4_0 values
+// are nibble - 8, IQ4_NL values ggml's code book (:30-37).  value * scale is
+// exact in fp32 and rounded once to fp16.
+// ---------------------------------------------------------------------------
+
+__constant__ int8_t kIq4NlValues[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
+__device__ inline uint16_t qk0_value(const uint8_t *__restrict__ blk, int j, int type) {
+  const int g = j / 32;
+  const uint16_t sbits = (uint16_t)(blk[2 * g] | (blk[2 * g + 1] << 8));
+  const float scale = (float)__builtin_bit_cast(_Float16, sbits);
+  int q;
+  if (type == HB_GGML_Q8_0) {
+    q = (int8_t)blk[16 + j];
+  } else {
+    const int v = j / 64, lane = j % 64;
+    const uint8_t byte = blk[16 + 2 * lane + (v & 1)];
+    const int nib = v < 2 ? (byte & 15) : (byte >> 4);
+    q = type == HB_GGML_IQ4_NL ? (int)kIq4NlValues[nib] : nib - 8;
+  }
+  float v = __fmul_rn((float)q, scale);
+  // Keeps the product and the conversion apart: fused, they become
+  // v_fma_mix(q, scale, +0), which turns a -0 product (code 0, negative
+  // scale) into +0.
+  asm volatile("" : "+v"(v));
+  return __builtin_bit_cast(uint16_t, (_Float16)v);
+}
+
+__global__ __launch_bounds__(256) void qk0_prepack(uint4 *__restrict__ packed, const uint8_t *__restrict__ blocks,
+                                                  int k, int n, int type, int block_bytes) {
+  const size_t slots = (size_t)n * (size_t)k / 8u;
+  const int kblocks = k / 32;
+  for (size_t slot = (size_t)blockIdx.x * blockDim.x + threadIdx.x; slot < slots;
+       slot += (size_t)gridDim.x * blockDim.x) {
+    const size_t blk = slot / 64u;
+    const int lane = (int)(slot % 64u);
+    const int nb = (int)(blk / (size_t)kblocks), kb = (int)(blk % (size_t)kblocks);
+    const int col = nb * 16 + lane % 16;
+    const int k0 = kb * 32 + (lane / 16) * 8;
+    uint32_t w[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int kk = k0 + 2 * g;  // even: (kk, kk+1) are adjacent in the permuted layout
+      const size_t idx = ((size_t)(col / 32) * (size_t)kblocks + (size_t)(kk / 32)) * 1024u +
+                         (size_t)((kk % 32) / 2) * 64u + (size_t)(col % 32) * 2u;
+      const uint8_t *sb = blocks + (idx / 256u) * (size_t)block_bytes;
+      const int j = (int)(idx % 256u);
+      w[g] = (uint32_t)qk0_value(sb, j, type) | ((uint32_t)qk0_value(sb, j + 1, type) << 16);
+    }
+    packed[slot] = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Epilogue activations (reference src/dsp/ops/mat_mul.c:788-826): stable
 // sigmoid with e = 2^max(-|a|*log2(e), -126).
 // ---------------------------------------------------------------------------
@@ -388,6 +449,33 @@ int hb_f16_prepack(uint16_t *d_packed, const uint16_t *d_permuted, int k, int n,
   return hb_check_launch("f16_prepack");
 }
 
+size_t hb_qk0_block_bytes(int type) {
+  switch (type) {
+    case HB_GGML_Q4_0:
+    case HB_GGML_IQ4_NL: return 16u + 128u;
+    case HB_GGML_Q8_0: return 16u + 256u;
+    default: return 0u;
+  }
+}
+
+size_t hb_qk0_weight_bytes(int k, int n, int type) {
+  if (k <= 0 || n <= 0 || k % 32 || n % 32) return 0;
+  return (size_t)k * (size_t)n / 256u * hb_qk0_block_bytes(type);
+}
+
+int hb_qk0_prepack(uint16_t *d_packed, const uint8_t *d_blocks, int k, int n, int type, hb_stream s) {
+  if (!d_packed || !d_blocks) return hb_invalid("hb_qk0_prepack null pointer");
+  if (k < 32 || k % 32 || n < 32 || n % 32) return hb_invalid("hb_qk0_prepack shape");
+  const size_t bb = hb_qk0_block_bytes(type);
+  if (!bb) return hb_invalid("hb_qk0_prepack type");
+  if (!aligned(d_packed, 16)) return hb_invalid("hb_qk0_prepack alignment");
+  const size_t slots = (size_t)n * k / 8u;
+  const int grid = (int)((slots + 255) / 256 < 65536 ? (slots + 255) / 256 : 65536);
+  hipLaunchKernelGGL(qk0_prepack, dim3(grid), dim3(256), 0, hb_resolve_stream(s), (uint4 *)d_packed, d_blocks, k, n,
+                     type, (int)bb);
+  return hb_check_launch("qk0_prepack");
+}
+
 size_t hb_f16_workspace_bytes(int m, int k, int n) {
   if (m < 1 || m > 128 || k < 32 || n < 32) return 0;
   // splits <= ceil(kblocks / 4) (one k-block per wave at the least)
@@ -405,9 +493,15 @@ int hb_f16_gemm_ws(float *d_y, const float *d_x, const uint16_t *d_packed, const
     return hb_invalid("hb_f16_gemm alignment");
   hipStream_t st = hb_resolve_stream(s);
   const size_t need = hb_f16_workspace_bytes(m, k, n);
-  const long long tiled_wgs = ((m + 31) / 32) * (long long)((n + 31) / 32);
+  // Tiled variant by output size; the split-K path takes over when that grid
+  // leaves CUs idle, and for m <= 16, where a tile's rows are mostly padding
+  // (measured at k=4096, n=14336: m=1 65 -> 28 us; 77x14336x4096: 264 -> 80 us).
+  const long long big = ((m + 127) / 128) * (long long)((n + 127) / 128);
+  const long long mid = ((m + 63) / 64) * (long long)((n + 63) / 64);
+  const long long small = ((m + 31) / 32) * (long long)((n + 31) / 32);
+  const long long tiled_wgs = big >= 256 ? big : mid >= 128 ? mid : small;
   if (d_workspace && need && workspace_bytes >= need && aligned(d_workspace, 16) &&
-      tiled_wgs < compute_units()) {
+      (tiled_wgs < compute_units() || m <= 16)) {
     int splits = 1, kpw = 1;
     skinny_plan(k, n, splits, kpw);
     const int cols = skinny_cols(n);
@@ -424,8 +518,6 @@ int hb_f16_gemm_ws(float *d_y, const float *d_x, const uint16_t *d_packed, const
                        splits);
     return hb_check_launch("f16_skinny_epilogue");
   }
-  const long long big = ((m + 127) / 128) * (long long)((n + 127) / 128);
-  const long long mid = ((m + 63) / 64) * (long long)((n + 63) / 64);
   if (big >= 256) {
     hipLaunchKernelGGL((f16_gemm_tiles<128, 128, 2, 2>), dim3((int)big), dim3(256), 0, st, d_y, d_x, d_packed, d_bias,
                        m, k, n, channels, mode);
@@ -433,9 +525,8 @@ int hb_f16_gemm_ws(float *d_y, const float *d_x, const uint16_t *d_packed, const
     hipLaunchKernelGGL((f16_gemm_tiles<64, 64, 2, 2>), dim3((int)mid), dim3(256), 0, st, d_y, d_x, d_packed, d_bias,
                        m, k, n, channels, mode);
   } else {
-    const int grid = ((m + 31) / 32) * ((n + 31) / 32);
-    hipLaunchKernelGGL((f16_gemm_tiles<32, 32, 2, 2>), dim3(grid), dim3(256), 0, st, d_y, d_x, d_packed, d_bias, m,
-                       k, n, channels, mode);
+    hipLaunchKernelGGL((f16_gemm_tiles<32, 32, 2, 2>), dim3((int)small), dim3(256), 0, st, d_y, d_x, d_packed, d_bias,
+                       m, k, n, channels, mode);
   }
   return hb_check_launch("f16_gemm_tiles");
 }

@@ -315,15 +315,15 @@ static uintptr_t primary_address(const htp_view *v) {
 }
 
 /* Shared F16 compute after validation.  Returns 0 or a negative code. */
-static int run_f16(htp_view *out, htp_view *act, htp_view *wgt, htp_view *bias, int m, int k, int n, int channels,
-                   int mode, int32_t *elapsed_us) {
+static int run_f16(int kind, htp_view *out, htp_view *act, htp_view *wgt, htp_view *bias, int m, int k, int n,
+                   int channels, int mode, int32_t *elapsed_us) {
   if (htp_executor_ensure_device() != 0) return -5;
   if (materialize(out) || materialize(act) || materialize(wgt) || (bias && materialize(bias))) return -5;
   hb_stream s = htp_executor_stream();
   void *packed = NULL;
   int built = 0;
   const double t_w0 = now_seconds();
-  int rc = htp_weight_cache_get(HTP_WEIGHT_F16, wgt, k, n, weight_signature(wgt), &packed, &built, s);
+  int rc = htp_weight_cache_get(kind, wgt, k, n, weight_signature(wgt), &packed, &built, s);
   if (rc) return rc;
   const double t_w1 = now_seconds();
   if (stage_in(act, s)) return -5;
@@ -387,7 +387,8 @@ static int exec_f16_epilogue(uint8_t *payload, size_t payload_size) {
    * (reference src/dsp/ops/mat_mul.c:947-949). */
   if ((primary_address(&out) | primary_address(&act) | primary_address(&wgt)) & 127u) return -12;
   int32_t elapsed = 0;
-  rc = run_f16(&out, &act, &wgt, p.bias.fd >= 0 ? &bias : NULL, p.m, p.k, p.n, p.channels, p.mode, &elapsed);
+  rc = run_f16(HTP_WEIGHT_F16, &out, &act, &wgt, p.bias.fd >= 0 ? &bias : NULL, p.m, p.k, p.n, p.channels, p.mode,
+               &elapsed);
   if (rc) return rc;
   memcpy(payload + offsetof(struct F16EpilogueParams, elapsed_us), &elapsed, sizeof(elapsed));
   return 0;
@@ -410,7 +411,7 @@ static int exec_matmul_params(const struct MatMulParams *p, int32_t *elapsed_us,
     *act_hash = 0;
     if (act.host) *act_hash = htp_fnv1a64(act.host, act.bytes);
   }
-  rc = run_f16(&out, &act, &wgt, NULL, m, k, n, n, 0, elapsed_us);
+  rc = run_f16(HTP_WEIGHT_F16, &out, &act, &wgt, NULL, m, k, n, n, 0, elapsed_us);
   if (rc) return rc;
   if (out_hash) {
     *out_hash = 0;
@@ -428,6 +429,33 @@ static int exec_matmul(uint8_t *payload, size_t payload_size) {
   if (rc == 0 && payload_size >= sizeof(struct MatMulProfileParams))
     memcpy(payload + offsetof(struct MatMulProfileParams, elapsed_us), &elapsed, sizeof(elapsed));
   return rc;
+}
+
+/* Opcodes 2/3/4: Q4_0 / Q8_0 / IQ4_NL super-blocks dequantized into the F16
+ * image (once per weight buffer, cached), then the F16 GEMM with mode 0 and
+ * no bias.  Reference src/dsp/op_executor.cc:771-800 (payload, buffer sizes
+ * m*n*4, m*k*4, k*n/256*block) and src/dsp/ops/mat_mul.c:1601-1617 (-1 for
+ * a missing buffer, a zero dimension, k or n not a multiple of 32, or an
+ * output, activation or weight address not 128-byte aligned). */
+static int exec_matmul_qk0(uint8_t *payload, size_t payload_size, int kind, int type) {
+  if (payload_size < sizeof(struct MatMulParams)) return -1;
+  struct MatMulParams p;
+  memcpy(&p, payload, sizeof(p));
+  const int m = p.m, k = p.k, n = p.n;
+  if (m <= 0 || k <= 0 || n <= 0 || k % 32 || n % 32) return -1;
+  size_t out_size, act_size;
+  const size_t weight_size = hb_qk0_weight_bytes(k, n, type);
+  if (!checked_mul((size_t)m, (size_t)n * sizeof(float), &out_size) ||
+      !checked_mul((size_t)m, (size_t)k * sizeof(float), &act_size) || !weight_size)
+    return -1;
+  htp_view out, act, wgt;
+  int rc = resolve(&p.output, out_size, &out, -1);
+  if (!rc) rc = resolve(&p.activation, act_size, &act, -1);
+  if (!rc) rc = resolve(&p.weight, weight_size, &wgt, -1);
+  if (rc) return rc;
+  if ((primary_address(&out) | primary_address(&act) | primary_address(&wgt)) & 127u) return -1;
+  int32_t elapsed = 0;
+  return run_f16(kind, &out, &act, &wgt, NULL, m, k, n, n, 0, &elapsed);
 }
 
 /* Direct (non-mailbox) opcode-1 entry used by htp_ops_mat_mul_permuted_w16a32[_trace]. */
@@ -563,6 +591,15 @@ int execute_op_simple(struct OpComputeRequest *req, size_t req_size) {
     case HTP_OPS_MAT_MUL_NATIVE_W8A8: rc = exec_w8a8(payload, payload_size); break;
     case HTP_OPS_MAT_MUL_F16_EPILOGUE: rc = exec_f16_epilogue(payload, payload_size); break;
     case HTP_OPS_MAT_MUL_PERMUTED_W16A32: rc = exec_matmul(payload, payload_size); break;
+    case HTP_OPS_MAT_MUL_PERMUTED_W4D16A32:
+      rc = exec_matmul_qk0(payload, payload_size, HTP_WEIGHT_Q4_0, HB_GGML_Q4_0);
+      break;
+    case HTP_OPS_MAT_MUL_PERMUTED_W8D16A32:
+      rc = exec_matmul_qk0(payload, payload_size, HTP_WEIGHT_Q8_0, HB_GGML_Q8_0);
+      break;
+    case HTP_OPS_MAT_MUL_PERMUTED_W4D16A32_IQ4_NL:
+      rc = exec_matmul_qk0(payload, payload_size, HTP_WEIGHT_IQ4_NL, HB_GGML_IQ4_NL);
+      break;
     case HTP_OPS_MODEL_AUX_F32: rc = exec_model_aux(payload, payload_size); break;
     default: rc = HTP_OPS_E_UNSUPPORTED; break;
   }

@@ -37,7 +37,14 @@ void htp_registry_touch(int fd);
 
 /* ---- prepacked weight cache (registry.c) -------------------------------- */
 
-enum { HTP_WEIGHT_W8A8 = 1, HTP_WEIGHT_F16 = 2 };
+enum {
+  HTP_WEIGHT_W8A8 = 1,
+  HTP_WEIGHT_F16 = 2,
+  /* quantized super-blocks of opcodes 2/3/4, dequantized into the F16 image */
+  HTP_WEIGHT_Q4_0 = 3,
+  HTP_WEIGHT_Q8_0 = 4,
+  HTP_WEIGHT_IQ4_NL = 5
+};
 
 /* Returns the device image of a prepacked weight for the given source view,
  * building it on a miss.  `sig` identifies the source contents (header bytes /

@@ -350,6 +350,16 @@ static size_t packed_bytes(int kind, int k, int n) {
   return kind == HTP_WEIGHT_W8A8 ? hb_w8a8_packed_bytes(k, n) : hb_f16_packed_bytes(k, n);
 }
 
+/* ggml type of a quantized-weight cache kind, 0 for the others. */
+static int qk0_type(int kind) {
+  switch (kind) {
+    case HTP_WEIGHT_Q4_0: return HB_GGML_Q4_0;
+    case HTP_WEIGHT_Q8_0: return HB_GGML_Q8_0;
+    case HTP_WEIGHT_IQ4_NL: return HB_GGML_IQ4_NL;
+    default: return 0;
+  }
+}
+
 int htp_weight_cache_get(int kind, const htp_view *src, int k, int n, uint64_t sig, void **packed, int *built,
                          hb_stream s) {
   *packed = NULL;
@@ -397,8 +407,12 @@ int htp_weight_cache_get(int kind, const htp_view *src, int k, int n, uint64_t s
     hb_free(tmp);
     return -5;
   }
-  rc = kind == HTP_WEIGHT_W8A8 ? hb_w8a8_prepack(img, dsrc, k, n, s)
-                               : hb_f16_prepack((uint16_t *)img, (const uint16_t *)dsrc, k, n, s);
+  if (kind == HTP_WEIGHT_W8A8)
+    rc = hb_w8a8_prepack(img, dsrc, k, n, s);
+  else if (qk0_type(kind))
+    rc = hb_qk0_prepack((uint16_t *)img, dsrc, k, n, qk0_type(kind), s);
+  else
+    rc = hb_f16_prepack((uint16_t *)img, (const uint16_t *)dsrc, k, n, s);
   if (rc == HB_OK) rc = hb_stream_sync(s);
   hb_free(tmp);
   if (rc != HB_OK) {

@@ -72,6 +72,9 @@ _SIGNATURES = {
     "hb_w8a8_force_tile": (_c_int, [_c_int]),
     # F16
     "hb_f16_packed_bytes": (_c_size_t, [_c_int, _c_int]),
+    "hb_qk0_block_bytes": (_c_size_t, [_c_int]),
+    "hb_qk0_weight_bytes": (_c_size_t, [_c_int, _c_int, _c_int]),
+    "hb_qk0_prepack": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_void_p]),
     "hb_f16_prepack": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
     "hb_f16_gemm": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int,
                              _c_void_p]),
@@ -333,6 +336,20 @@ def f16_prepack(permuted_dev, k, n):
     return packed
 
 
+GGML_Q4_0, GGML_Q8_0, GGML_IQ4_NL = 2, 8, 20
+
+
+def qk0_weight_bytes(k, n, wtype):
+    return lib().hb_qk0_weight_bytes(k, n, wtype)
+
+
+def qk0_prepack(blocks_dev, k, n, wtype):
+    """Quantized super-blocks (device) -> the hb_f16_prepack image (hb_qk0_prepack)."""
+    packed = DeviceBuffer(lib().hb_f16_packed_bytes(k, n))
+    check(lib().hb_qk0_prepack(packed.ptr, blocks_dev.ptr, k, n, wtype, None), "hb_qk0_prepack")
+    return packed
+
+
 def f16_workspace_bytes(m, k, n):
     return lib().hb_f16_workspace_bytes(m, k, n)
 
@@ -466,6 +483,9 @@ def permute_f16(w_kn_bits):
 import struct as _struct
 
 OP_MAT_MUL_PERMUTED_W16A32 = 1
+OP_MAT_MUL_PERMUTED_W4D16A32 = 2
+OP_MAT_MUL_PERMUTED_W8D16A32 = 3
+OP_MAT_MUL_PERMUTED_W4D16A32_IQ4_NL = 4
 OP_MAT_MUL_NATIVE_W8A8 = 15
 OP_MAT_MUL_F16_EPILOGUE = 16
 E_UNSUPPORTED = -95

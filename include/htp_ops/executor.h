@@ -7,6 +7,8 @@
  *     opcode 16 (F16+epilogue) reference src/dsp/op_executor.cc:446-471
  *     opcode 1  (F16)   reference src/dsp/op_executor.cc:473-540
  *     opcode 19 (model auxiliary f32 ops) reference src/dsp/op_executor.cc:371-404
+ *     opcodes 2/3/4 (Q4_0 / Q8_0 / IQ4_NL weights, F16 GEMM)
+ *                       reference src/dsp/op_executor.cc:771-800
  *
  * Return codes (unchanged from the reference):
  *   opcode 15: -1 payload size / shape / profile mode, -2 unmapped buffer,
@@ -14,6 +16,8 @@
  *              -12 CPU-control batch overflow.
  *   opcode 16: -1 validation or unmapped buffer, -10/-11/-12 kernel argument errors.
  *   opcode 1:  -1 short payload, -2 unmapped buffer, -3 misaligned buffer (128 B).
+ *   opcodes 2/3/4: -1 short payload, unmapped buffer, zero dimension, k or n
+ *              not a multiple of 32, misaligned buffer (128 B).
  *   opcode 19: -1 payload size / validation / unmapped buffer, -40 a norm with
  *              no whole row (the reference's empty worker pool).
  *   other opcodes: HTP_OPS_E_UNSUPPORTED (the reference silently returns 0).

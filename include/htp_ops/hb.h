@@ -15,6 +15,10 @@
  *       (hmx_mat_mul_f16_epilogue, hmx_mat_mul_permuted_w16a32)
  *   hb_f16_prepack    no reference counterpart (reference copies the permuted
  *       weight into VTCM per call, src/dsp/ops/mat_mul.c:157-244)
+ *   hb_qk0_prepack    replaces the per-call dequantization of Q4_0 / Q8_0 /
+ *       IQ4_NL super-blocks (dequantize_permuted_weight_chunk_qk_0_to_fp16_hvx,
+ *       src/dsp/ops/mat_mul.c:330-588) feeding hmx_mat_mul_permuted_qk_0_d16a32
+ *       (:1601-1720); the GEMM is then hb_f16_gemm
  *
  * Status codes: 0 success, HB_E_INVAL bad argument, HB_E_NODEV no usable GPU,
  * HB_E_HIP a HIP runtime error (text in hb_last_error()), HB_E_NOMEM.
@@ -138,6 +142,17 @@ int hb_w8a8_planes_from_raw(uint8_t *d_out, const int32_t *d_raw, int m, int n, 
 size_t hb_f16_packed_bytes(int k, int n);
 int hb_f16_prepack(uint16_t *d_packed, const uint16_t *d_permuted, int k, int n, hb_stream s);
 
+/* Quantized weights of opcodes 2/3/4 (ggml type ids, reference
+ * include/dsp/quants.h:33-54): super-blocks of 256 weights, 8 fp16 scales then
+ * 128 nibble bytes (Q4_0, IQ4_NL; 144 bytes) or 256 int8 (Q8_0; 272 bytes),
+ * covering consecutive positions of the permuted fp16 layout.  hb_qk0_prepack
+ * dequantizes them into the hb_f16_prepack image (value * scale rounded once
+ * to fp16), so the product then runs through hb_f16_gemm. */
+enum { HB_GGML_Q4_0 = 2, HB_GGML_Q8_0 = 8, HB_GGML_IQ4_NL = 20 };
+size_t hb_qk0_block_bytes(int type);           /* 0 for an unknown type */
+size_t hb_qk0_weight_bytes(int k, int n, int type);
+int hb_qk0_prepack(uint16_t *d_packed, const uint8_t *d_blocks, int k, int n, int type, hb_stream s);
+
 /*
  * y = epilogue(fp16(fp16(x) @ W)); x f32 [m][k]; bias f32[channels] or NULL.
  * mode 0: + bias; 1: + bias, GELU (tanh form); 2: + bias, QuickGELU;
@@ -151,10 +166,11 @@ int hb_f16_gemm(float *d_y, const float *d_x, const uint16_t *d_packed, const fl
 size_t hb_f16_workspace_bytes(int m, int k, int n);
 
 /* hb_f16_gemm with a workspace: for m <= 128, a workspace of at least
- * hb_f16_workspace_bytes, and a shape whose 32x32 output tiles number fewer
- * than the device's CUs, K is split across workgroups and the partial sums
- * are added in a fixed order before the fp16 readout rounding and the
- * epilogue (two kernels); otherwise identical to hb_f16_gemm. */
+ * hb_f16_workspace_bytes, and either m <= 16 or a shape whose output tiles
+ * (of the size hb_f16_gemm would use) number fewer than the device's CUs, K
+ * is split across workgroups and the partial sums are added in a fixed order
+ * before the fp16 readout rounding and the epilogue (two kernels); otherwise
+ * identical to hb_f16_gemm. */
 int hb_f16_gemm_ws(float *d_y, const float *d_x, const uint16_t *d_packed, const float *d_bias, int m, int k, int n,
                    int channels, int mode, void *d_workspace, size_t workspace_bytes, hb_stream s);
 

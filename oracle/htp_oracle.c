@@ -655,6 +655,71 @@ void oracle_f16_gemm_epilogue(float *y, const float *x, const uint16_t *permuted
 }
 
 /* ------------------------------------------------------------------------ */
+/* Dequantizing GEMM (opcodes 2/3/4): Q4_0, Q8_0, IQ4_NL super-blocks        */
+/* block formats: reference include/dsp/quants.h:16-31 (my_block_q4_0,      */
+/* my_block_q8_0); dequantization: src/dsp/ops/mat_mul.c:330-429 (Q4_0,     */
+/* IQ4_NL) and :431-530 (Q8_0); driver :1601-1720; executor                 */
+/* src/dsp/op_executor.cc:771-800                                           */
+/* ------------------------------------------------------------------------ */
+
+/* ggml's IQ4_NL code book (reference mat_mul.c:34-37, ggml's published
+ * kvalues_iq4nl). */
+static const int8_t k_iq4nl_values[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
+                                          1,    13,   25,  38,  53,  69,  89,  113};
+
+size_t oracle_qk0_block_bytes(int type) {
+  switch (type) {
+    case ORACLE_GGML_Q4_0:
+    case ORACLE_GGML_IQ4_NL: return 16u + 128u; /* 8 fp16 scales + 256 nibbles */
+    case ORACLE_GGML_Q8_0: return 16u + 256u;   /* 8 fp16 scales + 256 int8 */
+    default: return 0u;
+  }
+}
+
+/*
+ * Value j (0..255) of one super-block.  Super-block b holds positions
+ * [256*b, 256*b + 256) of the permuted F16 image of opcode 1 (the driver
+ * dequantizes n_cols*k consecutive values of a column chunk into the buffer
+ * the F16 core reads, mat_mul.c:1700-1712).  Position j uses scale j/32
+ * (vlut16 of the scale indices 0,2 / 1,3 per half, :338-346, :414-421).
+ *   Q8_0: quant byte j sign-extended (vunpack keeps byte order, :505-511).
+ *   Q4_0 / IQ4_NL: the four 64-lane vlut16 results are written in the order
+ *     lo(low nibbles), hi(low nibbles), lo(high nibbles), hi(high nibbles)
+ *     (:424-427); vlut16 sends the even bytes of its source to the lo vector
+ *     and the odd bytes to the hi vector (the single-group path re-interleaves
+ *     them with vshuff, :296-298), so lane i of result v reads byte 2*i+(v&1),
+ *     its low nibble for v < 2 and its high nibble otherwise.  Q4_0 values are
+ *     nibble-8 (:30-32), IQ4_NL values the code book above.
+ * The product value*scale is exact in binary32 and rounded once to binary16
+ * (RNE): parity unpinned against the qf16 multiply and conversion of the
+ * reference (Q6_Vqf16_vmpy_VhfVhf, Q6_Vhf_equals_Vqf16).
+ */
+uint16_t oracle_qk0_value(const uint8_t *block, int j, int type) {
+  const int g = j / 32;
+  const uint16_t sbits = (uint16_t)(block[2 * g] | (block[2 * g + 1] << 8));
+  const float scale = oracle_f16_to_f32(sbits);
+  int q;
+  if (type == ORACLE_GGML_Q8_0) {
+    q = (int8_t)block[16 + j];
+  } else {
+    const int v = j / 64, lane = j % 64;
+    const uint8_t byte = block[16 + 2 * lane + (v & 1)];
+    const int nib = v < 2 ? (byte & 15) : (byte >> 4);
+    q = type == ORACLE_GGML_IQ4_NL ? k_iq4nl_values[nib] : nib - 8;
+  }
+  return oracle_f32_to_f16((float)q * scale);
+}
+
+int oracle_qk0_dequant(uint16_t *permuted, const uint8_t *blocks, int k, int n, int type) {
+  const size_t bb = oracle_qk0_block_bytes(type);
+  if (!bb || k <= 0 || n <= 0 || k % 32 || n % 32) return -1;
+  const size_t nblk = (size_t)k * (size_t)n / 256u;
+  for (size_t b = 0; b < nblk; ++b)
+    for (int j = 0; j < 256; ++j) permuted[b * 256u + (size_t)j] = oracle_qk0_value(blocks + b * bb, j, type);
+  return 0;
+}
+
+/* ------------------------------------------------------------------------ */
 /* Deterministic synthetic inputs: splitmix64, Box-Muller in double          */
 /* ------------------------------------------------------------------------ */
 

@@ -37,6 +37,14 @@
  *   f16_gemm_epilogue         pinned: float64 brute force, all-ones gives K,
  *                               one-hot; parity unpinned against the HMX FP16
  *                               accumulation order and precision (mat_mul.c:724-748).
+ *   qk0_value/_dequant        pinned: a model of the HVX instructions the
+ *                               reference uses, run through the reference's
+ *                               single-group path, reproduces ggml's published
+ *                               Q4_0/Q8_0/IQ4_NL group order; the same model run
+ *                               through the super-block path equals this
+ *                               restatement; scale-one blocks give the codes
+ *                               exactly.  Parity unpinned against the sd.cpp
+ *                               packer (absent) and the qf16 product rounding.
  */
 #ifndef HTP_ORACLE_H
 #define HTP_ORACLE_H
@@ -86,6 +94,12 @@ int oracle_model_aux(float *y, const float *x, const float *w, const float *b, i
 
 /* ---- packed F16 GEMM -------------------------------------------------------- */
 size_t oracle_f16_permuted_index(int k_total, int k_idx, int n_idx);
+/* Dequantizing GEMM (opcodes 2/3/4); types are ggml's (reference
+ * include/dsp/quants.h:33-54). */
+enum { ORACLE_GGML_Q4_0 = 2, ORACLE_GGML_Q8_0 = 8, ORACLE_GGML_IQ4_NL = 20 };
+size_t oracle_qk0_block_bytes(int type);
+uint16_t oracle_qk0_value(const uint8_t *block, int j, int type);
+int oracle_qk0_dequant(uint16_t *permuted, const uint8_t *blocks, int k, int n, int type);
 void oracle_f16_permute(uint16_t *permuted, const uint16_t *w_kn, int k, int n);
 void oracle_f16_gemm_epilogue(float *y, const float *x, const uint16_t *permuted, const float *bias, int m, int k,
                               int n, int channels, int mode, int nthreads);

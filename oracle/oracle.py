@@ -41,6 +41,9 @@ _SIGS = {
     "oracle_f16_permuted_index": (_S, [_I, _I, _I]),
     "oracle_f16_permute": (None, [_P, _P, _I, _I]),
     "oracle_f16_gemm_epilogue": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I]),
+    "oracle_qk0_block_bytes": (_S, [_I]),
+    "oracle_qk0_value": (ctypes.c_uint16, [_P, _I, _I]),
+    "oracle_qk0_dequant": (_I, [_P, _P, _I, _I, _I]),
     "oracle_fill_normal": (None, [_P, _S, ctypes.c_float, ctypes.c_float, ctypes.c_uint64]),
     "oracle_fill_uniform": (None, [_P, _S, ctypes.c_float, ctypes.c_float, ctypes.c_uint64]),
     "oracle_fill_int8": (None, [_P, _S, _I, _I, ctypes.c_uint64]),
@@ -262,6 +265,28 @@ def f16_gemm_epilogue(x, permuted, bias, m, k, n, channels, mode, nthreads=0):
                                    _ptr(None if bias is None else np.ascontiguousarray(bias, np.float32)), m, k, n,
                                    channels, mode, nthreads)
     return y.reshape((channels, m) if mode == 3 else (m, n))
+
+
+# ---- dequantizing GEMM (opcodes 2/3/4) ----------------------------------------
+
+GGML_Q4_0, GGML_Q8_0, GGML_IQ4_NL = 2, 8, 20
+
+
+def qk0_block_bytes(wtype):
+    return lib().oracle_qk0_block_bytes(wtype)
+
+
+def qk0_value(block, j, wtype):
+    return lib().oracle_qk0_value(_ptr(np.ascontiguousarray(block, np.uint8)), j, wtype)
+
+
+def qk0_dequant(blocks, k, n, wtype):
+    """Super-blocks (uint8) -> the permuted F16 image (uint16 bits) of opcode 1."""
+    out = np.zeros(k * n, np.uint16)
+    rc = lib().oracle_qk0_dequant(_ptr(out), _ptr(np.ascontiguousarray(blocks, np.uint8)), k, n, wtype)
+    if rc:
+        raise ValueError(f"oracle_qk0_dequant rejected k={k} n={n} type={wtype}")
+    return out
 
 
 def num_threads():
