@@ -304,12 +304,39 @@ def all_configs(steps, warmup, with_cpu=False):
     return out
 
 
+def _timed_graph_us(launch, steps, warmup, stream):
+    """Settles the clock with stream-ordered launches, then the mean of one
+    graph replay of `steps` launches (µs per launch)."""
+    lib = hip.lib()
+    done, gpu_ms = 0, 0.0
+    while done < max(warmup, 1) or gpu_ms < SETTLE_MS:
+        a, b = hip.Event(), hip.Event()
+        a.record(stream)
+        for i in range(50):
+            launch(done + i)
+        b.record(stream)
+        hip.check(lib.hb_stream_sync(stream), "sync")
+        done, gpu_ms = done + 50, gpu_ms + a.elapsed_ms(b)
+    with hip.Graph.capture(stream) as g:
+        for i in range(steps):
+            launch(i)
+    a, b = hip.Event(), hip.Event()
+    hip.check(lib.hb_stream_sync(stream), "sync")
+    a.record(stream)
+    g.launch(stream)
+    b.record(stream)
+    hip.check(lib.hb_stream_sync(stream), "sync")
+    return a.elapsed_ms(b) * 1e3 / steps
+
+
 def qk0_cases(steps, warmup, rotate=4):
-    """Opcodes 2/3/4 (Q4_0 / Q8_0 / IQ4_NL weights): the one-time dequantizing
-    prepack into the F16 tile image (µs per weight, all three formats), then
-    the F16 GEMM that every later call runs (identical for the three formats;
-    Q4_0 weights, graph-replayed mean, stream-ordered as the executor issues
-    it).  Shapes: BASELINE C5 gate/up (K=4096, N=14336) at M=1, 77 and 2048."""
+    """Opcodes 2/3/4 (Q4_0 / Q8_0 / IQ4_NL weights) at BASELINE C5's gate/up
+    shape (K=4096, N=14336).  m <= 16 multiplies the super-blocks directly
+    (`direct_*`: algorithmic bytes 4MK + K*N*block/256 + 4MN, the quantized
+    weights read once); larger m runs the F16 GEMM on the dequantized image
+    (`f16_image_*`, identical for the three formats; the one-time
+    dequantizing prepack is `prepack_us`).  Graph-replayed means over
+    `rotate` weight sets."""
     lib = hip.lib()
     stream = hip.default_stream()
     rng = np.random.default_rng(4)
@@ -317,64 +344,64 @@ def qk0_cases(steps, warmup, rotate=4):
     out = {"prepack_us": {}}
     block_bytes = {hip.GGML_Q4_0: 144, hip.GGML_Q8_0: 272, hip.GGML_IQ4_NL: 144}
     names = {hip.GGML_Q4_0: "q4_0", hip.GGML_Q8_0: "q8_0", hip.GGML_IQ4_NL: "iq4_nl"}
-    packed_sets = []
+    image_sets = []
     for wtype, bb in block_bytes.items():
         nb = k * n // 256
-        blocks = rng.integers(0, 256, nb * bb, dtype=np.uint8).reshape(nb, bb)
-        blocks[:, :16] = (rng.uniform(1e-3, 2e-3, nb * 8).astype(np.float16)).view(np.uint8).reshape(nb, 16)
-        bd = hip.DeviceBuffer.from_array(blocks.ravel())
+        sets = []
+        for _ in range(rotate):
+            blocks = rng.integers(0, 256, nb * bb, dtype=np.uint8).reshape(nb, bb)
+            blocks[:, :16] = (rng.uniform(1e-3, 2e-3, nb * 8).astype(np.float16)).view(np.uint8).reshape(nb, 16)
+            sets.append(hip.DeviceBuffer.from_array(blocks.ravel()))
         packed = hip.DeviceBuffer(lib.hb_f16_packed_bytes(k, n))
-        for _ in range(3):  # first call pays module load; report the third
+        for _ in range(3):  # the first call pays module load; report the third
             a, b = hip.Event(), hip.Event()
             a.record(stream)
-            hip.check(lib.hb_qk0_prepack(packed.ptr, bd.ptr, k, n, wtype, stream), "hb_qk0_prepack")
+            hip.check(lib.hb_qk0_prepack(packed.ptr, sets[0].ptr, k, n, wtype, stream), "hb_qk0_prepack")
             b.record(stream)
             hip.check(lib.hb_stream_sync(stream), "sync")
         out["prepack_us"][names[wtype]] = round(a.elapsed_ms(b) * 1e3, 1)
-        bd.free()
         if wtype == hip.GGML_Q4_0:
-            packed_sets.append(packed)
+            image_sets.append(packed)
         else:
             packed.free()
-    while len(packed_sets) < rotate:
-        packed_sets.append(hip.DeviceBuffer(lib.hb_f16_packed_bytes(k, n)))
-        hip.check(lib.hb_memcpy_d2d(packed_sets[-1].ptr, packed_sets[0].ptr, packed_sets[0].nbytes, stream), "copy")
-    for m in (1, 77, 2048):
+        for m in (1, 16):
+            x = hip.DeviceBuffer.from_array(rng.standard_normal((m, k), dtype=np.float32))
+            y = hip.DeviceBuffer(m * n * 4)
+            ws = hip.DeviceBuffer(hip.f16_workspace_bytes(m, k, n))
+
+            def launch(i):
+                hip.check(lib.hb_qk0_gemm_ws(y.ptr, x.ptr, sets[i % rotate].ptr, m, k, n, wtype, ws.ptr, ws.nbytes,
+                                             stream), "hb_qk0_gemm_ws")
+
+            us = _timed_graph_us(launch, steps, warmup, stream)
+            nbytes = 4 * m * k + k * n // 256 * bb + 4 * m * n
+            out[f"direct_{names[wtype]}_M{m}_{k}x{n}"] = {
+                "us": round(us, 2), "gbps": round(nbytes / us * 1e-3, 1),
+                "frac_hbm": round(nbytes / us * 1e-3 / PEAK_HBM_GBPS, 4)}
+            for buf in (x, y, ws):
+                buf.free()
+        for buf in sets:
+            buf.free()
+    while len(image_sets) < rotate:
+        image_sets.append(hip.DeviceBuffer(lib.hb_f16_packed_bytes(k, n)))
+        hip.check(lib.hb_memcpy_d2d(image_sets[-1].ptr, image_sets[0].ptr, image_sets[0].nbytes, stream), "copy")
+    for m in (77, 2048):
         x = hip.DeviceBuffer.from_array(rng.standard_normal((m, k), dtype=np.float32))
         y = hip.DeviceBuffer(m * n * 4)
         ws = hip.DeviceBuffer(max(hip.f16_workspace_bytes(m, k, n), 256))
 
         def launch(i):
-            hip.check(lib.hb_f16_gemm_ws(y.ptr, x.ptr, packed_sets[i % rotate].ptr, None, m, k, n, n, 0, ws.ptr,
+            hip.check(lib.hb_f16_gemm_ws(y.ptr, x.ptr, image_sets[i % rotate].ptr, None, m, k, n, n, 0, ws.ptr,
                                          ws.nbytes, stream), "hb_f16_gemm_ws")
 
-        reps = steps if m < 2048 else max(steps // 10, 20)
-        done, gpu_ms = 0, 0.0
-        while done < max(warmup, 1) or gpu_ms < SETTLE_MS:
-            a, b = hip.Event(), hip.Event()
-            a.record(stream)
-            for i in range(50):
-                launch(done + i)
-            b.record(stream)
-            hip.check(lib.hb_stream_sync(stream), "sync")
-            done, gpu_ms = done + 50, gpu_ms + a.elapsed_ms(b)
-        with hip.Graph.capture(stream) as g:
-            for i in range(reps):
-                launch(i)
-        a, b = hip.Event(), hip.Event()
-        hip.check(lib.hb_stream_sync(stream), "sync")
-        a.record(stream)
-        g.launch(stream)
-        b.record(stream)
-        hip.check(lib.hb_stream_sync(stream), "sync")
-        us = a.elapsed_ms(b) * 1e3 / reps
-        nbytes = 4 * m * k + 2 * n * k + 4 * m * n  # fp16 tile image read per call
-        out[f"M{m}_{k}x{n}"] = {"us": round(us, 2), "tflops": round(2 * m * n * k / us * 1e-6, 2),
-                                "gbps_fp16_image": round(nbytes / us * 1e-3, 1),
-                                "frac_hbm": round(nbytes / us * 1e-3 / PEAK_HBM_GBPS, 4)}
+        us = _timed_graph_us(launch, steps if m < 2048 else max(steps // 10, 20), warmup, stream)
+        nbytes = 4 * m * k + 2 * n * k + 4 * m * n  # the fp16 image read per call
+        out[f"f16_image_M{m}_{k}x{n}"] = {"us": round(us, 2), "tflops": round(2 * m * n * k / us * 1e-6, 2),
+                                          "gbps": round(nbytes / us * 1e-3, 1),
+                                          "frac_hbm": round(nbytes / us * 1e-3 / PEAK_HBM_GBPS, 4)}
         for buf in (x, y, ws):
             buf.free()
-    for p in packed_sets:
+    for p in image_sets:
         p.free()
     return out
 

@@ -331,11 +331,257 @@ __global__ __launch_bounds__(64 * kSkinnyWaves) void f16_skinny_partial(float *_
   }
   __syncthreads();
   if (wave != 0) return;
-  // 16-byte stores through a buffer resource covering the slice: rows past
-  // mp fall outside it and are dropped by the hardware (no branches)
+  // 16-byte stores through a buffer resource covering the slice's first m
+  // rows: rows past m are never read and fall outside it (dropped, no branches)
   const int mp = (m + 15) / 16 * 16;
   const __amdgpu_buffer_rsrc_t rs =
-      __builtin_amdgcn_make_buffer_rsrc(ws + (size_t)s * mp * n, 0, mp * n * 4, 0x00020000);
+      __builtin_amdgcn_make_buffer_rsrc(ws + (size_t)s * mp * n, 0, m * n * 4, 0x00020000);
+#pragma unroll
+  for (int i = 0; i < RF; ++i) {
+#pragma unroll
+    for (int j = 0; j < CF; ++j) {
+      hb_f32x4 t = acc[i][j];
+#pragma unroll
+      for (int w = 1; w < kSkinnyWaves; ++w) t += red[w - 1][i * CF + j][lane];
+      const int row = 16 * i + (lane & 15), col = (g * CF + j) * 16 + 4 * (lane >> 4);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(hb_u32x4, t), rs, (uint32_t)(row * n + col) * 4u, 0,
+                                             0);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Few rows on quantized weights (opcodes 2/3/4, m <= 16): the split-K kernel
+// above with the weight fragment built from the super-blocks themselves, so
+// a call streams 4.5 (Q4_0, IQ4_NL) or 8.5 (Q8_0) bits per weight instead of
+// the 16 of the F16 image.  Fragment (16 columns gc, 32-k block kb), lane l:
+// column c = (gc%2)*16 + l%16 of 32-column tile gc/2, super-block q = l/16 of
+// the tile's k-block (8 k x 32 columns).  Its 8 values k = 2p+e (p < 4, e < 2)
+// sit, for Q4_0 / IQ4_NL, in the nibbles of quant word c (bytes 4c..4c+3):
+// pair p takes bytes (0,2), (1,3) low nibbles for p = 0, 1 and high nibbles
+// for p = 2, 3 (the vlut16 order of qk0_prepack, rewritten for one column);
+// for Q8_0 in the byte pair at 64p + 2c.  Scale of pair p: s[2p + c/16].
+// Values become fp16 exactly (1024 + biased code in the mantissa, minus the
+// bias) and one packed fp16 multiply rounds value*scale as qk0_prepack does,
+// so the result equals hb_f16_gemm_ws on the prepacked image bit for bit.
+// ---------------------------------------------------------------------------
+
+typedef _Float16 hb_f16x2 __attribute__((ext_vector_type(2)));
+
+template <int TYPE>
+struct Qk0Raw {
+  uint32_t q[TYPE == HB_GGML_Q8_0 ? 4 : 1];
+  hb_u32x4 s;  // the super-block's 8 fp16 scales
+};
+
+template <int TYPE>
+constexpr int qk0_block_bytes() {
+  return TYPE == HB_GGML_Q8_0 ? 272 : 144;
+}
+
+template <int TYPE>
+__device__ inline void qk0_load(Qk0Raw<TYPE> &r, const uint8_t *__restrict__ blocks, int gc, int kb, int kblocks,
+                                int lane) {
+  const int c = (gc & 1) * 16 + (lane & 15), q = lane >> 4;
+  const uint8_t *base = blocks + ((size_t)((gc >> 1) * kblocks + kb) * 4u + (size_t)q) * (size_t)qk0_block_bytes<TYPE>();
+  r.s = *(const hb_u32x4 *)base;
+  if constexpr (TYPE == HB_GGML_Q8_0) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p) r.q[p] = __builtin_nontemporal_load((const uint16_t *)(base + 16 + 64 * p + 2 * c));
+  } else {
+    r.q[0] = __builtin_nontemporal_load((const uint32_t *)(base + 16 + 4 * c));
+  }
+}
+
+// IQ4_NL code book + 128, as bytes (ggml's kvalues_iq4nl).
+constexpr uint32_t kIq4Biased[4] = {0x3F2D1801u, 0x766A5D4Fu, 0xA6998D81u, 0xF1D9C5B5u};
+
+// Four nibbles (one per byte) -> their biased IQ4_NL codes.
+__device__ inline uint32_t iq4_lookup(uint32_t nib) {
+  const uint32_t sel = nib & 0x07070707u;
+  const uint32_t lo = __builtin_amdgcn_perm(kIq4Biased[1], kIq4Biased[0], sel);
+  const uint32_t hi = __builtin_amdgcn_perm(kIq4Biased[3], kIq4Biased[2], sel);
+  const uint32_t m = ((nib >> 3) & 0x01010101u) * 0xFFu;
+  return (hi & m) | (lo & ~m);
+}
+
+template <int TYPE>
+__device__ inline hb_f16x8 qk0_fragment(const Qk0Raw<TYPE> &r, int odd) {
+  uint32_t u[4];  // pair p: two biased codes in the low byte of each half
+  float bias;
+  if constexpr (TYPE == HB_GGML_Q8_0) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p) u[p] = ((r.q[p] & 0xFFu) | ((r.q[p] & 0xFF00u) << 8)) ^ 0x00800080u;
+    bias = 1152.0f;
+  } else {
+    uint32_t lo = r.q[0] & 0x0F0F0F0Fu, hi = (r.q[0] >> 4) & 0x0F0F0F0Fu;
+    if constexpr (TYPE == HB_GGML_IQ4_NL) {
+      lo = iq4_lookup(lo);
+      hi = iq4_lookup(hi);
+      bias = 1152.0f;
+    } else {
+      bias = 1032.0f;
+    }
+    u[0] = lo & 0x00FF00FFu;
+    u[1] = (lo >> 8) & 0x00FF00FFu;
+    u[2] = hi & 0x00FF00FFu;
+    u[3] = (hi >> 8) & 0x00FF00FFu;
+  }
+  const hb_f16x2 b2 = {(_Float16)bias, (_Float16)bias};
+  hb_f16x8 out;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const uint32_t sw = r.s[p];
+    const uint32_t sb = odd ? (sw >> 16) : (sw & 0xFFFFu);
+    const hb_f16x2 sc = __builtin_bit_cast(hb_f16x2, sb | (sb << 16));
+    const hb_f16x2 v = __builtin_bit_cast(hb_f16x2, u[p] | 0x64006400u) - b2;  // exact codes
+    const hb_f16x2 d = v * sc;  // one fp16 rounding of code * scale
+    out[2 * p] = d[0];
+    out[2 * p + 1] = d[1];
+  }
+  return out;
+}
+
+// One row (m == 1) on quantized weights: one workgroup per 32-column tile,
+// WAVES waves each owning KB consecutive 32-k blocks of the whole K, so the
+// tile is finished in one launch with no partial sums in memory.  Every wave
+// first requests all its quant words and scales, the workgroup meanwhile
+// converts the row to fp16 into LDS (in the A-operand order: only lanes of
+// row 0, lane % 16 == 0, carry it), then the fragments are dequantized and
+// multiplied; the waves' sums are added in wave order in LDS before the fp16
+// readout.
+template <int TYPE, int WAVES, int KB, int BT>
+__global__ __launch_bounds__(64 * WAVES) void qk0_decode(float *__restrict__ y, const float *__restrict__ x,
+                                                        const uint8_t *__restrict__ blocks, int k, int n) {
+  static_assert(KB % BT == 0, "k-blocks per wave must split into batches");
+  constexpr int NB = KB / BT;                          // batches per wave
+  constexpr int XV = (WAVES * KB * 8) / (64 * WAVES);  // float4 of the row per thread
+  __shared__ __attribute__((aligned(16))) _Float16 xs[WAVES * KB * 32];
+  __shared__ float red[WAVES][32];
+  const int tile = blockIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int kblocks = k / 32;
+  const int kb0 = wave * KB;
+  // the row first (oldest loads: waiting for it leaves the weights in flight)
+  float4 xv[XV];
+#pragma unroll
+  for (int i = 0; i < XV; ++i) xv[i] = *(const float4 *)(x + 4 * min((int)threadIdx.x + 64 * WAVES * i, k / 4 - 1));
+  Qk0Raw<TYPE> raw[KB][2];
+  auto issue = [&](int b) {
+#pragma unroll
+    for (int t = b * BT; t < b * BT + BT; ++t)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        qk0_load<TYPE>(raw[t][j], blocks, 2 * tile + j, min(kb0 + t, kblocks - 1), kblocks, lane);
+  };
+  issue(0);
+  if (NB > 1) issue(1);
+#pragma unroll
+  for (int i = 0; i < XV; ++i) {
+    const int v = threadIdx.x + 64 * WAVES * i;
+    // unconditional use of the loads (a conditional one lets the compiler
+    // move them into a branch, behind a wait for every weight request)
+    xs[4 * v] = (_Float16)xv[i].x;
+    xs[4 * v + 1] = (_Float16)xv[i].y;
+    xs[4 * v + 2] = (_Float16)xv[i].z;
+    xs[4 * v + 3] = (_Float16)xv[i].w;
+    if (4 * v >= k) *(uint2 *)(xs + 4 * v) = make_uint2(0u, 0u);  // zeros past k
+  }
+  __syncthreads();
+  const bool has_row = (lane & 15) == 0;
+  hb_f32x4 acc[2] = {hb_f32x4{0.0f, 0.0f, 0.0f, 0.0f}, hb_f32x4{0.0f, 0.0f, 0.0f, 0.0f}};
+  // Batch b is multiplied while batches b+1 and b+2 are in flight.  No
+  // branches around the multiplies (a branch would let the compiler sink the
+  // loads into it): k-blocks past k multiply zero weights by the zero row.
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    if (b + 2 < NB) issue(b + 2);
+#pragma unroll
+    for (int t = b * BT; t < b * BT + BT; ++t) {
+      const int kb = kb0 + t;
+      const bool live = kb < kblocks;
+      const hb_f16x8 a = has_row ? *(const hb_f16x8 *)(xs + kb * 32 + 8 * (lane >> 4)) : hb_f16x8{};
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const hb_f16x8 w = live ? qk0_fragment<TYPE>(raw[t][j], j) : hb_f16x8{};
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, a, acc[j], 0, 0, 0);
+      }
+    }
+  }
+  // row 0 of the product: element r of lanes 0, 16, 32, 48 holds column 4*(lane/16) + r
+  if (has_row) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[wave][16 * j + 4 * (lane >> 4) + r] = acc[j][r];
+  }
+  __syncthreads();
+  if (threadIdx.x >= 32) return;
+  float sum = red[0][threadIdx.x];
+#pragma unroll
+  for (int w = 1; w < WAVES; ++w) sum += red[w][threadIdx.x];
+  y[tile * 32 + threadIdx.x] = (float)(_Float16)sum;
+}
+
+template <int RF, int CF, int KPW, int TYPE>
+__global__ __launch_bounds__(64 * kSkinnyWaves) void qk0_skinny_partial(float *__restrict__ ws,
+                                                                        const float *__restrict__ x,
+                                                                        const uint8_t *__restrict__ blocks, int m,
+                                                                        int k, int n) {
+  __shared__ hb_f32x4 red[kSkinnyWaves - 1][RF * CF][64];
+  const int g = blockIdx.x, s = blockIdx.y;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int kblocks = k / 32;
+  const int kb0 = (s * kSkinnyWaves + wave) * KPW;
+  Qk0Raw<TYPE> raw[KPW][CF];
+  float4 alo[KPW][RF], ahi[KPW][RF];
+#pragma unroll
+  for (int t = 0; t < KPW; ++t) {
+    const int kb = min(kb0 + t, kblocks - 1);
+#pragma unroll
+    for (int j = 0; j < CF; ++j) qk0_load<TYPE>(raw[t][j], blocks, g * CF + j, kb, kblocks, lane);
+#pragma unroll
+    for (int i = 0; i < RF; ++i) {
+      const float *xr = x + (size_t)min(16 * i + (lane & 15), m - 1) * k + kb * 32 + 8 * (lane >> 4);
+      alo[t][i] = *(const float4 *)xr;
+      ahi[t][i] = *(const float4 *)(xr + 4);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);  // every load is in flight before the first use
+  hb_f32x4 acc[RF][CF];
+#pragma unroll
+  for (int i = 0; i < RF; ++i)
+#pragma unroll
+    for (int j = 0; j < CF; ++j) acc[i][j] = hb_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int t = 0; t < KPW; ++t) {
+    if (kb0 + t < kblocks) {
+      hb_f16x8 b[CF];
+#pragma unroll
+      for (int j = 0; j < CF; ++j) b[j] = qk0_fragment<TYPE>(raw[t][j], (g * CF + j) & 1);
+#pragma unroll
+      for (int i = 0; i < RF; ++i) {
+        const hb_f16x8 a = {(_Float16)alo[t][i].x, (_Float16)alo[t][i].y, (_Float16)alo[t][i].z,
+                            (_Float16)alo[t][i].w, (_Float16)ahi[t][i].x, (_Float16)ahi[t][i].y,
+                            (_Float16)ahi[t][i].z, (_Float16)ahi[t][i].w};
+#pragma unroll
+        for (int j = 0; j < CF; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(b[j], a, acc[i][j], 0, 0, 0);
+      }
+    }
+  }
+  if (wave != 0) {
+#pragma unroll
+    for (int i = 0; i < RF; ++i)
+#pragma unroll
+      for (int j = 0; j < CF; ++j) red[wave - 1][i * CF + j][lane] = acc[i][j];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  // 16-byte stores through a buffer resource covering the slice's first m
+  // rows: rows past m are never read and fall outside it (dropped, no branches)
+  const int mp = (m + 15) / 16 * 16;
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(ws + (size_t)s * mp * n, 0, m * n * 4, 0x00020000);
 #pragma unroll
   for (int i = 0; i < RF; ++i) {
 #pragma unroll
@@ -429,6 +675,26 @@ void launch_skinny(int rf, int kpw, dim3 grid, dim3 block, hipStream_t st, float
   else launch_skinny_k<CF, 1>(rf, grid, block, st, ws, x, packed, m, k, n);
 }
 
+template <int CF, int TYPE>
+void launch_qk0_skinny(int kpw, dim3 grid, dim3 block, hipStream_t st, float *ws, const float *x,
+                       const uint8_t *blocks, int m, int k, int n) {
+  if (kpw == 8)
+    hipLaunchKernelGGL((qk0_skinny_partial<1, CF, 8, TYPE>), grid, block, 0, st, ws, x, blocks, m, k, n);
+  else if (kpw == 4)
+    hipLaunchKernelGGL((qk0_skinny_partial<1, CF, 4, TYPE>), grid, block, 0, st, ws, x, blocks, m, k, n);
+  else if (kpw == 2)
+    hipLaunchKernelGGL((qk0_skinny_partial<1, CF, 2, TYPE>), grid, block, 0, st, ws, x, blocks, m, k, n);
+  else
+    hipLaunchKernelGGL((qk0_skinny_partial<1, CF, 1, TYPE>), grid, block, 0, st, ws, x, blocks, m, k, n);
+}
+
+template <int TYPE>
+void launch_qk0_skinny_type(int cols, int kpw, dim3 grid, dim3 block, hipStream_t st, float *ws, const float *x,
+                            const uint8_t *blocks, int m, int k, int n) {
+  if (cols == 64) launch_qk0_skinny<4, TYPE>(kpw, grid, block, st, ws, x, blocks, m, k, n);
+  else launch_qk0_skinny<2, TYPE>(kpw, grid, block, st, ws, x, blocks, m, k, n);
+}
+
 }  // namespace
 
 extern "C" {
@@ -474,6 +740,50 @@ int hb_qk0_prepack(uint16_t *d_packed, const uint8_t *d_blocks, int k, int n, in
   hipLaunchKernelGGL(qk0_prepack, dim3(grid), dim3(256), 0, hb_resolve_stream(s), (uint4 *)d_packed, d_blocks, k, n,
                      type, (int)bb);
   return hb_check_launch("qk0_prepack");
+}
+
+int hb_qk0_gemm_ws(float *d_y, const float *d_x, const uint8_t *d_blocks, int m, int k, int n, int type,
+                   void *d_workspace, size_t workspace_bytes, hb_stream s) {
+  if (!d_y || !d_x || !d_blocks || !d_workspace) return hb_invalid("hb_qk0_gemm_ws null pointer");
+  if (m < 1 || m > 16 || k < 32 || k % 32 || n < 32 || n % 32) return hb_invalid("hb_qk0_gemm_ws shape");
+  if (!hb_qk0_block_bytes(type)) return hb_invalid("hb_qk0_gemm_ws type");
+  if (workspace_bytes < hb_f16_workspace_bytes(m, k, n)) return hb_invalid("hb_qk0_gemm_ws workspace too small");
+  if (!aligned(d_x, 16) || !aligned(d_blocks, 16) || !aligned(d_y, 4) || !aligned(d_workspace, 16))
+    return hb_invalid("hb_qk0_gemm_ws alignment");
+  hipStream_t st = hb_resolve_stream(s);
+  // One row: the whole-K kernel (measured at k=4096, n=14336, m=1: Q4_0 11.0
+  // against 14.1 us split-K; Q8_0 25.3 either way, 16 waves keep its
+  // registers at one round).
+  if (m == 1 && k <= 8 * 16 * 32) {
+    if (type == HB_GGML_Q4_0)
+      hipLaunchKernelGGL((qk0_decode<HB_GGML_Q4_0, 8, 16, 2>), dim3(n / 32), dim3(512), 0, st, d_y, d_x, d_blocks, k,
+                         n);
+    else if (type == HB_GGML_IQ4_NL)
+      hipLaunchKernelGGL((qk0_decode<HB_GGML_IQ4_NL, 8, 16, 2>), dim3(n / 32), dim3(512), 0, st, d_y, d_x, d_blocks,
+                         k, n);
+    else
+      hipLaunchKernelGGL((qk0_decode<HB_GGML_Q8_0, 16, 8, 2>), dim3(n / 32), dim3(1024), 0, st, d_y, d_x, d_blocks,
+                         k, n);
+    return hb_check_launch("qk0_decode");
+  }
+  int splits = 1, kpw = 1;
+  skinny_plan(k, n, splits, kpw);
+  const int cols = skinny_cols(n);
+  const dim3 grid(n / cols, splits), block(64 * kSkinnyWaves);
+  float *ws = (float *)d_workspace;
+  if (type == HB_GGML_Q4_0)
+    launch_qk0_skinny_type<HB_GGML_Q4_0>(cols, kpw, grid, block, st, ws, d_x, d_blocks, m, k, n);
+  else if (type == HB_GGML_Q8_0)
+    launch_qk0_skinny_type<HB_GGML_Q8_0>(cols, kpw, grid, block, st, ws, d_x, d_blocks, m, k, n);
+  else
+    launch_qk0_skinny_type<HB_GGML_IQ4_NL>(cols, kpw, grid, block, st, ws, d_x, d_blocks, m, k, n);
+  int rc = hb_check_launch("qk0_skinny_partial");
+  if (rc) return rc;
+  const size_t outs = (size_t)m * (size_t)n;
+  const int eg = (int)((outs + 255) / 256 < 4096 ? (outs + 255) / 256 : 4096);
+  hipLaunchKernelGGL(f16_skinny_epilogue, dim3(eg), dim3(256), 0, st, d_y, ws, (const float *)nullptr, m, n, n, 0,
+                     splits);
+  return hb_check_launch("f16_skinny_epilogue");
 }
 
 size_t hb_f16_workspace_bytes(int m, int k, int n) {

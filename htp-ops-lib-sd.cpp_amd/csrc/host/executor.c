@@ -314,16 +314,25 @@ static uintptr_t primary_address(const htp_view *v) {
   return v->is_device ? (uintptr_t)v->dev : (uintptr_t)v->host;
 }
 
-/* Shared F16 compute after validation.  Returns 0 or a negative code. */
-static int run_f16(int kind, htp_view *out, htp_view *act, htp_view *wgt, htp_view *bias, int m, int k, int n,
-                   int channels, int mode, int32_t *elapsed_us) {
+/* Shared F16 compute after validation.  Returns 0 or a negative code.
+ * qk0_type != 0 (opcodes 2/3/4): with m <= 16 the quantized super-blocks are
+ * multiplied directly (in place when already device-resident and aligned,
+ * else from a cached device copy); otherwise through their cached F16 image. */
+static int run_f16(int kind, int qk0_type, htp_view *out, htp_view *act, htp_view *wgt, htp_view *bias, int m, int k,
+                   int n, int channels, int mode, int32_t *elapsed_us) {
   if (htp_executor_ensure_device() != 0) return -5;
   if (materialize(out) || materialize(act) || materialize(wgt) || (bias && materialize(bias))) return -5;
   hb_stream s = htp_executor_stream();
+  const int direct = qk0_type != 0 && m <= 16;
   void *packed = NULL;
   int built = 0;
   const double t_w0 = now_seconds();
-  int rc = htp_weight_cache_get(kind, wgt, k, n, weight_signature(wgt), &packed, &built, s);
+  int rc = 0;
+  if (direct && wgt->is_device && ((uintptr_t)wgt->dev & 15u) == 0)
+    packed = wgt->dev;
+  else
+    rc = htp_weight_cache_get(direct ? HTP_WEIGHT_QK0_RAW : kind, wgt, k, n, weight_signature(wgt), &packed, &built,
+                              s);
   if (rc) return rc;
   const double t_w1 = now_seconds();
   if (stage_in(act, s)) return -5;
@@ -351,7 +360,9 @@ static int run_f16(int kind, htp_view *out, htp_view *act, htp_view *wgt, htp_vi
     return -5;
   }
   int hrc = hb_event_record(ev.e[0], s);
-  if (!hrc) hrc = hb_f16_gemm_ws(y, x, (const uint16_t *)packed, b, m, k, n, channels, mode, ws, ws_bytes, s);
+  if (!hrc)
+    hrc = direct ? hb_qk0_gemm_ws(y, x, (const uint8_t *)packed, m, k, n, qk0_type, ws, ws_bytes, s)
+                 : hb_f16_gemm_ws(y, x, (const uint16_t *)packed, b, m, k, n, channels, mode, ws, ws_bytes, s);
   if (!hrc) hrc = hb_event_record(ev.e[1], s);
   if (!hrc && (void *)y != (void *)out->dev) hrc = hb_memcpy_d2d(out->dev, y, out_bytes, s);
   if (!hrc) hrc = hb_stream_sync(s);
@@ -387,8 +398,8 @@ static int exec_f16_epilogue(uint8_t *payload, size_t payload_size) {
    * (reference src/dsp/ops/mat_mul.c:947-949). */
   if ((primary_address(&out) | primary_address(&act) | primary_address(&wgt)) & 127u) return -12;
   int32_t elapsed = 0;
-  rc = run_f16(HTP_WEIGHT_F16, &out, &act, &wgt, p.bias.fd >= 0 ? &bias : NULL, p.m, p.k, p.n, p.channels, p.mode,
-               &elapsed);
+  rc = run_f16(HTP_WEIGHT_F16, 0, &out, &act, &wgt, p.bias.fd >= 0 ? &bias : NULL, p.m, p.k, p.n, p.channels,
+               p.mode, &elapsed);
   if (rc) return rc;
   memcpy(payload + offsetof(struct F16EpilogueParams, elapsed_us), &elapsed, sizeof(elapsed));
   return 0;
@@ -411,7 +422,7 @@ static int exec_matmul_params(const struct MatMulParams *p, int32_t *elapsed_us,
     *act_hash = 0;
     if (act.host) *act_hash = htp_fnv1a64(act.host, act.bytes);
   }
-  rc = run_f16(HTP_WEIGHT_F16, &out, &act, &wgt, NULL, m, k, n, n, 0, elapsed_us);
+  rc = run_f16(HTP_WEIGHT_F16, 0, &out, &act, &wgt, NULL, m, k, n, n, 0, elapsed_us);
   if (rc) return rc;
   if (out_hash) {
     *out_hash = 0;
@@ -431,9 +442,9 @@ static int exec_matmul(uint8_t *payload, size_t payload_size) {
   return rc;
 }
 
-/* Opcodes 2/3/4: Q4_0 / Q8_0 / IQ4_NL super-blocks dequantized into the F16
- * image (once per weight buffer, cached), then the F16 GEMM with mode 0 and
- * no bias.  Reference src/dsp/op_executor.cc:771-800 (payload, buffer sizes
+/* Opcodes 2/3/4: Q4_0 / Q8_0 / IQ4_NL super-blocks.  m <= 16 multiplies the
+ * blocks directly; larger m dequantizes them into the F16 image (once per
+ * weight buffer, cached) and runs the F16 GEMM with mode 0 and no bias.  Reference src/dsp/op_executor.cc:771-800 (payload, buffer sizes
  * m*n*4, m*k*4, k*n/256*block) and src/dsp/ops/mat_mul.c:1601-1617 (-1 for
  * a missing buffer, a zero dimension, k or n not a multiple of 32, or an
  * output, activation or weight address not 128-byte aligned). */
@@ -455,7 +466,7 @@ static int exec_matmul_qk0(uint8_t *payload, size_t payload_size, int kind, int 
   if (rc) return rc;
   if ((primary_address(&out) | primary_address(&act) | primary_address(&wgt)) & 127u) return -1;
   int32_t elapsed = 0;
-  return run_f16(kind, &out, &act, &wgt, NULL, m, k, n, n, 0, &elapsed);
+  return run_f16(kind, type, &out, &act, &wgt, NULL, m, k, n, n, 0, &elapsed);
 }
 
 /* Direct (non-mailbox) opcode-1 entry used by htp_ops_mat_mul_permuted_w16a32[_trace]. */

@@ -43,7 +43,9 @@ enum {
   /* quantized super-blocks of opcodes 2/3/4, dequantized into the F16 image */
   HTP_WEIGHT_Q4_0 = 3,
   HTP_WEIGHT_Q8_0 = 4,
-  HTP_WEIGHT_IQ4_NL = 5
+  HTP_WEIGHT_IQ4_NL = 5,
+  /* a device copy of host-resident quantized super-blocks (few-row calls) */
+  HTP_WEIGHT_QK0_RAW = 6
 };
 
 /* Returns the device image of a prepacked weight for the given source view,

@@ -346,7 +346,8 @@ int htp_weight_cache_drop_fd(int fd) {
   return dropped;
 }
 
-static size_t packed_bytes(int kind, int k, int n) {
+static size_t packed_bytes(int kind, const htp_view *src, int k, int n) {
+  if (kind == HTP_WEIGHT_QK0_RAW) return src->bytes;
   return kind == HTP_WEIGHT_W8A8 ? hb_w8a8_packed_bytes(k, n) : hb_f16_packed_bytes(k, n);
 }
 
@@ -403,12 +404,14 @@ int htp_weight_cache_get(int kind, const htp_view *src, int k, int n, uint64_t s
     dsrc = (const uint8_t *)tmp;
   }
   void *img = NULL;
-  if (hb_malloc(&img, packed_bytes(kind, k, n)) != HB_OK) {
+  if (hb_malloc(&img, packed_bytes(kind, src, k, n)) != HB_OK) {
     hb_free(tmp);
     return -5;
   }
   if (kind == HTP_WEIGHT_W8A8)
     rc = hb_w8a8_prepack(img, dsrc, k, n, s);
+  else if (kind == HTP_WEIGHT_QK0_RAW)
+    rc = hb_memcpy_d2d(img, dsrc, src->bytes, s);
   else if (qk0_type(kind))
     rc = hb_qk0_prepack((uint16_t *)img, dsrc, k, n, qk0_type(kind), s);
   else

@@ -75,6 +75,8 @@ _SIGNATURES = {
     "hb_qk0_block_bytes": (_c_size_t, [_c_int]),
     "hb_qk0_weight_bytes": (_c_size_t, [_c_int, _c_int, _c_int]),
     "hb_qk0_prepack": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_void_p]),
+    "hb_qk0_gemm_ws": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_void_p,
+                                _c_size_t, _c_void_p]),
     "hb_f16_prepack": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
     "hb_f16_gemm": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int,
                              _c_void_p]),
@@ -348,6 +350,12 @@ def qk0_prepack(blocks_dev, k, n, wtype):
     packed = DeviceBuffer(lib().hb_f16_packed_bytes(k, n))
     check(lib().hb_qk0_prepack(packed.ptr, blocks_dev.ptr, k, n, wtype, None), "hb_qk0_prepack")
     return packed
+
+
+def qk0_gemm(y_dev, x_dev, blocks_dev, m, k, n, wtype, workspace, stream=None):
+    """hb_qk0_gemm_ws: few rows (m <= 16) straight from the super-blocks."""
+    check(lib().hb_qk0_gemm_ws(y_dev.ptr, x_dev.ptr, blocks_dev.ptr, m, k, n, wtype, workspace.ptr,
+                               workspace.nbytes, stream), "hb_qk0_gemm_ws")
 
 
 def f16_workspace_bytes(m, k, n):

@@ -152,6 +152,16 @@ enum { HB_GGML_Q4_0 = 2, HB_GGML_Q8_0 = 8, HB_GGML_IQ4_NL = 20 };
 size_t hb_qk0_block_bytes(int type);           /* 0 for an unknown type */
 size_t hb_qk0_weight_bytes(int k, int n, int type);
 int hb_qk0_prepack(uint16_t *d_packed, const uint8_t *d_blocks, int k, int n, int type, hb_stream s);
+/* Few rows (1 <= m <= 16) straight from the super-blocks, each weight fragment
+ * dequantized in registers (the same fp16 values as hb_qk0_prepack), mode 0,
+ * no bias; workspace of at least hb_f16_workspace_bytes(m, k, n).  m == 1 with
+ * k <= 4096 runs one whole-K kernel per 32-column tile (the workspace is not
+ * touched); otherwise the split-K path of hb_f16_gemm_ws, equal bit for bit to
+ * hb_f16_gemm_ws on the hb_qk0_prepack image.  Replaces the
+ * per-call dequantization of hmx_mat_mul_permuted_qk_0_d16a32
+ * (reference src/dsp/ops/mat_mul.c:1601-1720) for decode-sized calls. */
+int hb_qk0_gemm_ws(float *d_y, const float *d_x, const uint8_t *d_blocks, int m, int k, int n, int type,
+                   void *d_workspace, size_t workspace_bytes, hb_stream s);
 
 /*
  * y = epilogue(fp16(fp16(x) @ W)); x f32 [m][k]; bias f32[channels] or NULL.
