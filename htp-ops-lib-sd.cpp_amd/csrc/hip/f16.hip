@@ -262,6 +262,147 @@ __global__ __launch_bounds__(64 * WM *WN) void f16_gemm_tiles(float *__restrict_
 }
 
 // ---------------------------------------------------------------------------
+// Large M: both operands as 1 KB fp16 tiles in MFMA lane order, streamed
+// through the direct-to-LDS ring of the int8 GEMM.  f16_pack_a converts the
+// activations once per call (fp32 -> fp16 RNE, 16 rows x 32 k per tile, rows
+// past m zero); the packed weights already have this form.  The k loop is the
+// same sequence of v_mfma_f32_16x16x32_f16 per accumulator as f16_gemm_tiles,
+// so the results are identical to it.
+// ---------------------------------------------------------------------------
+
+#include "hb_lds_ring.h"
+static_assert(kFragBytes == kRingTileBytes, "operand tiles are the ring's tiles");
+
+__global__ __launch_bounds__(256) void f16_pack_a(uint4 *__restrict__ img, const float *__restrict__ x, int m, int k,
+                                                 int mp) {
+  const size_t slots = (size_t)mp * (size_t)k / 8u;
+  const int kblocks = k / 32;
+  for (size_t slot = (size_t)blockIdx.x * blockDim.x + threadIdx.x; slot < slots;
+       slot += (size_t)gridDim.x * blockDim.x) {
+    const size_t tile = slot / 64u;
+    const int lane = (int)(slot % 64u);
+    const int mb = (int)(tile / (size_t)kblocks), kb = (int)(tile % (size_t)kblocks);
+    const int row = mb * 16 + (lane & 15);
+    const int k0 = kb * 32 + 8 * (lane >> 4);
+    uint4 out = make_uint4(0u, 0u, 0u, 0u);
+    if (row < m) {
+      const float *xr = x + (size_t)row * k + k0;
+      const hb_f32x4 lo = __builtin_nontemporal_load((const hb_f32x4 *)xr);
+      const hb_f32x4 hi = __builtin_nontemporal_load((const hb_f32x4 *)(xr + 4));
+      const hb_f16x8 h = {(_Float16)lo[0], (_Float16)lo[1], (_Float16)lo[2], (_Float16)lo[3],
+                          (_Float16)hi[0], (_Float16)hi[1], (_Float16)hi[2], (_Float16)hi[3]};
+      out = __builtin_bit_cast(uint4, h);
+    }
+    img[slot] = out;
+  }
+}
+
+template <int BM, int BN, int WM, int WN, int S>
+__global__ __launch_bounds__(64 * WM *WN) void f16_gemm_ring(float *__restrict__ y, const int8_t *__restrict__ aimg,
+                                                             const int8_t *__restrict__ wpack,
+                                                             const float *__restrict__ bias, int m, int k, int n,
+                                                             int mode) {
+  constexpr int NW = WM * WN;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int FM = WTM / 16, FN = WTN / 16;
+  constexpr int ABLK = BM / 16, BBLK = BN / 16;
+  constexpr int NB = ABLK + BBLK;
+  constexpr int PW = (NB + NW - 1) / NW;
+  constexpr int PW_LO = NB / NW;
+  static_assert(PW_LO >= 1, "every wave takes part in the DMA");
+  constexpr int STAGE = NB * kFragBytes;
+  __shared__ __attribute__((aligned(1024))) int8_t lds[S * STAGE];
+
+  const int tiles_m = (m + BM - 1) / BM, tiles_n = (n + BN - 1) / BN;
+  int tm, tn;
+  tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int kt_count = k / 32;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int wm = wave / WN, wn = wave % WN;
+
+  const int8_t *src[PW];
+  int stride[PW];
+  const int nblocks = n / 16;
+#pragma unroll
+  for (int i = 0; i < PW; ++i) {
+    const int b = min(i * NW + wave, NB - 1);
+    if (b < ABLK) {
+      const int mb = min(m0 / 16 + b, (m + 15) / 16 - 1);
+      src[i] = aimg + (size_t)mb * kt_count * kFragBytes + lane * 16;
+    } else {
+      const int nb = min(n0 / 16 + (b - ABLK), nblocks - 1);
+      src[i] = wpack + (size_t)nb * kt_count * kFragBytes + lane * 16;
+    }
+    stride[i] = kFragBytes;
+  }
+
+  hb_f32x4 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = hb_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+#pragma unroll
+  for (int s = 0; s < S - 1; ++s)
+    if (s < kt_count) dma_stage<PW, NW, NB>(lds + (s % S) * STAGE, src, stride, s, wave, lane);
+  for (int kt = 0; kt < kt_count; ++kt) {
+    if (PW == PW_LO || wave < NB % NW)
+      wait_stage<PW, S - 2>(kt_count - 1 - kt);
+    else
+      wait_stage<PW_LO, S - 2>(kt_count - 1 - kt);
+    block_barrier();
+    if (kt + S - 1 < kt_count)
+      dma_stage<PW, NW, NB>(lds + ((kt + S - 1) % S) * STAGE, src, stride, kt + S - 1, wave, lane);
+    const int8_t *base = lds + (kt % S) * STAGE;
+    const int8_t *la = base + (wm * FM) * kFragBytes + lane * 16;
+    const int8_t *lb = base + (ABLK + wn * FN) * kFragBytes + lane * 16;
+    hb_f16x8 bf[FN];
+#pragma unroll
+    for (int j = 0; j < FN; ++j) bf[j] = *(const hb_f16x8 *)(lb + j * kFragBytes);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const hb_f16x8 af = *(const hb_f16x8 *)(la + i * kFragBytes);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[j], acc[i][j], 0, 0, 0);
+    }
+  }
+
+  // Epilogue: fp16 readout, bias, activation, then each 16-row chunk staged
+  // in wave-private padded LDS and written as 16-byte vectors along rows.
+  const int row0 = m0 + wm * WTM;
+  const int col0 = n0 + wn * WTN;
+  float bj[FN];
+#pragma unroll
+  for (int j = 0; j < FN; ++j) bj[j] = bias ? bias[min(col0 + j * 16 + (lane & 15), n - 1)] : 0.0f;
+  block_barrier();  // every wave is done with the operand stages: LDS becomes staging
+  constexpr int SROW = WTN + 4;
+  static_assert(16 * SROW * 4 * NW <= S * STAGE, "staging must fit in the operand LDS");
+  float *stg = (float *)lds + wave * 16 * SROW;
+  constexpr int VPR = WTN / 4;
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float v = (float)(_Float16)acc[i][j][r];
+        const float z = bias ? __fadd_rn(v, bj[j]) : v;
+        stg[((lane >> 4) * 4 + r) * SROW + j * 16 + (lane & 15)] = apply_mode(z, mode);
+      }
+#pragma unroll
+    for (int v = lane; v < 16 * VPR; v += 64) {
+      const int r = v / VPR, c4 = v % VPR;
+      const int row = row0 + i * 16 + r, col = col0 + c4 * 4;
+      if (row < m && col < n) {
+        const hb_f32x4 val = *(const hb_f32x4 *)(stg + r * SROW + c4 * 4);
+        __builtin_nontemporal_store(val, (hb_f32x4 *)(y + (size_t)row * n + col));
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Few rows (m <= 128): split-K.  Workgroup (g, s) computes all rows x 32
 // columns (col-group g) over the s-th range of 32-k blocks; its 4 waves take
 // the range's blocks round robin and are summed in LDS in wave order, then
@@ -695,6 +836,77 @@ void launch_qk0_skinny_type(int cols, int kpw, dim3 grid, dim3 block, hipStream_
   else launch_qk0_skinny<2, TYPE>(kpw, grid, block, st, ws, x, blocks, m, k, n);
 }
 
+// Partial sums of the split-K path: one mp x n f32 slice per split, for
+// m <= 128 only (0 otherwise).
+size_t split_k_bytes(int m, int k, int n) {
+  if (m < 1 || m > 128 || k < 32 || n < 32) return 0;
+  // splits <= ceil(kblocks / 4) (one k-block per wave at the least)
+  const int max_splits = (k / 32 + kSkinnyWaves - 1) / kSkinnyWaves;
+  return (size_t)max_splits * (size_t)((m + 15) / 16 * 16) * (size_t)n * 4u;
+}
+
+// The fp16 activation image of the ring path: mp rows x k, 2 bytes each.
+size_t a_image_bytes(int m, int k) { return hb_round_up((size_t)((m + 15) / 16 * 16) * (size_t)k * 2u, 256); }
+
+// The ring path pays one extra launch (f16_pack_a); it is used from 4 GFLOP
+// of work with at least 64 rows (measured: 77x4096x14336 74 -> 29 us,
+// 2048x4096x14336 613 -> 250 us, 4096x1536x6144 212 -> 89 us).
+bool ring_worth_it(int m, int k, int n) { return m >= 64 && 2.0 * m * (double)n * k >= 4e9; }
+
+// Ring tile shapes, cheapest (rounds of resident workgroups) x (work per
+// round per CU) / measured efficiency; 128x192 only when n allows.
+struct RingShape {
+  int bm, bn, occ, eff;
+};
+constexpr RingShape kRingShapes[] = {{128, 192, 2, 100}, {128, 128, 2, 92}, {64, 64, 4, 60}};
+
+int pick_ring_shape(int m, int n) {
+  const int cus = compute_units();
+  int best = -1;
+  long long best_cost = -1;
+  for (int i = 0; i < 3; ++i) {
+    const RingShape t = kRingShapes[i];
+    if (n % t.bn != 0 && t.bn == 192) continue;
+    const long long tiles = (long long)((m + t.bm - 1) / t.bm) * ((n + t.bn - 1) / t.bn);
+    const long long slots = (long long)cus * t.occ;
+    const long long cost = (tiles + slots - 1) / slots * t.bm * t.bn * t.occ * 100 / t.eff;
+    if (best_cost < 0 || cost < best_cost) {
+      best_cost = cost;
+      best = i;
+    }
+  }
+  return best;
+}
+
+int launch_ring(float *y, const float *x, const uint16_t *packed, const float *bias, int m, int k, int n, int mode,
+                void *ws, hipStream_t st) {
+  const int mp = (m + 15) / 16 * 16;
+  const size_t slots = (size_t)mp * k / 8u;
+  const int pg = (int)((slots + 255) / 256 < 65536 ? (slots + 255) / 256 : 65536);
+  hipLaunchKernelGGL(f16_pack_a, dim3(pg), dim3(256), 0, st, (uint4 *)ws, x, m, k, mp);
+  int rc = hb_check_launch("f16_pack_a");
+  if (rc) return rc;
+  const int shape = pick_ring_shape(m, n);
+  const RingShape t = kRingShapes[shape];
+  const int grid = ((m + t.bm - 1) / t.bm) * ((n + t.bn - 1) / t.bn);
+  const int8_t *a = (const int8_t *)ws, *w = (const int8_t *)packed;
+  switch (shape) {
+    case 0:
+      hipLaunchKernelGGL((f16_gemm_ring<128, 192, 2, 2, 4>), dim3(grid), dim3(256), 0, st, y, a, w, bias, m, k, n,
+                         mode);
+      break;
+    case 1:
+      hipLaunchKernelGGL((f16_gemm_ring<128, 128, 2, 2, 4>), dim3(grid), dim3(256), 0, st, y, a, w, bias, m, k, n,
+                         mode);
+      break;
+    default:
+      hipLaunchKernelGGL((f16_gemm_ring<64, 64, 2, 2, 4>), dim3(grid), dim3(256), 0, st, y, a, w, bias, m, k, n,
+                         mode);
+      break;
+  }
+  return hb_check_launch("f16_gemm_ring");
+}
+
 }  // namespace
 
 extern "C" {
@@ -747,7 +959,7 @@ int hb_qk0_gemm_ws(float *d_y, const float *d_x, const uint8_t *d_blocks, int m,
   if (!d_y || !d_x || !d_blocks || !d_workspace) return hb_invalid("hb_qk0_gemm_ws null pointer");
   if (m < 1 || m > 16 || k < 32 || k % 32 || n < 32 || n % 32) return hb_invalid("hb_qk0_gemm_ws shape");
   if (!hb_qk0_block_bytes(type)) return hb_invalid("hb_qk0_gemm_ws type");
-  if (workspace_bytes < hb_f16_workspace_bytes(m, k, n)) return hb_invalid("hb_qk0_gemm_ws workspace too small");
+  if (workspace_bytes < split_k_bytes(m, k, n)) return hb_invalid("hb_qk0_gemm_ws workspace too small");
   if (!aligned(d_x, 16) || !aligned(d_blocks, 16) || !aligned(d_y, 4) || !aligned(d_workspace, 16))
     return hb_invalid("hb_qk0_gemm_ws alignment");
   hipStream_t st = hb_resolve_stream(s);
@@ -787,10 +999,10 @@ int hb_qk0_gemm_ws(float *d_y, const float *d_x, const uint8_t *d_blocks, int m,
 }
 
 size_t hb_f16_workspace_bytes(int m, int k, int n) {
-  if (m < 1 || m > 128 || k < 32 || n < 32) return 0;
-  // splits <= ceil(kblocks / 4) (one k-block per wave at the least)
-  const int max_splits = (k / 32 + kSkinnyWaves - 1) / kSkinnyWaves;
-  return (size_t)max_splits * (size_t)((m + 15) / 16 * 16) * (size_t)n * 4u;
+  if (m < 1 || k < 32 || n < 32) return 0;
+  const size_t ring = ring_worth_it(m, k, n) ? a_image_bytes(m, k) : 0;
+  const size_t partials = split_k_bytes(m, k, n);
+  return ring > partials ? ring : partials;
 }
 
 int hb_f16_gemm_ws(float *d_y, const float *d_x, const uint16_t *d_packed, const float *d_bias, int m, int k, int n,
@@ -802,7 +1014,8 @@ int hb_f16_gemm_ws(float *d_y, const float *d_x, const uint16_t *d_packed, const
   if (!aligned(d_x, 16) || !aligned(d_packed, 16) || !aligned(d_y, 4) || (d_bias && !aligned(d_bias, 4)))
     return hb_invalid("hb_f16_gemm alignment");
   hipStream_t st = hb_resolve_stream(s);
-  const size_t need = hb_f16_workspace_bytes(m, k, n);
+  // The split-K path holds m <= 128 rows (8 row fragments) of partial sums.
+  const size_t need = split_k_bytes(m, k, n);
   // Tiled variant by output size; the split-K path takes over when that grid
   // leaves CUs idle, and for m <= 16, where a tile's rows are mostly padding
   // (measured at k=4096, n=14336: m=1 65 -> 28 us; 77x14336x4096: 264 -> 80 us).
@@ -810,7 +1023,7 @@ int hb_f16_gemm_ws(float *d_y, const float *d_x, const uint16_t *d_packed, const
   const long long mid = ((m + 63) / 64) * (long long)((n + 63) / 64);
   const long long small = ((m + 31) / 32) * (long long)((n + 31) / 32);
   const long long tiled_wgs = big >= 256 ? big : mid >= 128 ? mid : small;
-  if (d_workspace && need && workspace_bytes >= need && aligned(d_workspace, 16) &&
+  if (m <= 128 && d_workspace && need && workspace_bytes >= need && aligned(d_workspace, 16) &&
       (tiled_wgs < compute_units() || m <= 16)) {
     int splits = 1, kpw = 1;
     skinny_plan(k, n, splits, kpw);
@@ -828,6 +1041,9 @@ int hb_f16_gemm_ws(float *d_y, const float *d_x, const uint16_t *d_packed, const
                        splits);
     return hb_check_launch("f16_skinny_epilogue");
   }
+  if (mode != 3 && d_workspace && ring_worth_it(m, k, n) && workspace_bytes >= a_image_bytes(m, k) &&
+      aligned(d_workspace, 256) && aligned(d_y, 16))
+    return launch_ring(d_y, d_x, d_packed, d_bias, m, k, n, mode, d_workspace, st);
   if (big >= 256) {
     hipLaunchKernelGGL((f16_gemm_tiles<128, 128, 2, 2>), dim3((int)big), dim3(256), 0, st, d_y, d_x, d_packed, d_bias,
                        m, k, n, channels, mode);

@@ -298,62 +298,8 @@ __device__ inline void store_result(void *y, int ldy, int row, int col, int32_t 
 // A = q int8 [mp][kp] row-major; B = packed tiles (see hb.h).
 // ---------------------------------------------------------------------------
 
-#define HB_LDS_PTR(p) ((__attribute__((address_space(3))) void *)(p))
-
-template <int N>
-__device__ inline void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-__device__ inline void block_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
-// Waits until at most `ahead` later stages (PW DMA instructions each) are
-// still in flight for this wave; ahead <= A.
-template <int PW, int A>
-__device__ inline void wait_stage(int ahead) {
-  if constexpr (A == 0) {
-    wait_vmcnt<0>();
-  } else {
-    if (ahead >= A) {
-      wait_vmcnt<A * PW>();
-    } else {
-      wait_stage<PW, A - 1>(ahead);
-    }
-  }
-}
-
-// Workgroups are dispatched round-robin over the 8 XCDs: tile ids are first
-// made contiguous per XCD, then walked in groups of 4 row-blocks so that
-// workgroups resident together on one XCD share A and B blocks in its L2.
-__device__ inline void tile_coords(int bid, int tiles_m, int tiles_n, int &tm, int &tn) {
-  const int total = tiles_m * tiles_n;
-  const int pid = (total % 8 == 0) ? (bid % 8) * (total / 8) + bid / 8 : bid;
-  constexpr int G = 4;
-  const int first_m = (pid / (G * tiles_n)) * G;
-  const int gsize = min(tiles_m - first_m, G);
-  const int in_group = pid % (G * tiles_n);
-  tm = first_m + in_group % gsize;
-  tn = in_group / gsize;
-}
-
-// Issues one stage's DMA: instruction i of this wave fills block i*NW + wave
-// of the NB blocks of a stage (waves below NB % NW issue one more than the
-// others when the blocks do not split evenly).
-template <int PW, int NW, int NB = PW * NW>
-__device__ inline void dma_stage(int8_t *stage, const int8_t *const *src, const int *stride, int kt,
-                                 int wave, int lane) {
-  (void)lane;
-#pragma unroll
-  for (int i = 0; i < PW; ++i)
-    if (NB % NW == 0 || i * NW + wave < NB)
-      __builtin_amdgcn_global_load_lds(src[i] + (size_t)kt * stride[i],
-                                       HB_LDS_PTR(stage + (i * NW + wave) * kFragBytes), 16, 0, 0);
-}
+#include "hb_lds_ring.h"
+static_assert(kFragBytes == kRingTileBytes, "operand tiles are the ring's tiles");
 
 template <int BM, int BN, int WM, int WN, int S, int EPI>
 __global__ __launch_bounds__(64 * WM *WN) void w8a8_gemm_tiles(void *__restrict__ y, int ldy,

@@ -171,16 +171,23 @@ int hb_qk0_gemm_ws(float *d_y, const float *d_x, const uint8_t *d_blocks, int m,
 int hb_f16_gemm(float *d_y, const float *d_x, const uint16_t *d_packed, const float *d_bias, int m, int k, int n,
                 int channels, int mode, hb_stream s);
 
-/* Workspace for the few-rows (m <= 128) split-K path of hb_f16_gemm_ws; 0
- * when the shape takes the tiled path (no workspace needed). */
+/* Workspace of hb_f16_gemm_ws: the larger of the few-rows (m <= 128) split-K
+ * partial sums and, for 64 or more rows and at least 4 GFLOP, the fp16
+ * activation image of the ring path (2 * ceil(m/16)*16 * k bytes); 0 when
+ * neither applies (the tiled kernel needs none). */
 size_t hb_f16_workspace_bytes(int m, int k, int n);
 
 /* hb_f16_gemm with a workspace: for m <= 128, a workspace of at least
  * hb_f16_workspace_bytes, and either m <= 16 or a shape whose output tiles
  * (of the size hb_f16_gemm would use) number fewer than the device's CUs, K
  * is split across workgroups and the partial sums are added in a fixed order
- * before the fp16 readout rounding and the epilogue (two kernels); otherwise
- * identical to hb_f16_gemm. */
+ * before the fp16 readout rounding and the epilogue (two kernels).
+ * Otherwise, for modes 0-2 with a workspace of at least
+ * hb_f16_workspace_bytes, a 16-byte aligned output and 64 or more rows (4
+ * GFLOP or more), x is converted once into fp16 MFMA tiles in the workspace
+ * and both operands stream through the direct-to-LDS ring of the int8 GEMM;
+ * the result equals hb_f16_gemm bit for bit.  Otherwise identical to
+ * hb_f16_gemm. */
 int hb_f16_gemm_ws(float *d_y, const float *d_x, const uint16_t *d_packed, const float *d_bias, int m, int k, int n,
                    int channels, int mode, void *d_workspace, size_t workspace_bytes, hb_stream s);
 

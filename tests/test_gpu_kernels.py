@@ -292,6 +292,36 @@ def test_f16_gemm_epilogue(hip, orc, m, k, n, mode, channels, bias, split_k):
     assert_f16_close(got, ref, v_ref, bias_cols, absdot, k)
 
 
+@pytest.mark.parametrize("m,k,n,mode,bias,check_oracle", [
+    (512, 4096, 1024, 0, True, True),     # 128x128 tiles
+    (1024, 1536, 3072, 2, True, False),   # 128x192 tiles, QuickGELU
+    (300, 4096, 2048, 1, False, True),    # rows past m in the last tile, GELU
+    (640, 2048, 1600, 0, True, False),    # n % 128 != 0: columns past n in the last tile
+    (100, 4096, 14336, 2, True, False),   # few rows, 64x64 tiles
+])
+def test_f16_ring_matches_tiles(hip, orc, m, k, n, mode, bias, check_oracle):
+    """Large M with a workspace: the fp16 activation image and the
+    direct-to-LDS ring give the same bits as the tiled kernel (same MFMA
+    sequence per accumulator), and stay within the F16 bound of the oracle."""
+    ws_bytes = hip.f16_workspace_bytes(m, k, n)
+    assert ws_bytes >= ((m + 15) // 16 * 16) * k * 2
+    x, w, perm, b = f16_case(orc, m, k, n, seed=m + k + n, bias=bias)
+    packed = hip.f16_prepack(hip.DeviceBuffer.from_array(perm), k, n)
+    xd = hip.DeviceBuffer.from_array(x)
+    bd = hip.DeviceBuffer.from_array(b) if bias else None
+    y_ring, y_tiles = hip.DeviceBuffer(m * n * 4), hip.DeviceBuffer(m * n * 4)
+    hip.f16_gemm(y_ring, xd, packed, bd, m, k, n, n, mode, workspace=hip.DeviceBuffer(ws_bytes))
+    hip.f16_gemm(y_tiles, xd, packed, bd, m, k, n, n, mode)
+    hip.sync()
+    got = y_ring.read(np.uint32, m * n)
+    np.testing.assert_array_equal(got, y_tiles.read(np.uint32, m * n))
+    if check_oracle:
+        ref = orc.f16_gemm_epilogue(x, perm, b, m, k, n, n, mode)
+        v_ref = orc.f16_gemm_epilogue(x, perm, None, m, k, n, n, 0)
+        bias_cols = np.abs(b)[None, :] if b is not None else 0.0
+        assert_f16_close(got.view(np.float32).reshape(m, n), ref, v_ref, bias_cols, f16_abs_dot(x, w), k)
+
+
 def test_f16_all_ones_gives_k(hip, orc):
     m, k, n = 32, 256, 64
     x = np.ones((m, k), np.float32)
