@@ -613,6 +613,120 @@ __global__ __launch_bounds__(64 * WAVES, MINW) void w8a8_decode_fused(void *__re
 }
 
 // ---------------------------------------------------------------------------
+// A few rows (2 <= m <= R <= 4, k <= 4096) with the quantization fused in:
+// the 16-wave, two-block shape of w8a8_decode_fused.  Every workgroup
+// quantizes all m rows itself (one workgroup reduction for all rows) before
+// it streams its weight tiles; rows of the MFMA A operand past m are zero.
+// ---------------------------------------------------------------------------
+
+template <int R, int EPI>
+__global__ __launch_bounds__(1024, 8) void w8a8_decode_rows(void *__restrict__ y, int ldy, const float *__restrict__ x,
+                                                         const float *__restrict__ inv,
+                                                         const int8_t *__restrict__ wpack,
+                                                         const float *__restrict__ sw,
+                                                         const int32_t *__restrict__ corr, int m, int k, int kp,
+                                                         int nblocks) {
+  constexpr int WAVES = 16, BPW = 2, VW = 8;
+  constexpr int WPB = WAVES / BPW;
+  constexpr int KQ = VW * WPB * kKStep;  // the longest row served (4096)
+  static_assert(R >= 2 && R <= 4, "two to four rows");
+  __shared__ __attribute__((aligned(16))) int8_t qs[R][KQ];
+  __shared__ float red[R][WAVES];
+  __shared__ float srow[R];
+  __shared__ int32_t part[WAVES][R][16];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, tid = threadIdx.x;
+  const int wib = wave % WPB;
+  const int nb_raw = blockIdx.x * BPW + wave / WPB;
+  const int nb = min(nb_raw, nblocks - 1);
+  const int kc = kp / kKStep, nvec = k / 4;
+  const int col = nb * 16 + (lane & 15);
+  const int32_t cc = corr[col];
+  const float sc = sw[col];
+  // 1. the rows and the smoothing vector (a resource covering m rows; offsets
+  //    past a row's end are pushed out of range and read as zeros)
+  const __amdgpu_buffer_rsrc_t ri = __builtin_amdgcn_make_buffer_rsrc((void *)inv, 0, (uint32_t)nvec * 16u, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rx =
+      __builtin_amdgcn_make_buffer_rsrc((void *)x, 0, (uint32_t)m * (uint32_t)nvec * 16u, 0x00020000);
+  const bool in_row = tid < nvec;
+  const hb_u32x4 ivb = __builtin_amdgcn_raw_buffer_load_b128(ri, (uint32_t)tid * 16u, 0, 0);
+  hb_u32x4 xv[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    xv[r] = __builtin_amdgcn_raw_buffer_load_b128(
+        rx, in_row ? ((uint32_t)r * (uint32_t)nvec + (uint32_t)tid) * 16u : 0x80000000u, 0, 0);
+  // 2. every row's absmax in one workgroup reduction, then the rows quantized
+  //    into LDS -- before the weight stream, whose registers it would compete
+  //    for (a load issued after the weights could only be waited for behind them)
+  float4 t[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    t[r] = make_float4(__fmul_rn(__uint_as_float(xv[r][0]), __uint_as_float(ivb[0])),
+                       __fmul_rn(__uint_as_float(xv[r][1]), __uint_as_float(ivb[1])),
+                       __fmul_rn(__uint_as_float(xv[r][2]), __uint_as_float(ivb[2])),
+                       __fmul_rn(__uint_as_float(xv[r][3]), __uint_as_float(ivb[3])));
+    float amax = in_row ? fmaxf(fmaxf(fabsf(t[r].x), fabsf(t[r].y)), fmaxf(fabsf(t[r].z), fabsf(t[r].w))) : 0.0f;
+    amax = wave_max(amax);
+    if (lane == 0) red[r][wave] = amax;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    float a = red[r][0];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) a = fmaxf(a, red[r][w]);
+    const float sr = fmaxf(__fdiv_rn(a, 127.0f), 1e-12f);
+    const float rcp = __fdiv_rn(1.0f, sr);
+    if (tid == 0) srow[r] = sr;
+    if (tid < kp / 4) {
+      const uint32_t word = in_row ? (quantize_byte(t[r].x, rcp) | (quantize_byte(t[r].y, rcp) << 8) |
+                                      (quantize_byte(t[r].z, rcp) << 16) | (quantize_byte(t[r].w, rcp) << 24))
+                                   : 0u;
+      *(uint32_t *)(&qs[r][4 * tid]) = word;
+    }
+  }
+  // 3. the weight tiles (reads past the image return zeros and are never used)
+  const __amdgpu_buffer_rsrc_t rw =
+      __builtin_amdgcn_make_buffer_rsrc((void *)wpack, 0, (uint32_t)nblocks * (uint32_t)kc * kFragBytes, 0x00020000);
+  const uint32_t wv = ((uint32_t)nb * (uint32_t)kc + (uint32_t)(wib * VW)) * kFragBytes + (uint32_t)lane * 16u;
+  hb_i32x4 b[VW];
+#pragma unroll
+  for (int i = 0; i < VW; ++i) {
+    const hb_u32x4 tb = __builtin_amdgcn_raw_buffer_load_b128(rw, wv + i * kFragBytes, 0, 2);
+    b[i] = hb_i32x4{(int)tb[0], (int)tb[1], (int)tb[2], (int)tb[3]};
+  }
+  __syncthreads();  // qs and srow complete
+  // MFMA: lane l carries row l % 16 of the A operand (zero past R)
+  const int arow = lane & 15;
+  hb_i32x4 acc = {0, 0, 0, 0};
+#pragma unroll
+  for (int i = 0; i < VW; ++i) {
+    const int kt = wib * VW + i;
+    if (kt < kc) {
+      const hb_i32x4 av = arow < R ? *(const hb_i32x4 *)(&qs[arow][kt * kKStep + (lane >> 4) * 16])
+                                   : hb_i32x4{0, 0, 0, 0};
+      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b[i], acc, 0, 0, 0);
+    }
+  }
+  // element rr of lane l is row 4*(l/16) + rr, column l % 16
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) {
+    const int row = 4 * (lane >> 4) + rr;
+    if (row < R) part[wave][row][lane & 15] = acc[rr];
+  }
+  __syncthreads();
+  if (wib != 0 || nb_raw >= nblocks) return;
+  for (int idx = lane; idx < R * 16; idx += 64) {
+    const int row = idx / 16;  // idx % 16 == lane % 16: this lane's column
+    if (row >= m) continue;
+    int32_t tot = part[wave][row][lane & 15];
+#pragma unroll
+    for (int w = 1; w < WPB; ++w) tot = (int32_t)((uint32_t)tot + (uint32_t)part[wave + w][row][lane & 15]);
+    __builtin_nontemporal_store(epilogue_bits<EPI>(tot, cc, sc, srow[row]),
+                                (uint32_t *)y + (size_t)row * (size_t)ldy + col);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Raw accumulator -> byte-plane export of the CPU-control variant.
 // One thread per output byte position (row, 32-column half, byte in 128).
 // ---------------------------------------------------------------------------
@@ -962,6 +1076,34 @@ int hb_w8a8_linear(float *d_y, const float *d_x, const void *d_packed, int m, in
     return epilogue == HB_W8A8_EPI_SCALE
                ? launch_decode_fused<HB_W8A8_EPI_SCALE>(d_y, d_x, inv, wpack, sw, delta, k, n, kp, st)
                : launch_decode_fused<HB_W8A8_EPI_SCALE_GELU>(d_y, d_x, inv, wpack, sw, delta, k, n, kp, st);
+  }
+  // Two to four rows: quantization fused into the weight stream as well.
+  const int nblocks = n / 16;
+  if (m >= 2 && m <= 4 && kp <= 8 * 8 * kKStep && k >= 32 && k % 32 == 0 && n >= 16 && n % 16 == 0 && d_y && d_x &&
+      aligned(d_x, 16) && aligned(d_packed, 256) && (size_t)nblocks * (size_t)kp * 16u < ((size_t)1 << 32) &&
+      (epilogue == HB_W8A8_EPI_SCALE || epilogue == HB_W8A8_EPI_SCALE_GELU)) {
+    const uint8_t *base = (const uint8_t *)d_packed;
+    const int8_t *wpack = (const int8_t *)(base + hb_w8a8_packed_offset(k, n, HB_W8A8_WEIGHTS));
+    const float *sw = (const float *)(base + hb_w8a8_packed_offset(k, n, HB_W8A8_SW));
+    const int32_t *delta = (const int32_t *)(base + hb_w8a8_packed_offset(k, n, HB_W8A8_DELTA));
+    hipStream_t st = hb_resolve_stream(s);
+    const dim3 grid((nblocks + 1) / 2), block(1024);
+    if (m == 2) {
+      if (epilogue == HB_W8A8_EPI_SCALE)
+        hipLaunchKernelGGL((w8a8_decode_rows<2, HB_W8A8_EPI_SCALE>), grid, block, 0, st, d_y, n, d_x, inv, wpack, sw,
+                           delta, m, k, kp, nblocks);
+      else
+        hipLaunchKernelGGL((w8a8_decode_rows<2, HB_W8A8_EPI_SCALE_GELU>), grid, block, 0, st, d_y, n, d_x, inv,
+                           wpack, sw, delta, m, k, kp, nblocks);
+    } else {
+      if (epilogue == HB_W8A8_EPI_SCALE)
+        hipLaunchKernelGGL((w8a8_decode_rows<4, HB_W8A8_EPI_SCALE>), grid, block, 0, st, d_y, n, d_x, inv, wpack, sw,
+                           delta, m, k, kp, nblocks);
+      else
+        hipLaunchKernelGGL((w8a8_decode_rows<4, HB_W8A8_EPI_SCALE_GELU>), grid, block, 0, st, d_y, n, d_x, inv,
+                           wpack, sw, delta, m, k, kp, nblocks);
+    }
+    return hb_check_launch("w8a8_decode_rows");
   }
   int rc = hb_w8a8_quantize(q, scales, d_x, inv, m, k, s);
   if (rc) return rc;

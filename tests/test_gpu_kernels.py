@@ -190,6 +190,27 @@ def test_w8a8_decode_fused_bit_exact(hip, orc, m, k, n):
     np.testing.assert_array_equal(y.read(np.uint32, m * n).reshape(m, n), ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("m,k,n", [
+    (2, 4096, 14336),   # two rows, C5 gate/up shape
+    (4, 4096, 14336),   # four rows
+    (3, 1568, 1024),    # three rows (one zero A row), k % 64 == 32
+    (4, 32, 64),        # smallest K
+    (4, 4064, 14272),   # row shorter than the threads
+])
+def test_w8a8_decode_rows_bit_exact(hip, orc, m, k, n):
+    """Two to four rows: quantization fused into the weight stream as well."""
+    x, _, blob = make_w8a8(orc, m, k, n, seed=k + n + m, inv_kind="uniform", sums_kind="random", outliers=0.01,
+                           scale_lo=5e-5, scale_hi=5e-4)
+    x[m - 1] *= 7.0  # rows with different scales
+    packed = hip.w8a8_prepack(upload_blob(hip, blob), k, n)
+    ws = hip.DeviceBuffer(hip.w8a8_workspace_bytes(m, k))
+    y = hip.DeviceBuffer(m * n * 4)
+    hip.w8a8_linear(y, hip.DeviceBuffer.from_array(x), packed, m, k, n, ws)
+    hip.sync()
+    ref = orc.linear(x, blob, k, n)
+    np.testing.assert_array_equal(y.read(np.uint32, m * n).reshape(m, n), ref.view(np.uint32))
+
+
 def test_w8a8_decode_fused_special_rows(hip, orc):
     """Zero row (s = 1e-12, u = 128), a row whose absmax is exactly 127
     (s = 1, so u = rint(t + 128)), and halves that round to even."""
