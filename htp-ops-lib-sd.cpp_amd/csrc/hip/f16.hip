@@ -10,6 +10,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 
 #include "hb_internal.h"
 
@@ -737,6 +738,95 @@ __global__ __launch_bounds__(64 * kSkinnyWaves) void qk0_skinny_partial(float *_
   }
 }
 
+// ---------------------------------------------------------------------------
+// Small GEMMs (few rows, K <= W*KPW*32): one workgroup per 16 rows x 16*CF
+// columns over the whole K.  Its W waves split K, each requesting all of its
+// operands (KPW 32-k blocks of x and of CF weight tiles) before the first
+// multiply, so a workgroup pays one memory latency; the waves' sums are added
+// in LDS in wave order (deterministic), then the fp16 readout, bias and
+// activation, and 16-byte row stores (or the channel-major store of mode 3).
+// One launch, no workspace.  Weights are the MFMA A operand, as in the
+// split-K kernel: lane l holds 4 consecutive columns of row l % 16.
+// ---------------------------------------------------------------------------
+
+// TYPE 0: weights are the packed fp16 image; HB_GGML_*: quantized
+// super-blocks, each fragment dequantized in registers as in qk0_skinny_partial
+// (the same fp16 values, so both forms give the same bits).
+template <int CF, int W, int KPW, int TYPE>
+__global__ __launch_bounds__(64 * W) void f16_small(float *__restrict__ y, const float *__restrict__ x,
+                                                   const void *__restrict__ weights, const float *__restrict__ bias,
+                                                   int m, int k, int n, int channels, int mode) {
+  __shared__ hb_f32x4 red[W][CF][64];
+  const int rt = blockIdx.x, g = blockIdx.y;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int kblocks = k / 32;
+  const int kb0 = wave * KPW;
+  const int row = rt * 16 + (lane & 15);
+  const float *xr = x + (size_t)min(row, m - 1) * k + 8 * (lane >> 4);
+  using Raw = typename std::conditional<TYPE == 0, hb_f16x8, Qk0Raw<TYPE == 0 ? HB_GGML_Q4_0 : TYPE>>::type;
+  Raw b[KPW][CF];
+  float4 alo[KPW], ahi[KPW];
+#pragma unroll
+  for (int t = 0; t < KPW; ++t) {
+    const int kb = min(kb0 + t, kblocks - 1);  // blocks past k are loaded, then zeroed
+#pragma unroll
+    for (int j = 0; j < CF; ++j) {
+      if constexpr (TYPE == 0)
+        b[t][j] = *(const hb_f16x8 *)((const uint16_t *)weights + ((size_t)(g * CF + j) * kblocks + kb) * 512u +
+                                      lane * 8);
+      else
+        qk0_load<TYPE>(b[t][j], (const uint8_t *)weights, g * CF + j, kb, kblocks, lane);
+    }
+    alo[t] = *(const float4 *)(xr + kb * 32);
+    ahi[t] = *(const float4 *)(xr + kb * 32 + 4);
+  }
+  hb_f32x4 acc[CF];
+#pragma unroll
+  for (int j = 0; j < CF; ++j) acc[j] = hb_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int t = 0; t < KPW; ++t) {
+    const bool live = kb0 + t < kblocks;
+    const hb_f16x8 a = live ? hb_f16x8{(_Float16)alo[t].x, (_Float16)alo[t].y, (_Float16)alo[t].z,
+                                       (_Float16)alo[t].w, (_Float16)ahi[t].x, (_Float16)ahi[t].y,
+                                       (_Float16)ahi[t].z, (_Float16)ahi[t].w}
+                            : hb_f16x8{};
+#pragma unroll
+    for (int j = 0; j < CF; ++j) {
+      hb_f16x8 w;
+      if constexpr (TYPE == 0)
+        w = b[t][j];
+      else
+        w = qk0_fragment<TYPE>(b[t][j], (g * CF + j) & 1);
+      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, a, acc[j], 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < CF; ++j) red[wave][j][lane] = acc[j];
+  __syncthreads();
+  // one output fragment per wave (CF <= W): rows of lane % 16, 4 columns
+  if (wave >= CF || row >= m) return;
+  const int j = wave;
+  hb_f32x4 tot = red[0][j][lane];
+#pragma unroll
+  for (int w = 1; w < W; ++w) tot += red[w][j][lane];
+  const int col = (g * CF + j) * 16 + 4 * (lane >> 4);
+  hb_f32x4 out;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float v = (float)(_Float16)tot[r];
+    out[r] = bias && col + r < channels ? __fadd_rn(v, bias[col + r]) : v;
+  }
+  if (mode == 3) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (col + r < channels) y[(size_t)(col + r) * m + row] = out[r];
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) out[r] = apply_mode(out[r], mode);
+    *(hb_f32x4 *)(y + (size_t)row * n + col) = out;
+  }
+}
+
 __global__ __launch_bounds__(256) void f16_skinny_epilogue(float *__restrict__ y, const float *__restrict__ ws,
                                                           const float *__restrict__ bias, int m, int n,
                                                           int channels, int mode, int splits) {
@@ -907,6 +997,45 @@ int launch_ring(float *y, const float *x, const uint16_t *packed, const float *b
   return hb_check_launch("f16_gemm_ring");
 }
 
+// Few rows in one launch (f16_small): m <= 128, k <= 3072, a weight image
+// of at most 32 MB, and below the ring path's size.  Column fragments per
+// workgroup: 4 when that still gives a workgroup per two CUs (and k <= 2048,
+// for registers), else 2 when that gives one per CU, else 1.  Returns 0 when
+// the shape does not qualify.  hb_f16_gemm_ws and hb_qk0_gemm_ws plan with
+// the same function, so they take the same summation order.
+int small_cf(int m, int k, int n) {
+  if (m > 128 || k > 96 * 32 || (size_t)n * (size_t)k * 2u > ((size_t)32 << 20) || ring_worth_it(m, k, n)) return 0;
+  const long long rt = (m + 15) / 16;
+  const int cus = compute_units();
+  if (n % 64 == 0 && k <= 64 * 32 && rt * (n / 64) >= cus / 2) return 4;
+  if (rt * (n / 32) >= cus) return 2;
+  return 1;
+}
+
+template <int CF, int TYPE>
+void launch_small_cf(float *y, const float *x, const void *weights, const float *bias, int m, int k, int n,
+                     int channels, int mode, hipStream_t st) {
+  const int kblocks = k / 32;
+  const dim3 grid((m + 15) / 16, n / (16 * CF)), block(1024);
+  if (kblocks <= 16)
+    hipLaunchKernelGGL((f16_small<CF, 16, 1, TYPE>), grid, block, 0, st, y, x, weights, bias, m, k, n, channels, mode);
+  else if (kblocks <= 32)
+    hipLaunchKernelGGL((f16_small<CF, 16, 2, TYPE>), grid, block, 0, st, y, x, weights, bias, m, k, n, channels, mode);
+  else if (kblocks <= 64)
+    hipLaunchKernelGGL((f16_small<CF, 16, 4, TYPE>), grid, block, 0, st, y, x, weights, bias, m, k, n, channels, mode);
+  else if constexpr (CF < 4)
+    hipLaunchKernelGGL((f16_small<CF, 16, 6, TYPE>), grid, block, 0, st, y, x, weights, bias, m, k, n, channels, mode);
+}
+
+template <int TYPE>
+int launch_small(int cf, float *y, const float *x, const void *weights, const float *bias, int m, int k, int n,
+                 int channels, int mode, hipStream_t st) {
+  if (cf == 4) launch_small_cf<4, TYPE>(y, x, weights, bias, m, k, n, channels, mode, st);
+  else if (cf == 2) launch_small_cf<2, TYPE>(y, x, weights, bias, m, k, n, channels, mode, st);
+  else launch_small_cf<1, TYPE>(y, x, weights, bias, m, k, n, channels, mode, st);
+  return hb_check_launch("f16_small");
+}
+
 }  // namespace
 
 extern "C" {
@@ -978,6 +1107,14 @@ int hb_qk0_gemm_ws(float *d_y, const float *d_x, const uint8_t *d_blocks, int m,
                          k, n);
     return hb_check_launch("qk0_decode");
   }
+  // Small shapes in one launch, planned as hb_f16_gemm_ws plans them.
+  if (const int cf = aligned(d_y, 16) ? small_cf(m, k, n) : 0) {
+    if (type == HB_GGML_Q4_0)
+      return launch_small<HB_GGML_Q4_0>(cf, d_y, d_x, d_blocks, nullptr, m, k, n, n, 0, st);
+    if (type == HB_GGML_IQ4_NL)
+      return launch_small<HB_GGML_IQ4_NL>(cf, d_y, d_x, d_blocks, nullptr, m, k, n, n, 0, st);
+    return launch_small<HB_GGML_Q8_0>(cf, d_y, d_x, d_blocks, nullptr, m, k, n, n, 0, st);
+  }
   int splits = 1, kpw = 1;
   skinny_plan(k, n, splits, kpw);
   const int cols = skinny_cols(n);
@@ -1014,6 +1151,8 @@ int hb_f16_gemm_ws(float *d_y, const float *d_x, const uint16_t *d_packed, const
   if (!aligned(d_x, 16) || !aligned(d_packed, 16) || !aligned(d_y, 4) || (d_bias && !aligned(d_bias, 4)))
     return hb_invalid("hb_f16_gemm alignment");
   hipStream_t st = hb_resolve_stream(s);
+  if (const int cf = aligned(d_y, 16) ? small_cf(m, k, n) : 0)
+    return launch_small<0>(cf, d_y, d_x, d_packed, d_bias, m, k, n, channels, mode, st);
   // The split-K path holds m <= 128 rows (8 row fragments) of partial sums.
   const size_t need = split_k_bytes(m, k, n);
   // Tiled variant by output size; the split-K path takes over when that grid

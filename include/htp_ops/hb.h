@@ -165,6 +165,9 @@ int hb_qk0_gemm_ws(float *d_y, const float *d_x, const uint8_t *d_blocks, int m,
 
 /*
  * y = epilogue(fp16(fp16(x) @ W)); x f32 [m][k]; bias f32[channels] or NULL.
+ * Small shapes (m <= 128, k <= 3072, a weight image of at most 32 MB, a
+ * 16-byte aligned y) run as one kernel over the whole K per 16-row tile, with
+ * or without a workspace.
  * mode 0: + bias; 1: + bias, GELU (tanh form); 2: + bias, QuickGELU;
  * mode 3: + bias, stored channel-major y[c][m] for c < channels.
  */
