@@ -727,6 +727,107 @@ __global__ __launch_bounds__(1024, 8) void w8a8_decode_rows(void *__restrict__ y
 }
 
 // ---------------------------------------------------------------------------
+// Small problems (m <= 128, k <= 1536) in one launch: a 16-wave workgroup per
+// 16 rows x 16*CF columns quantizes its 16 rows itself (one wave per row,
+// exactly the quantization kernels' arithmetic) into LDS, then multiplies the
+// whole K with every wave's weight tiles requested up front, adds the waves'
+// int32 sums in LDS and applies the epilogue.  The weights are the MFMA A
+// operand, so a lane ends with 4 consecutive columns of one row and stores
+// them as one 16-byte vector.
+// ---------------------------------------------------------------------------
+
+template <int CF, int KPW, int VX, int EPI>
+__global__ __launch_bounds__(1024) void w8a8_small(void *__restrict__ y, const float *__restrict__ x,
+                                                   const float *__restrict__ inv, const int8_t *__restrict__ wpack,
+                                                   const float *__restrict__ sw, const int32_t *__restrict__ corr,
+                                                   int m, int k, int n, int kp) {
+  constexpr int WAVES = 16;
+  __shared__ __attribute__((aligned(16))) int8_t qs[16][VX * 256];
+  __shared__ float srow[16];
+  __shared__ hb_i32x4 red[WAVES][CF][64];
+  const int rt = blockIdx.x, g = blockIdx.y;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int kc = kp / kKStep, nvec = k / 4;
+  // 1. this wave's row (clamped; rows past m are quantized but never stored)
+  const int qrow = min(rt * 16 + wave, m - 1);
+  const float4 *xr = (const float4 *)(x + (size_t)qrow * k);
+  float4 a[VX], iv[VX];
+#pragma unroll
+  for (int j = 0; j < VX; ++j) {
+    const int v = min(lane + 64 * j, nvec - 1);
+    a[j] = xr[v];
+    iv[j] = ((const float4 *)inv)[v];
+  }
+  // 2. the weight tiles of this wave's k-blocks (clamped; past kc never used)
+  const int kb0 = wave * KPW;
+  hb_i32x4 b[KPW][CF];
+#pragma unroll
+  for (int t = 0; t < KPW; ++t)
+#pragma unroll
+    for (int j = 0; j < CF; ++j)
+      b[t][j] = __builtin_nontemporal_load(
+          (const hb_i32x4 *)(wpack + ((size_t)(g * CF + j) * kc + min(kb0 + t, kc - 1)) * kFragBytes + lane * 16));
+  // 3. quantize the row into LDS
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < VX; ++j) {
+    a[j] = make_float4(__fmul_rn(a[j].x, iv[j].x), __fmul_rn(a[j].y, iv[j].y), __fmul_rn(a[j].z, iv[j].z),
+                       __fmul_rn(a[j].w, iv[j].w));
+    if (lane + 64 * j < nvec)
+      amax = fmaxf(amax, fmaxf(fmaxf(fabsf(a[j].x), fabsf(a[j].y)), fmaxf(fabsf(a[j].z), fabsf(a[j].w))));
+  }
+  amax = wave_max(amax);
+  const float s = fmaxf(__fdiv_rn(amax, 127.0f), 1e-12f);
+  const float r = __fdiv_rn(1.0f, s);
+  if (lane == 0) srow[wave] = s;
+#pragma unroll
+  for (int j = 0; j < VX; ++j) {
+    const int v = lane + 64 * j;
+    if (v < kp / 4) {
+      const uint32_t word = v < nvec ? (quantize_byte(a[j].x, r) | (quantize_byte(a[j].y, r) << 8) |
+                                        (quantize_byte(a[j].z, r) << 16) | (quantize_byte(a[j].w, r) << 24))
+                                     : 0u;
+      *(uint32_t *)(&qs[wave][4 * v]) = word;
+    }
+  }
+  __syncthreads();
+  // 4. MFMA over this wave's k-blocks: weights as A (16 columns), rows as B
+  hb_i32x4 acc[CF];
+#pragma unroll
+  for (int j = 0; j < CF; ++j) acc[j] = hb_i32x4{0, 0, 0, 0};
+#pragma unroll
+  for (int t = 0; t < KPW; ++t) {
+    const int kt = kb0 + t;
+    if (kt < kc) {
+      const hb_i32x4 av = *(const hb_i32x4 *)(&qs[lane & 15][kt * kKStep + (lane >> 4) * 16]);
+#pragma unroll
+      for (int j = 0; j < CF; ++j) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(b[t][j], av, acc[j], 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < CF; ++j) red[wave][j][lane] = acc[j];
+  __syncthreads();
+  // 5. wave j < CF finishes column fragment j: lane l has row l % 16, columns
+  //    4*(l/16) .. +3
+  const int row = rt * 16 + (lane & 15);
+  if (wave >= CF || row >= m) return;
+  const int j = wave;
+  hb_i32x4 tot = red[0][j][lane];
+#pragma unroll
+  for (int w = 1; w < WAVES; ++w) {
+    const hb_i32x4 p = red[w][j][lane];
+    tot = hb_i32x4{(int)((uint32_t)tot[0] + (uint32_t)p[0]), (int)((uint32_t)tot[1] + (uint32_t)p[1]),
+                   (int)((uint32_t)tot[2] + (uint32_t)p[2]), (int)((uint32_t)tot[3] + (uint32_t)p[3])};
+  }
+  const int col = (g * CF + j) * 16 + 4 * (lane >> 4);
+  const float sv = srow[lane & 15];
+  hb_u32x4 out;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) out[q] = epilogue_bits<EPI>(tot[q], corr[col + q], sw[col + q], sv);
+  __builtin_nontemporal_store(out, (hb_u32x4 *)((uint32_t *)y + (size_t)row * n + col));
+}
+
+// ---------------------------------------------------------------------------
 // Raw accumulator -> byte-plane export of the CPU-control variant.
 // One thread per output byte position (row, 32-column half, byte in 128).
 // ---------------------------------------------------------------------------
@@ -924,6 +1025,39 @@ int launch_decode_fused(void *y, const float *x, const float *inv, const int8_t 
   return hb_check_launch("w8a8_decode_fused");
 }
 
+// One-launch small path (w8a8_small): 5 <= m <= 128, kp <= 1536, a weight
+// image of at most 16 MB.  Column fragments per workgroup as for the F16
+// small kernel: 4 while that leaves a workgroup per two CUs, 2 while one per
+// CU, else 1.
+template <int VX, int KPW, int EPI>
+void launch_w8a8_small_v(int cf, void *y, const float *x, const float *inv, const int8_t *wpack, const float *sw,
+                         const int32_t *corr, int m, int k, int n, int kp, hipStream_t st) {
+  const dim3 block(1024);
+  const int rt = (m + 15) / 16;
+  if (cf == 4)
+    hipLaunchKernelGGL((w8a8_small<4, KPW, VX, EPI>), dim3(rt, n / 64), block, 0, st, y, x, inv, wpack, sw, corr, m,
+                       k, n, kp);
+  else if (cf == 2)
+    hipLaunchKernelGGL((w8a8_small<2, KPW, VX, EPI>), dim3(rt, n / 32), block, 0, st, y, x, inv, wpack, sw, corr, m,
+                       k, n, kp);
+  else
+    hipLaunchKernelGGL((w8a8_small<1, KPW, VX, EPI>), dim3(rt, n / 16), block, 0, st, y, x, inv, wpack, sw, corr, m,
+                       k, n, kp);
+}
+
+template <int EPI>
+int launch_w8a8_small(void *y, const float *x, const float *inv, const int8_t *wpack, const float *sw,
+                      const int32_t *corr, int m, int k, int n, int kp, hipStream_t st) {
+  const long long rt = (m + 15) / 16;
+  const int cus = compute_units();
+  const int cf = (n % 64 == 0 && rt * (n / 64) >= cus / 2) ? 4 : (n % 32 == 0 && rt * (n / 32) >= cus) ? 2 : 1;
+  if (kp <= 768)
+    launch_w8a8_small_v<3, 1, EPI>(cf, y, x, inv, wpack, sw, corr, m, k, n, kp, st);
+  else
+    launch_w8a8_small_v<6, 2, EPI>(cf, y, x, inv, wpack, sw, corr, m, k, n, kp, st);
+  return hb_check_launch("w8a8_small");
+}
+
 }  // namespace
 
 extern "C" {
@@ -1076,6 +1210,26 @@ int hb_w8a8_linear(float *d_y, const float *d_x, const void *d_packed, int m, in
     return epilogue == HB_W8A8_EPI_SCALE
                ? launch_decode_fused<HB_W8A8_EPI_SCALE>(d_y, d_x, inv, wpack, sw, delta, k, n, kp, st)
                : launch_decode_fused<HB_W8A8_EPI_SCALE_GELU>(d_y, d_x, inv, wpack, sw, delta, k, n, kp, st);
+  }
+  // Small problems: one launch that quantizes its own rows.  Every 16-row
+  // tile streams the whole weight matrix, so the path is taken while the
+  // weight bytes summed over row tiles stay within 16 MB (77x768x3072:
+  // 8.0 -> 6.1 us; 64x1536x6144, 38 MB over its 4 row tiles, is faster as
+  // quantize + GEMM: 9.5 against 16.0 us).  HTP_OPS_AMD_W8A8_SMALL=0 turns
+  // the path off, for comparisons.
+  static const int small_on = getenv("HTP_OPS_AMD_W8A8_SMALL") ? atoi(getenv("HTP_OPS_AMD_W8A8_SMALL")) : 1;
+  if (small_on && m >= 5 && m <= 128 && kp <= 1536 && k >= 32 && k % 32 == 0 && n >= 16 && n % 16 == 0 &&
+      (size_t)((m + 15) / 16) * (size_t)n * (size_t)kp <= ((size_t)16 << 20) && d_y && d_x && aligned(d_x, 16) &&
+      aligned(d_y, 16) &&
+      aligned(d_packed, 256) && (epilogue == HB_W8A8_EPI_SCALE || epilogue == HB_W8A8_EPI_SCALE_GELU)) {
+    const uint8_t *base = (const uint8_t *)d_packed;
+    const int8_t *wpack = (const int8_t *)(base + hb_w8a8_packed_offset(k, n, HB_W8A8_WEIGHTS));
+    const float *sw = (const float *)(base + hb_w8a8_packed_offset(k, n, HB_W8A8_SW));
+    const int32_t *delta = (const int32_t *)(base + hb_w8a8_packed_offset(k, n, HB_W8A8_DELTA));
+    hipStream_t st = hb_resolve_stream(s);
+    return epilogue == HB_W8A8_EPI_SCALE
+               ? launch_w8a8_small<HB_W8A8_EPI_SCALE>(d_y, d_x, inv, wpack, sw, delta, m, k, n, kp, st)
+               : launch_w8a8_small<HB_W8A8_EPI_SCALE_GELU>(d_y, d_x, inv, wpack, sw, delta, m, k, n, kp, st);
   }
   // Two to four rows: quantization fused into the weight stream as well.
   const int nblocks = n / 16;

@@ -127,7 +127,12 @@ int hb_w8a8_gemm(void *d_y, int ldy, const int8_t *d_q, const float *d_scales, c
  * The environment variable HTP_OPS_AMD_W8A8_TILE gives the initial value. */
 int hb_w8a8_force_tile(int index);
 
-/* Full opcode-15 computation: quantize + GEMM + epilogue (workspace from hb_w8a8_workspace_bytes). */
+/* Full opcode-15 computation: quantize + GEMM + epilogue (workspace from hb_w8a8_workspace_bytes).
+ * With the SCALE or SCALE_GELU epilogue, 16-byte aligned x and y and K a
+ * multiple of 32, small problems run as one launch that quantizes its own
+ * rows: m == 1 (K <= 16384), 2 <= m <= 4 (K <= 4096), and 5 <= m <= 128 with
+ * K <= 1536 and ceil(m/16) * n * K <= 16 MB (HTP_OPS_AMD_W8A8_SMALL=0 turns
+ * the last one off).  Every path gives the same bits. */
 int hb_w8a8_linear(float *d_y, const float *d_x, const void *d_packed, int m, int k, int n, int epilogue,
                    void *d_workspace, size_t workspace_bytes, hb_stream s);
 

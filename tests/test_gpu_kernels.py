@@ -211,6 +211,33 @@ def test_w8a8_decode_rows_bit_exact(hip, orc, m, k, n):
     np.testing.assert_array_equal(y.read(np.uint32, m * n).reshape(m, n), ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("m,k,n,gelu", [
+    (77, 768, 3072, False),   # BASELINE C1: 64-column workgroups
+    (5, 1536, 2048, True),    # fewest rows, longest k of the path, GELU
+    (128, 1504, 192, False),  # k % 64 == 32, few column groups: 16-column workgroups
+    (77, 32, 64, True),       # smallest K
+    (100, 768, 2048, False),  # rows past m in the last 16-row tile
+])
+def test_w8a8_small_bit_exact(hip, orc, m, k, n, gelu):
+    """5 <= m <= 128, k <= 1536: one launch that quantizes its own rows."""
+    x, _, blob = make_w8a8(orc, m, k, n, seed=m + k + n, inv_kind="uniform", sums_kind="random", outliers=0.01,
+                           scale_lo=1e-3 if gelu else 1e-4, scale_hi=1e-2 if gelu else 1e-3)
+    x[::7] *= 5.0  # rows with different scales
+    packed = hip.w8a8_prepack(upload_blob(hip, blob), k, n)
+    ws = hip.DeviceBuffer(hip.w8a8_workspace_bytes(m, k))
+    y = hip.DeviceBuffer(m * n * 4)
+    hip.w8a8_linear(y, hip.DeviceBuffer.from_array(x), packed, m, k, n, ws,
+                    epilogue=hip.EPI_SCALE_GELU if gelu else hip.EPI_SCALE)
+    hip.sync()
+    ref = orc.linear(x, blob, k, n)
+    if gelu:
+        ref = orc.gelu_tanh_array(ref)
+        got = y.read(np.float32, m * n).reshape(m, n)
+        np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-30)
+    else:
+        np.testing.assert_array_equal(y.read(np.uint32, m * n).reshape(m, n), ref.view(np.uint32))
+
+
 def test_w8a8_decode_fused_special_rows(hip, orc):
     """Zero row (s = 1e-12, u = 128), a row whose absmax is exactly 127
     (s = 1, so u = rint(t + 128)), and halves that round to even."""
