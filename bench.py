@@ -618,9 +618,9 @@ def main():
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--rotate", type=int, default=6)
-    ap.add_argument("--config", default="headline", choices=["headline", "all", "c2", "aux", "qk0"],
-                    help="c2 / aux / qk0: only the F16 text-MLP case / the opcode-19 cases / the opcode-2/3/4 "
-                         "cases (profiling aids; print those cases alone)")
+    ap.add_argument("--config", default="headline", choices=["headline", "all", "small", "aux", "qk0"],
+                    help="small / aux / qk0: only the C1 W8A8 and C2 F16 text-MLP cases / the opcode-19 cases / "
+                         "the opcode-2/3/4 cases (profiling aids; print those cases alone)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--traffic-probe", action="store_true")
     ap.add_argument("--profile-summary", metavar="DIR")
@@ -638,8 +638,10 @@ def main():
         return
 
     hip.init(0)
-    if args.config == "c2":
-        print(json.dumps({"C2_f16_text_mlp_77x768x3072x768": f16_mlp_case(args.steps, args.warmup)}), flush=True)
+    if args.config == "small":
+        r = run_w8a8(77, 768, 3072, args.steps, args.warmup, 4, scale=(1e-4, 1e-3))
+        print(json.dumps({"C1_77x768x3072_us": round(r["ms_per_step"] * 1e3, 2),
+                          "C2_f16_text_mlp_77x768x3072x768": f16_mlp_case(args.steps, args.warmup)}), flush=True)
         return
     if args.config == "aux":
         print(json.dumps({"opcode19_aux": aux_cases(args.steps, args.warmup, with_cpu=not args.no_cpu)}), flush=True)
