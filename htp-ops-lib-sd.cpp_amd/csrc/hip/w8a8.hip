@@ -613,6 +613,100 @@ __global__ __launch_bounds__(64 * WAVES, MINW) void w8a8_decode_fused(void *__re
 }
 
 // ---------------------------------------------------------------------------
+// Single-row decode balanced over the CUs (m == 1, k <= 2048).  Workgroup g
+// owns the 8-column half blocks [g*H, g*H + H) with H <= 7, which touch at
+// most four 16-column blocks; with one workgroup per CU every CU streams the
+// same number of weight bytes (n = 14336 on 256 CUs: 3.5 blocks each, where
+// whole blocks per workgroup leave the busiest CU with 4).  Four waves per
+// touched block split its k-tiles.  A lane whose half block lies outside the
+// range gets an out-of-range buffer offset, so its loads return zeros without
+// a memory request, and it stores nothing.  Quantization and arithmetic are
+// those of w8a8_decode_fused, so results are identical.
+// ---------------------------------------------------------------------------
+
+template <int VW, int EPI>
+__global__ __launch_bounds__(1024) void w8a8_decode_even(void *__restrict__ y, const float *__restrict__ x,
+                                                         const float *__restrict__ inv,
+                                                         const int8_t *__restrict__ wpack,
+                                                         const float *__restrict__ sw,
+                                                         const int32_t *__restrict__ corr, int k, int kp,
+                                                         int nblocks, int hpw) {
+  constexpr int WAVES = 16, SLOTS = 4, WPS = WAVES / SLOTS;
+  constexpr int KQ = VW * WPS * kKStep;  // the longest row served
+  static_assert(KQ <= 4 * 64 * WAVES, "one float4 of the row per thread");
+  __shared__ __attribute__((aligned(16))) int8_t qs[KQ];
+  __shared__ float red[WAVES];
+  __shared__ int32_t part[WAVES][16];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, tid = threadIdx.x;
+  const int slot = wave / WPS, wis = wave % WPS;
+  const int h0 = blockIdx.x * hpw, h1 = min(h0 + hpw, 2 * nblocks);
+  const int nb_raw = h0 / 2 + slot;
+  const int nb = min(nb_raw, nblocks - 1);
+  const int half = 2 * nb_raw + ((lane & 15) >> 3);  // this lane's column's half block
+  const bool mine = half >= h0 && half < h1;         // implies nb_raw < nblocks
+  const int kc = kp / kKStep, nvec = k / 4;
+  const int col = nb * 16 + (lane & 15);
+  const int32_t cc = corr[col];
+  const float sc = sw[col];
+  // 1. the row, the smoothing vector and this wave's weight tiles, all
+  //    requested before any is used (tiles past kc are fetched, never used)
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void *)x, 0, (uint32_t)nvec * 16u, 0x00020000);
+  const __amdgpu_buffer_rsrc_t ri = __builtin_amdgcn_make_buffer_rsrc((void *)inv, 0, (uint32_t)nvec * 16u, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rw =
+      __builtin_amdgcn_make_buffer_rsrc((void *)wpack, 0, (uint32_t)nblocks * (uint32_t)kc * kFragBytes, 0x00020000);
+  const hb_u32x4 xv = __builtin_amdgcn_raw_buffer_load_b128(rx, (uint32_t)tid * 16u, 0, 0);
+  const hb_u32x4 iw = __builtin_amdgcn_raw_buffer_load_b128(ri, (uint32_t)tid * 16u, 0, 0);
+  const uint32_t wv =
+      mine ? ((uint32_t)nb * (uint32_t)kc + (uint32_t)(wis * VW)) * kFragBytes + (uint32_t)lane * 16u : 0x80000000u;
+  hb_i32x4 b[VW];
+#pragma unroll
+  for (int i = 0; i < VW; ++i) {
+    const hb_u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(rw, wv + i * kFragBytes, 0, 2);
+    b[i] = hb_i32x4{(int)t[0], (int)t[1], (int)t[2], (int)t[3]};
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // 2. row absmax of t = x * inv, then the quantized row into LDS
+  const float4 a = make_float4(__fmul_rn(__uint_as_float(xv[0]), __uint_as_float(iw[0])),
+                               __fmul_rn(__uint_as_float(xv[1]), __uint_as_float(iw[1])),
+                               __fmul_rn(__uint_as_float(xv[2]), __uint_as_float(iw[2])),
+                               __fmul_rn(__uint_as_float(xv[3]), __uint_as_float(iw[3])));
+  float amax = tid < nvec ? fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))) : 0.0f;
+  amax = wave_max(amax);
+  if (lane == 0) red[wave] = amax;
+  __syncthreads();
+  amax = red[0];
+#pragma unroll
+  for (int w = 1; w < WAVES; ++w) amax = fmaxf(amax, red[w]);
+  const float s = fmaxf(__fdiv_rn(amax, 127.0f), 1e-12f);
+  const float r = __fdiv_rn(1.0f, s);
+  if (tid < kp / 4) {
+    const uint32_t word = tid < nvec ? (quantize_byte(a.x, r) | (quantize_byte(a.y, r) << 8) |
+                                        (quantize_byte(a.z, r) << 16) | (quantize_byte(a.w, r) << 24))
+                                     : 0u;
+    *(uint32_t *)(qs + 4 * tid) = word;
+  }
+  __syncthreads();
+  // 3. MFMA: lanes of row 0 (lane % 16 == 0) carry the row, the others zeros
+  const bool has_row = (lane & 15) == 0;
+  hb_i32x4 acc = {0, 0, 0, 0};
+#pragma unroll
+  for (int i = 0; i < VW; ++i) {
+    const int kt = wis * VW + i;
+    if (kt < kc) {
+      const hb_i32x4 av = has_row ? *(const hb_i32x4 *)(qs + kt * kKStep + (lane >> 4) * 16) : hb_i32x4{0, 0, 0, 0};
+      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b[i], acc, 0, 0, 0);
+    }
+  }
+  if (lane < 16) part[wave][lane] = acc[0];
+  __syncthreads();
+  if (wis != 0 || lane >= 16 || !mine) return;
+  int32_t tot = part[wave][lane];
+#pragma unroll
+  for (int w = 1; w < WPS; ++w) tot = (int32_t)((uint32_t)tot + (uint32_t)part[wave + w][lane]);
+  __builtin_nontemporal_store(epilogue_bits<EPI>(tot, cc, sc, s), (uint32_t *)y + col);
+}
+
+// ---------------------------------------------------------------------------
 // A few rows (2 <= m <= R <= 4, k <= 4096) with the quantization fused in:
 // the 16-wave, two-block shape of w8a8_decode_fused.  Every workgroup
 // quantizes all m rows itself (one workgroup reduction for all rows) before
@@ -1016,6 +1110,18 @@ int launch_decode_fused(void *y, const float *x, const float *inv, const int8_t 
   const int per_cu_one = (nblocks + cus - 1) / cus;
   const int per_cu_two = 2 * (((nblocks + 1) / 2 + cus - 1) / cus);
   bool done = false;
+  // k <= 2048 with 2.5-3.5 blocks per CU: the half-block split, one
+  // workgroup per CU (n = 9216, k = 2048: 6.2 against 7.5 us).  At k = 4096
+  // it is slower than the shapes below (n = 14336: 11.8 against 11.4 us;
+  // n = 12288: 11.2 against 10.1 us): its 16 tiles per wave take 96 VGPRs,
+  // which leaves a CU one 16-wave workgroup where the shapes below keep 24-32
+  // waves per CU in flight.
+  const int halves = 2 * nblocks, hpw = (halves + cus - 1) / cus;
+  if ((size_t)nblocks * (size_t)kp * 16u < ((size_t)1 << 31) && kc <= 32 && hpw >= 5 && hpw <= 7) {
+    hipLaunchKernelGGL((w8a8_decode_even<8, EPI>), dim3((halves + hpw - 1) / hpw), dim3(1024), 0, st, y, x, inv,
+                       wpack, sw, corr, k, kp, nblocks, hpw);
+    return hb_check_launch("w8a8_decode_even");
+  }
   if (buf && kc > 48 && nblocks >= cus && per_cu_two <= per_cu_one)
     done = launch_decode_cfg<16, 2, 8, 8, true, EPI>(y, x, inv, wpack, sw, corr, k, nblocks, kp, st);
   if (!done) done = launch_decode_cfg<8, 1, 8, 1, false, EPI>(y, x, inv, wpack, sw, corr, k, nblocks, kp, st);

@@ -168,6 +168,9 @@ DECODE_FUSED_SHAPES = [
     (1, 4064, 14272),  # two blocks per workgroup, row shorter than the threads
     (1, 3104, 8192),   # two blocks per workgroup, 49 of 64 tiles per block present
     (1, 4096, 12288),  # one block per workgroup (three per CU)
+    (1, 2048, 9216),   # 5 half blocks per workgroup (w8a8_decode_even)
+    (1, 1568, 10240),  # 5 half blocks per workgroup, k % 64 == 32
+    (1, 2016, 14272),  # 7 half blocks per workgroup (odd starts), a short last workgroup, row shorter than the threads
     (1, 14336, 4096),  # BASELINE decode down shape
     (1, 4160, 256),    # just past the first variant
     (1, 8192, 512),
