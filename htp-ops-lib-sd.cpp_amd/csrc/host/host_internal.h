@@ -53,6 +53,9 @@ enum {
  * sampled hash).  *built is set when a prepack ran. */
 int htp_weight_cache_get(int kind, const htp_view *src, int k, int n, uint64_t sig, void **packed, int *built,
                          hb_stream s);
+/* 1 when a valid image for the source view is cached (what
+ * htp_weight_cache_get would return without building), else 0. */
+int htp_weight_cache_peek(int kind, const htp_view *src, int k, int n, uint64_t sig);
 int htp_weight_cache_drop_fd(int fd);
 int htp_weight_cache_enabled(void);
 

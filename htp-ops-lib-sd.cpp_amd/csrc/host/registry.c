@@ -361,6 +361,19 @@ static int qk0_type(int kind) {
   }
 }
 
+int htp_weight_cache_peek(int kind, const htp_view *src, int k, int n, uint64_t sig) {
+  if (!htp_weight_cache_enabled()) return 0;
+  int found = 0;
+  pthread_mutex_lock(&g_lock);
+  for (size_t i = 0; i < g_cache_count && !found; ++i) {
+    const cache_entry *c = &g_cache[i];
+    found = c->kind == kind && c->fd == src->fd && c->offset == src->offset && c->bytes == src->bytes &&
+            c->k == k && c->n == n && c->sig == sig && c->generation == src->generation;
+  }
+  pthread_mutex_unlock(&g_lock);
+  return found;
+}
+
 int htp_weight_cache_get(int kind, const htp_view *src, int k, int n, uint64_t sig, void **packed, int *built,
                          hb_stream s) {
   *packed = NULL;
