@@ -108,6 +108,28 @@ def test_opcode15_weight_cache_follows_rewrites(hip, orc):
     assert h.lib().htp_ops_amd_invalidate_weights(cst.fd) >= 1
 
 
+def test_opcode15_device_blob_header_after_cache_hit(hip, orc):
+    """A cached device blob skips the header read-back; a rewrite with a bad
+    header is still rejected (-3), and a good rewrite runs again."""
+    m, k, n = 8, 128, 128
+    x, blob = w8a8_inputs(orc, m, k, n, seed=31)
+    out, act, cst = rpc(m * n * 4, True), rpc(m * k * 4, True), rpc(blob.nbytes, True)
+    act.write(x)
+    cst.write(blob)
+    params = h.w8a8_params((out.fd, 0), (act.fd, 0), (cst.fd, 0), m, k, n)
+    ref = orc.linear(x, blob, k, n)
+    for _ in range(2):  # build, then a cache hit
+        assert h.execute(15, params)[0] == 0
+        assert np.array_equal(out.read(np.float32, m * n).reshape(m, n), ref)
+    bad = blob.copy()
+    bad[:4] ^= 0xFF  # magic
+    cst.write(bad)
+    assert h.execute(15, params)[0] == -3
+    cst.write(blob)
+    assert h.execute(15, params)[0] == 0
+    assert np.array_equal(out.read(np.float32, m * n).reshape(m, n), ref)
+
+
 @pytest.mark.parametrize("device", [False, True])
 @pytest.mark.parametrize("mode,channels", [(0, 768), (1, 768), (2, 768), (3, 700)])
 def test_opcode16_modes(hip, orc, device, mode, channels):
