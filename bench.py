@@ -88,7 +88,8 @@ class W8A8Set:
         self.host_x, self.host_blob = (x, blob) if seed == 0 else (None, None)
 
 
-def run_w8a8(m, k, n, steps, warmup, rotate, outliers=0.0, scale=(1e-4, 1e-3), settle_ms=SETTLE_MS):
+def run_w8a8(m, k, n, steps, warmup, rotate, outliers=0.0, scale=(1e-4, 1e-3), settle_ms=SETTLE_MS,
+             epilogue=None):
     """Times `steps` opcode-15 steps launched in stream order (the library's
     own launches, as a caller issues them; the host enqueues ahead of the
     GPU), then the same number of GEMM-only and quantize-only launches, for
@@ -100,17 +101,19 @@ def run_w8a8(m, k, n, steps, warmup, rotate, outliers=0.0, scale=(1e-4, 1e-3), s
     stream = hip.default_stream()
     sets = [W8A8Set(m, k, n, seed, outliers, *scale) for seed in range(rotate)]
 
+    epi = hip.EPI_SCALE if epilogue is None else epilogue
+
     def quant(st):
         hip.check(lib.hb_w8a8_quantize(st.q_ptr, st.s_ptr, st.x.ptr, st.inv_ptr, m, k, stream), "quantize")
 
     def gemm(st):
-        hip.check(lib.hb_w8a8_gemm(st.y.ptr, n, st.q_ptr, st.s_ptr, st.packed.ptr, m, k, n, hip.EPI_SCALE,
+        hip.check(lib.hb_w8a8_gemm(st.y.ptr, n, st.q_ptr, st.s_ptr, st.packed.ptr, m, k, n, epi,
                                    stream), "gemm")
 
     def step(st):
         # the full op as the library runs it: quantize + GEMM, or for one row
         # the fused decode kernel
-        hip.check(lib.hb_w8a8_linear(st.y.ptr, st.x.ptr, st.packed.ptr, m, k, n, hip.EPI_SCALE, st.ws.ptr,
+        hip.check(lib.hb_w8a8_linear(st.y.ptr, st.x.ptr, st.packed.ptr, m, k, n, epi, st.ws.ptr,
                                      st.ws.nbytes, stream), "linear")
 
     def capture(fn, count):
@@ -288,10 +291,12 @@ def all_configs(steps, warmup, with_cpu=False):
     for name, (m, k, n, outl, sc) in {
             "C1_77x768x3072": (77, 768, 3072, 0.0, (1e-4, 1e-3)),
             "C3_qkv_4096x1536x4608": (4096, 1536, 4608, 0.01, (1e-4, 1e-3)),
+            "C3_up_gelu_4096x1536x6144": (4096, 1536, 6144, 0.01, (1e-4, 1e-3)),
             "C3_down_4096x6144x1536": (4096, 6144, 1536, 0.01, (1e-4, 1e-3)),
             "C4_qkv_2048x4096x6144": (2048, 4096, 6144, 0.0, (5e-5, 5e-4)),
             "C4_o_2048x4096x4096": (2048, 4096, 4096, 0.0, (5e-5, 5e-4))}.items():
-        r = run_w8a8(m, k, n, steps, warmup, 4, outliers=outl, scale=sc)
+        r = run_w8a8(m, k, n, steps, warmup, 4, outliers=outl, scale=sc,
+                     epilogue=hip.EPI_SCALE_GELU if "gelu" in name else None)
         out[name] = {"us": round(r["ms_per_step"] * 1e3, 2),
                      "tops": round(2 * m * n * k / (r["ms_per_step"] * 1e-3) / 1e12, 1),
                      "gemm_us": round(r["gemm_ms_mean"] * 1e3, 2)}

@@ -259,13 +259,18 @@ __global__ __launch_bounds__(kRowThreads) void w8a8_quant_rows_wg(int8_t *__rest
 
 __device__ inline float gelu_tanh(float z) {
   // z * sigmoid(1.5957691216057308*(z + 0.044715*z^3)), stable sigmoid
-  // (reference src/dsp/ops/mat_mul.c:788-826, mode 1).
+  // (reference src/dsp/ops/mat_mul.c:788-826, mode 1).  The exponential and
+  // the reciprocal are the hardware's v_exp_f32 and v_rcp_f32 (each within
+  // 1 ulp; the argument is at least -126, 1 + e lies in [1, 2]), about 3e-7
+  // relative in all, inside the 1e-5 bound; IEEE division would cost a long
+  // sequence per output element (the GELU GEMM at 4096x1536x6144 took 59.6
+  // against 47.0 us).
   const float cubic = __fmul_rn(__fmul_rn(z, z), z);
   const float inner = __fadd_rn(z, __fmul_rn(cubic, 0.044715f));
   const float a = __fmul_rn(inner, 1.5957691216057308f);
   const float neg = fmaxf(__fmul_rn(fabsf(a), -1.4426950408889634f), -126.0f);
-  const float e = exp2f(neg);
-  const float inv = __fdiv_rn(1.0f, __fadd_rn(e, 1.0f));
+  const float e = __builtin_amdgcn_exp2f(neg);
+  const float inv = __builtin_amdgcn_rcpf(__fadd_rn(e, 1.0f));
   const float sig = a < 0.0f ? __fmul_rn(e, inv) : inv;
   return __fmul_rn(z, sig);
 }
