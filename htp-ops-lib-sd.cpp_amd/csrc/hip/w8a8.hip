@@ -618,6 +618,87 @@ __global__ __launch_bounds__(64 * WAVES, MINW) void w8a8_decode_fused(void *__re
 }
 
 // ---------------------------------------------------------------------------
+// Few-row GEMM on quantized rows (2 <= m <= 16, k <= 4096) in the shape of
+// the one-row kernel: 16 waves, two 16-column blocks per workgroup, each
+// wave's 8 weight tiles requested up front with buffer loads.  The A tiles
+// (rows 0-15 of the quantized activations, 1 KB per k-step) are read once
+// per workgroup into LDS, requested before the weights so waiting for them
+// does not wait for the weight stream; rows past m are zeroed at the MFMA.
+// ---------------------------------------------------------------------------
+
+template <int EPI>
+__global__ __launch_bounds__(1024) void w8a8_decode_q(void *__restrict__ y, int ldy, const int8_t *__restrict__ q,
+                                                      const float *__restrict__ scales,
+                                                      const int8_t *__restrict__ wpack,
+                                                      const float *__restrict__ sw,
+                                                      const int32_t *__restrict__ corr, int m, int kp, int nblocks) {
+  constexpr int WAVES = 16, WPB = 8, VW = 8, KT = VW * WPB;  // k-steps served: 64 (k <= 4096)
+  __shared__ __attribute__((aligned(16))) int8_t qs[KT * kFragBytes];  // reused for the wave sums
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int wib = wave % WPB;
+  const int nb_raw = blockIdx.x * 2 + wave / WPB;
+  const int nb = min(nb_raw, nblocks - 1);
+  const int kc = kp / kKStep;
+  const int col = nb * 16 + (lane & 15);
+  const int32_t cc = corr[col];
+  const float sc = sw[col];
+  float sv[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) sv[r] = EPI == HB_W8A8_EPI_RAW ? 0.0f : scales[min((lane >> 4) * 4 + r, m - 1)];
+  // 1. A tiles: wave w loads k-steps w, w+16, w+32, w+48 (past kc: zeros)
+  const __amdgpu_buffer_rsrc_t rq =
+      __builtin_amdgcn_make_buffer_rsrc((void *)q, 0, (uint32_t)kc * kFragBytes, 0x00020000);
+  hb_u32x4 av[KT / WAVES];
+#pragma unroll
+  for (int j = 0; j < KT / WAVES; ++j)
+    av[j] = __builtin_amdgcn_raw_buffer_load_b128(rq, (uint32_t)(wave + WAVES * j) * kFragBytes + lane * 16u, 0, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  // 2. this wave's weight tiles (reads past the image return zeros; tiles
+  //    past kc are fetched, never multiplied)
+  const __amdgpu_buffer_rsrc_t rw =
+      __builtin_amdgcn_make_buffer_rsrc((void *)wpack, 0, (uint32_t)nblocks * (uint32_t)kc * kFragBytes, 0x00020000);
+  const uint32_t wv = ((uint32_t)nb * (uint32_t)kc + (uint32_t)(wib * VW)) * kFragBytes + (uint32_t)lane * 16u;
+  hb_i32x4 b[VW];
+#pragma unroll
+  for (int i = 0; i < VW; ++i) {
+    const hb_u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(rw, wv + i * kFragBytes, 0, 2);
+    b[i] = hb_i32x4{(int)t[0], (int)t[1], (int)t[2], (int)t[3]};
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int j = 0; j < KT / WAVES; ++j) *(hb_u32x4 *)(qs + (wave + WAVES * j) * kFragBytes + lane * 16) = av[j];
+  __syncthreads();
+  // 3. MFMA: lane l carries A row l % 16 (zero past m)
+  const bool has_row = (lane & 15) < m;
+  hb_i32x4 acc = {0, 0, 0, 0};
+#pragma unroll
+  for (int i = 0; i < VW; ++i) {
+    const int kt = wib * VW + i;
+    if (kt < kc) {
+      const hb_i32x4 a = has_row ? *(const hb_i32x4 *)(qs + kt * kFragBytes + lane * 16) : hb_i32x4{0, 0, 0, 0};
+      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b[i], acc, 0, 0, 0);
+    }
+  }
+  __syncthreads();  // every wave is done reading qs
+  hb_i32x4 *part = (hb_i32x4 *)qs;  // [WAVES][64]
+  part[wave * 64 + lane] = acc;
+  __syncthreads();
+  if (wib != 0 || nb_raw >= nblocks) return;
+  hb_i32x4 total = part[wave * 64 + lane];
+#pragma unroll
+  for (int w = 1; w < WPB; ++w) {
+    const hb_i32x4 p = part[(wave + w) * 64 + lane];
+    total = hb_i32x4{(int)((uint32_t)total[0] + (uint32_t)p[0]), (int)((uint32_t)total[1] + (uint32_t)p[1]),
+                     (int)((uint32_t)total[2] + (uint32_t)p[2]), (int)((uint32_t)total[3] + (uint32_t)p[3])};
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int row = (lane >> 4) * 4 + r;
+    if (row < m) store_result<EPI>(y, ldy, row, col, total[r], cc, sc, sv[r]);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Single-row decode balanced over the CUs (m == 1, k <= 2048).  Workgroup g
 // owns the 8-column half blocks [g*H, g*H + H) with H <= 7, which touch at
 // most four 16-column blocks; with one workgroup per CU every CU streams the
@@ -1057,7 +1138,13 @@ int launch_decode(void *y, int ldy, const int8_t *q, const float *scales, const 
   // Size the workgroup so every wave is resident in a single round
   // (about 16 waves per CU) with 8 one-kilobyte loads in flight each.
   const int nblocks = n / 16;
-  if (nblocks >= 512) {
+  // k <= 4096 with at least 3.5 column blocks per CU: two blocks per 16-wave
+  // workgroup (16 x 4096 x 14336: 17.6 -> 15.1 us for the op).  With fewer
+  // blocks its workgroups leave CUs idle (16 x 4096 x 4096: 7.7 -> 9.0 us).
+  if (kp <= 64 * kKStep && 2 * nblocks >= 7 * compute_units()) {
+    hipLaunchKernelGGL((w8a8_decode_q<EPI>), dim3((nblocks + 1) / 2), dim3(1024), 0, st, y, ldy, q, scales, wpack,
+                       sw, corr, m, kp, nblocks);
+  } else if (nblocks >= 512) {
     hipLaunchKernelGGL((w8a8_gemm_decode<4, 8, EPI>), dim3(nblocks), dim3(256), 0, st, y, ldy, q, scales, wpack, sw,
                        corr, m, n, kp);
   } else if (nblocks >= 128) {

@@ -94,6 +94,8 @@ GEMM_SHAPES = [
     (4, 4096, 512),    # decode
     (16, 1024, 2048),  # decode, full 16 rows
     (16, 14336, 256),  # decode, K beyond the reference envelope
+    (16, 4096, 14336),  # few rows, two column blocks per 16-wave workgroup (w8a8_decode_q)
+    (3, 1504, 14336),  # w8a8_decode_q, three rows, K % 64 == 32
     (1, 96, 64),       # decode, K % 64 == 32
     (300, 1536, 768),  # tiled kernels (automatic shape choice from here on)
     (2048, 128, 2048),
