@@ -444,15 +444,27 @@ __global__ __launch_bounds__(64 * WAVES) void w8a8_gemm_decode(void *__restrict_
                                                                const int8_t *__restrict__ wpack,
                                                                const float *__restrict__ sw,
                                                                const int32_t *__restrict__ corr, int m, int n,
-                                                               int kp) {
+                                                               int kp, int rtiles) {
   __shared__ hb_i32x4 part[WAVES][64];
-  const int nb = blockIdx.x;
+  // blockIdx.x -> (column block, 16-row tile).  With several row tiles, the
+  // tiles of one column block go to one XCD (workgroups are handed to the 8
+  // XCDs in turn) one after another, so they share that XCD's L2 copy of the
+  // block's weights; the grid covers the column blocks rounded up to 8.
+  int nb = blockIdx.x, rtile = 0;
+  if (rtiles > 1) {
+    const int slot = blockIdx.x / 8;
+    nb = (slot / rtiles) * 8 + blockIdx.x % 8;
+    rtile = slot % rtiles;
+    if (nb >= n / 16) return;
+  }
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int kt_count = kp / kKStep;
   const int8_t *wb = wpack + (size_t)nb * kt_count * kFragBytes + lane * 16;
+  const int row0 = rtile * 16;
   const int arow = lane & 15;
-  const bool has_row = arow < m;
-  const int8_t *qa = q + lane * 16;  // tiled A: block row 0, lane-ordered 1 KB per k-step
+  const bool has_row = row0 + arow < m;
+  // tiled A: row tile rtile, lane-ordered 1 KB per k-step
+  const int8_t *qa = q + (size_t)rtile * kt_count * kFragBytes + lane * 16;
   // Epilogue parameters are requested before the weight stream so their
   // latency is hidden behind it.
   const int col = nb * 16 + (lane & 15);
@@ -461,7 +473,7 @@ __global__ __launch_bounds__(64 * WAVES) void w8a8_gemm_decode(void *__restrict_
   float sv[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r)
-    sv[r] = EPI == HB_W8A8_EPI_RAW ? 0.0f : scales[min((lane >> 4) * 4 + r, m - 1)];
+    sv[r] = EPI == HB_W8A8_EPI_RAW ? 0.0f : scales[min(row0 + (lane >> 4) * 4 + r, m - 1)];
 
   hb_i32x4 acc = {0, 0, 0, 0};
   for (int kt0 = wave * U; kt0 < kt_count; kt0 += WAVES * U) {
@@ -488,7 +500,7 @@ __global__ __launch_bounds__(64 * WAVES) void w8a8_gemm_decode(void *__restrict_
   }
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const int row = (lane >> 4) * 4 + r;
+    const int row = row0 + (lane >> 4) * 4 + r;
     if (row < m) store_result<EPI>(y, ldy, row, col, total[r], cc, sc, sv[r]);
   }
 }
@@ -1146,13 +1158,13 @@ int launch_decode(void *y, int ldy, const int8_t *q, const float *scales, const 
                        sw, corr, m, kp, nblocks);
   } else if (nblocks >= 512) {
     hipLaunchKernelGGL((w8a8_gemm_decode<4, 8, EPI>), dim3(nblocks), dim3(256), 0, st, y, ldy, q, scales, wpack, sw,
-                       corr, m, n, kp);
+                       corr, m, n, kp, 1);
   } else if (nblocks >= 128) {
     hipLaunchKernelGGL((w8a8_gemm_decode<16, 8, EPI>), dim3(nblocks), dim3(1024), 0, st, y, ldy, q, scales, wpack,
-                       sw, corr, m, n, kp);
+                       sw, corr, m, n, kp, 1);
   } else {
     hipLaunchKernelGGL((w8a8_gemm_decode<16, 4, EPI>), dim3(nblocks), dim3(1024), 0, st, y, ldy, q, scales, wpack,
-                       sw, corr, m, n, kp);
+                       sw, corr, m, n, kp, 1);
   }
   return hb_check_launch("w8a8_gemm_decode");
 }
@@ -1161,6 +1173,20 @@ template <int EPI>
 int launch_gemm(void *y, int ldy, const int8_t *q, const float *scales, const int8_t *wpack, const float *sw,
                 const int32_t *corr, int m, int n, int kp, hipStream_t st) {
   if (m <= 16) return launch_decode<EPI>(y, ldy, q, scales, wpack, sw, corr, m, n, kp, st);
+  // 17-80 rows whose output holds at most one 64x64 tile per four CUs: the
+  // decode kernel per 16-row tile and 16-column block spreads the weight
+  // stream over the whole chip (op time 64 x 14336 x 4096: 53.6 -> 38.2 us;
+  // 32 x 4096 x 4096: 15.6 -> 9.1; 77 x 4096 x 2048: 20.4 -> 15.2).  With
+  // more row tiles the weight re-reads cost more than the tiles gain
+  // (128 x 4096 x 4096: 20.6 -> 24.9 us), as with more output tiles
+  // (100 x 1536 x 6144: 11.1 -> 19.4 us).
+  const int rtiles = (m + 15) / 16;
+  if (rtiles <= 5 && 4LL * ((m + 63) / 64) * (n / 64) <= compute_units()) {
+    const int nb8 = (n / 16 + 7) / 8 * 8;
+    hipLaunchKernelGGL((w8a8_gemm_decode<16, 8, EPI>), dim3(nb8 * rtiles), dim3(1024), 0, st, y, ldy, q, scales,
+                       wpack, sw, corr, m, n, kp, rtiles);
+    return hb_check_launch("w8a8_gemm_decode");
+  }
   return launch_tiles<EPI>(y, ldy, q, scales, wpack, sw, corr, m, n, kp, st);
 }
 

@@ -97,6 +97,8 @@ GEMM_SHAPES = [
     (16, 4096, 14336),  # few rows, two column blocks per 16-wave workgroup (w8a8_decode_q)
     (3, 1504, 14336),  # w8a8_decode_q, three rows, K % 64 == 32
     (1, 96, 64),       # decode, K % 64 == 32
+    (64, 14336, 4096),  # 17-128 rows, few output tiles: decode kernel per 16-row tile
+    (72, 1056, 2048),  # the same, partial last row tile, K % 64 == 32
     (300, 1536, 768),  # tiled kernels (automatic shape choice from here on)
     (2048, 128, 2048),
     (4096, 64, 4096),
