@@ -48,6 +48,13 @@ HEADLINE = (4096, 1536, 6144)
 SETTLE_MS = 80.0          # untimed GPU time before each timed sequence (clock ramp)
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "w8a8_gemm_tiles_4096x1536x6144_traffic.md")
 COPY_PROBE_BYTES = 256 << 20
+CHUNKS = 20               # timed steps are split into this many event-bracketed chunks (median reported)
+USE_GRAPHS = True         # --no-graph: no graph capture or replay anywhere (for traced runs)
+
+
+def progress(msg):
+    """One progress line on stderr per finished case, so a failing run names its case."""
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
 def w8a8_bytes(m, k, n):
@@ -127,14 +134,20 @@ def run_w8a8(m, k, n, steps, warmup, rotate, outliers=0.0, scale=(1e-4, 1e-3), s
         hip.sync()
 
     def timed_stream(fn, count):
-        a, b = hip.Event(), hip.Event()
+        """Total ms of `count` stream-ordered launches, and the median over
+        CHUNKS event-bracketed chunks of the per-launch ms."""
+        chunks = max(1, min(CHUNKS, count))
+        bounds = [count * c // chunks for c in range(chunks + 1)]
+        events = [hip.Event() for _ in range(chunks + 1)]
         synced()
-        a.record(stream)
-        for i in range(count):
-            fn(sets[i % rotate])
-        b.record(stream)
+        events[0].record(stream)
+        for c in range(chunks):
+            for i in range(bounds[c], bounds[c + 1]):
+                fn(sets[i % rotate])
+            events[c + 1].record(stream)
         synced()
-        return a.elapsed_ms(b)
+        per = [events[c].elapsed_ms(events[c + 1]) / max(1, bounds[c + 1] - bounds[c]) for c in range(chunks)]
+        return events[0].elapsed_ms(events[-1]), statistics.median(per)
 
     def timed_graph(graph):
         a, b = hip.Event(), hip.Event()
@@ -165,18 +178,21 @@ def run_w8a8(m, k, n, steps, warmup, rotate, outliers=0.0, scale=(1e-4, 1e-3), s
     synced()
     settle(warmup)
     wall0 = time.perf_counter()
-    total_ms = timed_stream(step, steps)
+    total_ms, step_median = timed_stream(step, steps)
     wall = time.perf_counter() - wall0
-    gemm_ms = timed_stream(gemm, steps) / steps
-    quant_ms = timed_stream(quant, steps) / steps
-    graphs = {name: capture(fn, steps) for name, fn in (("step", step), ("gemm", gemm), ("quant", quant))}
-    graph_ms = {}
-    for name, g in graphs.items():
-        settle(0)
-        graph_ms[name] = timed_graph(g) / steps
-    return {"ms_per_step": total_ms / steps, "wall_ms_per_step": wall * 1e3 / steps, "gemm_ms_mean": gemm_ms,
-            "quant_ms_mean": quant_ms, "graph_ms_per_step": graph_ms["step"], "graph_gemm_ms_mean": graph_ms["gemm"],
-            "graph_quant_ms_mean": graph_ms["quant"], "sets": sets}
+    gemm_total, gemm_median = timed_stream(gemm, steps)
+    quant_total, quant_median = timed_stream(quant, steps)
+    graph_ms = {"step": None, "gemm": None, "quant": None}
+    if USE_GRAPHS:
+        for name, fn in (("step", step), ("gemm", gemm), ("quant", quant)):
+            g = capture(fn, steps)
+            settle(0)
+            graph_ms[name] = timed_graph(g) / steps
+            g.destroy()
+    return {"ms_per_step": total_ms / steps, "ms_per_step_median": step_median, "wall_ms_per_step": wall * 1e3 / steps,
+            "gemm_ms_mean": gemm_total / steps, "gemm_ms_median": gemm_median, "quant_ms_mean": quant_total / steps,
+            "quant_ms_median": quant_median, "graph_ms_per_step": graph_ms["step"],
+            "graph_gemm_ms_mean": graph_ms["gemm"], "graph_quant_ms_mean": graph_ms["quant"], "sets": sets}
 
 
 def cpu_model():
@@ -283,7 +299,8 @@ def decode_case(m, k, n, steps, warmup, rotate):
             "gemm_us": round(r["gemm_ms_mean"] * 1e3, 3),
             "gemm_gbps": round(gemm_bytes(m, k, n) / (r["gemm_ms_mean"] * 1e-3) / 1e9, 1),
             "quant_us": round(r["quant_ms_mean"] * 1e3, 3), "rotated_sets": rotate,
-            "graph_us_per_call": round(r["graph_ms_per_step"] * 1e3, 3)}
+            "us_per_call_median": round(r["ms_per_step_median"] * 1e3, 3),
+            "graph_us_per_call": None if r["graph_ms_per_step"] is None else round(r["graph_ms_per_step"] * 1e3, 3)}
 
 
 def all_configs(steps, warmup, with_cpu=False):
@@ -295,23 +312,33 @@ def all_configs(steps, warmup, with_cpu=False):
             "C3_down_4096x6144x1536": (4096, 6144, 1536, 0.01, (1e-4, 1e-3)),
             "C4_qkv_2048x4096x6144": (2048, 4096, 6144, 0.0, (5e-5, 5e-4)),
             "C4_o_2048x4096x4096": (2048, 4096, 4096, 0.0, (5e-5, 5e-4))}.items():
+        progress(f"start {name}")
         r = run_w8a8(m, k, n, steps, warmup, 4, outliers=outl, scale=sc,
                      epilogue=hip.EPI_SCALE_GELU if "gelu" in name else None)
-        out[name] = {"us": round(r["ms_per_step"] * 1e3, 2),
+        out[name] = {"us": round(r["ms_per_step"] * 1e3, 2), "us_median": round(r["ms_per_step_median"] * 1e3, 2),
                      "tops": round(2 * m * n * k / (r["ms_per_step"] * 1e-3) / 1e12, 1),
                      "gemm_us": round(r["gemm_ms_mean"] * 1e3, 2)}
+        del r
+        progress(f"done {name}: {out[name]['us']} us")
     for m in (1, 4, 16):
         for k, n in ((4096, 14336), (14336, 4096)):
+            progress(f"start C5 M={m} {k}x{n}")
             out[f"C5_M{m}_{k}x{n}"] = decode_case(m, k, n, steps, warmup, 6)
+            progress(f"done C5 M={m} {k}x{n}: {out[f'C5_M{m}_{k}x{n}']['us_per_call']} us")
+    progress("start C2")
     out["C2_f16_text_mlp_77x768x3072x768"] = f16_mlp_case(steps, warmup)
+    progress("start opcode 19")
     out["opcode19_aux"] = aux_cases(steps, warmup, with_cpu=with_cpu)
+    progress("start opcodes 2/3/4")
     out["opcodes_2_3_4_qk0"] = qk0_cases(steps, warmup)
+    progress("done all configs")
     return out
 
 
 def _timed_graph_us(launch, steps, warmup, stream):
     """Settles the clock with stream-ordered launches, then the mean of one
-    graph replay of `steps` launches (µs per launch)."""
+    graph replay of `steps` launches (µs per launch); with --no-graph, the
+    mean of `steps` stream-ordered launches instead."""
     lib = hip.lib()
     done, gpu_ms = 0, 0.0
     while done < max(warmup, 1) or gpu_ms < SETTLE_MS:
@@ -322,15 +349,23 @@ def _timed_graph_us(launch, steps, warmup, stream):
         b.record(stream)
         hip.check(lib.hb_stream_sync(stream), "sync")
         done, gpu_ms = done + 50, gpu_ms + a.elapsed_ms(b)
+    a, b = hip.Event(), hip.Event()
+    if not USE_GRAPHS:
+        a.record(stream)
+        for i in range(steps):
+            launch(i)
+        b.record(stream)
+        hip.check(lib.hb_stream_sync(stream), "sync")
+        return a.elapsed_ms(b) * 1e3 / steps
     with hip.Graph.capture(stream) as g:
         for i in range(steps):
             launch(i)
-    a, b = hip.Event(), hip.Event()
     hip.check(lib.hb_stream_sync(stream), "sync")
     a.record(stream)
     g.launch(stream)
     b.record(stream)
     hip.check(lib.hb_stream_sync(stream), "sync")
+    g.destroy()
     return a.elapsed_ms(b) * 1e3 / steps
 
 
@@ -542,16 +577,7 @@ def f16_mlp_case(steps, warmup, m=77, k=768, n=3072, rotate=6):
             b.record(stream)
             hip.check(lib.hb_stream_sync(stream), "sync")
             done, gpu_ms = done + 200, gpu_ms + a.elapsed_ms(b)
-        with hip.Graph.capture(stream) as g:
-            for i in range(steps):
-                launch(i)
-        a, b = hip.Event(), hip.Event()
-        hip.check(lib.hb_stream_sync(stream), "sync")
-        a.record(stream)
-        g.launch(stream)
-        b.record(stream)
-        hip.check(lib.hb_stream_sync(stream), "sync")
-        us = a.elapsed_ms(b) * 1e3 / steps
+        us = _timed_graph_us(launch, steps, 0, stream)
         nbytes = 4 * m * kk + 2 * nn * kk + 4 * nn + 4 * m * nn
         out["layer1_quickgelu" if li == 0 else "layer2_bias"] = {
             "shape": f"M={m} K={kk} N={nn} mode={mode}", "us": round(us, 3),
@@ -627,6 +653,8 @@ def main():
                     help="small / aux / qk0: only the C1 W8A8 and C2 F16 text-MLP cases / the opcode-19 cases / "
                          "the opcode-2/3/4 cases (profiling aids; print those cases alone)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="no HIP graph capture or replay (every timing stream-ordered); for profiler-traced runs")
     ap.add_argument("--traffic-probe", action="store_true")
     ap.add_argument("--profile-summary", metavar="DIR")
     args = ap.parse_args()
@@ -638,6 +666,8 @@ def main():
               "multi-GPU sharding is design-only). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     rank = int(os.environ.get("RANK", "0"))
+    global USE_GRAPHS
+    USE_GRAPHS = not args.no_graph
     if args.traffic_probe:
         traffic_probe()
         return
@@ -678,17 +708,24 @@ def main():
         "mfma_frac_full_op": round(tops / PEAK_INT8_TOPS, 4),
         "hbm_gbps_full_op": round(w8a8_bytes(m, k, n) / (r["ms_per_step"] * 1e-3) / 1e9, 1),
         "quant_us": round(r["quant_ms_mean"] * 1e3, 3),
-        "timing": "stream-ordered launches between HIP events; graph replay of the same steps: "
-                  f"{r['graph_ms_per_step'] * 1e3:.3f} us/step, GEMM {r['graph_gemm_ms_mean'] * 1e3:.3f} us",
+        "us_per_step_median": round(r["ms_per_step_median"] * 1e3, 3),
+        "timing": f"{args.steps} stream-ordered launches between HIP events on the library stream (value: their "
+                  f"mean; median over {CHUNKS} event-bracketed chunks beside it)" +
+                  ("" if r["graph_ms_per_step"] is None else
+                   f"; graph replay of the same steps: {r['graph_ms_per_step'] * 1e3:.3f} us/step, "
+                   f"GEMM {r['graph_gemm_ms_mean'] * 1e3:.3f} us"),
         "roofline": {"kernel": "w8a8_gemm_tiles", "bound": "mfma", "achieved": round(gemm_tops, 2),
-                     "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s", "frac": round(gemm_tops / PEAK_INT8_TOPS, 4),
+                     "peak": PEAK_INT8_TOPS, "unit": "TOPS", "frac": round(gemm_tops / PEAK_INT8_TOPS, 4),
                      "traffic": read_traffic(), "gemm_us": round(r["gemm_ms_mean"] * 1e3, 3),
                      "gemm_gbps": round(gemm_bytes(m, k, n) / (r["gemm_ms_mean"] * 1e-3) / 1e9, 1),
                      "algorithmic_ops_per_launch": ops,
                      "algorithmic_bytes_per_launch": gemm_bytes(m, k, n)},
     }
+    line["roofline"]["gemm_us_median"] = round(r["gemm_ms_median"] * 1e3, 3)
     del r
+    progress(f"headline {line['ms_per_step'] * 1e3:.2f} us/step")
     line["decode_m1"] = decode_case(1, 4096, 14336, args.steps, args.warmup, 6)
+    progress(f"decode M=1 {line['decode_m1']['us_per_call']} us")
     line["e2e_opcode15"] = e2e_opcode15(m, k, n)
     if args.config == "all":
         line["configs"] = all_configs(args.steps, args.warmup, with_cpu=not args.no_cpu)

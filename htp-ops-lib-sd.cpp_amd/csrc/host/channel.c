@@ -11,7 +11,8 @@
  *   - RPCMEM_MAP V1 releases n_puts fds; V2 checks the session token, then
  *     releases n_puts and resolves n_gets views (any failure -> -1);
  *   - completion stores v[0] | 1 << 8 into the state word with release
- *     semantics, after every output is host-visible.
+ *     semantics, after every output is host-visible; requests on HBM
+ *     tensors are synchronised once per message, not once each.
  */
 #include <pthread.h>
 #include <sched.h>
@@ -40,6 +41,12 @@ static void process_map(struct RequestHeader *r, size_t data_size, uint64_t toke
     return;
   }
   int32_t state = 0;
+  /* a put frees device mirrors and cached weight images that queued work of
+   * earlier requests in this message may still read */
+  if (htp_executor_flush() != 0) {
+    set_state(r, -1);
+    return;
+  }
   const struct RpcmemMapRequestV2 *v2 = (const struct RpcmemMapRequestV2 *)r->data;
   const int is_v2 = data_size >= sizeof(struct RpcmemMapRequestV2) && v2->magic == RPCMEM_MAP_REQUEST_SESSION_MAGIC &&
                     v2->version == RPCMEM_MAP_REQUEST_VERSION_SESSION;
@@ -82,6 +89,7 @@ static void process_map(struct RequestHeader *r, size_t data_size, uint64_t toke
 void htp_channel_process(htp_backend *backend, struct MessageHeader *msg, size_t capacity, uint64_t token) {
   size_t used = 0;
   if (!message_header_validate_layout(msg, capacity, &used)) return;
+  htp_executor_message_begin();
   for (int32_t i = 0; i < msg->n_reqs; ++i) {
     const size_t wire = (size_t)msg->req_offsets[i + 1] - (size_t)msg->req_offsets[i];
     const size_t data_size = wire - sizeof(struct RequestHeader);
@@ -93,13 +101,16 @@ void htp_channel_process(htp_backend *backend, struct MessageHeader *msg, size_t
         if (backend && !htp_backend_compute_allowed(backend)) {
           set_state(r, AEE_EBADSTATE);
         } else {
-          set_state(r, execute_op_simple((struct OpComputeRequest *)r->data, data_size));
+          set_state(r, htp_executor_message_request((struct OpComputeRequest *)r->data, data_size, &r->state));
         }
         break;
       case REQUEST_TYPE_RPCMEM_MAP: process_map(r, data_size, token); break;
       default: break;
     }
   }
+  /* one synchronisation for the message: every output is host-visible
+   * before the caller sees the completion flag */
+  (void)htp_executor_message_end();
 }
 
 static void backoff(unsigned *idle) {

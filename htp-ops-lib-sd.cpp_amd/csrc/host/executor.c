@@ -51,6 +51,8 @@ void *htp_executor_scratch(int slot, size_t bytes) {
   if (slot < 0 || slot >= kScratchSlots) return NULL;
   if (bytes == 0) bytes = 256;
   if (g_scratch_size[slot] < bytes) {
+    /* queued (deferred) work may still use the old buffer */
+    if (g_scratch[slot] && hb_stream_sync(htp_executor_stream()) != HB_OK) return NULL;
     if (g_scratch[slot]) hb_free(g_scratch[slot]);
     g_scratch[slot] = NULL;
     g_scratch_size[slot] = 0;
@@ -73,19 +75,49 @@ static int checked_mul(size_t a, size_t b, size_t *out) {
   return 1;
 }
 
-/* Content signature of a host-resident weight: FNV-1a of the first 128 bytes
- * plus 64 evenly spaced 64-byte samples.  HBM-resident weights change only
- * through this library, which bumps the fd generation instead. */
-static uint64_t weight_signature(const htp_view *v) {
+static inline uint64_t rotl64(uint64_t v, int r) { return (v << r) | (v >> (64 - r)); }
+
+/* Hash of every byte of a host buffer: four independent 64-bit
+ * multiply-rotate lanes over 32-byte blocks, then the tail bytes (about
+ * 10 GB/s on one core, so a 9.4 MB weight costs about 1 ms). */
+static uint64_t content_hash(const uint8_t *p, size_t n) {
+  const uint64_t k1 = 0x9e3779b97f4a7c15ull, k2 = 0xc2b2ae3d27d4eb4full;
+  uint64_t lane[4] = {k1, k2, k1 ^ 0x5555555555555555ull, k2 ^ 0xaaaaaaaaaaaaaaaaull};
+  size_t i = 0;
+  for (; i + 32 <= n; i += 32) {
+    uint64_t w[4];
+    memcpy(w, p + i, sizeof(w));
+    for (int j = 0; j < 4; ++j) lane[j] = rotl64(lane[j] ^ (w[j] * k2), 29) * k1;
+  }
+  uint64_t h = (uint64_t)n * k2;
+  for (int j = 0; j < 4; ++j) h = rotl64(h ^ lane[j], 31) * k1;
+  for (; i < n; ++i) h = (h ^ p[i]) * 1099511628211ull;
+  return h ^ (h >> 32);
+}
+
+/* Signature of a host-resident weight's contents.  The reference reads the
+ * constants from DDR on every call (reference src/dsp/ops/linear_w8a8.c:242-268),
+ * so a caller may rewrite them in place between calls without a map "put";
+ * by default every byte is hashed, so any rewrite rebuilds the prepacked
+ * image.  HTP_OPS_AMD_WEIGHT_CACHE=sampled is for callers that always
+ * "put" (or call htp_ops_amd_invalidate_weights) after writing: it hashes
+ * the first 128 bytes (the W8A8 header), the last `tail` bytes in full (the
+ * W8A8 scale, sum and smoothing sections) and 64 spaced 64-byte samples of
+ * the rest.  HBM-resident weights change only through this library, which
+ * bumps the fd generation instead. */
+static uint64_t weight_signature(const htp_view *v, size_t tail) {
   if (v->is_device || !v->host) return 0;
-  uint64_t h = htp_fnv1a64(v->host, v->bytes < 128 ? v->bytes : 128);
-  if (v->bytes > 128) {
-    const size_t span = v->bytes - 128;
-    for (int i = 0; i < 64; ++i) {
-      const size_t off = 128 + span / 64 * (size_t)i;
-      const size_t len = v->bytes - off < 64 ? v->bytes - off : 64;
-      h ^= htp_fnv1a64(v->host + off, len) + 0x9e3779b97f4a7c15ull * (uint64_t)(i + 1);
-    }
+  static int sampled = -1;
+  if (sampled < 0) {
+    const char *e = getenv("HTP_OPS_AMD_WEIGHT_CACHE");
+    sampled = e && strcmp(e, "sampled") == 0;
+  }
+  if (!sampled || v->bytes <= 128 + tail + 64 * 64) return content_hash(v->host, v->bytes);
+  uint64_t h = content_hash(v->host, 128) ^ rotl64(content_hash(v->host + v->bytes - tail, tail), 17);
+  const size_t span = v->bytes - 128 - tail;
+  for (int i = 0; i < 64; ++i) {
+    const size_t off = 128 + span / 64 * (size_t)i;
+    h ^= rotl64(content_hash(v->host + off, 64), i) + 0x9e3779b97f4a7c15ull * (uint64_t)(i + 1);
   }
   return h;
 }
@@ -129,29 +161,138 @@ typedef struct {
   int n;
 } event_set;
 
-/* Timing events are created once and reused: every op runs under
- * g_exec_lock, so one set serves all of them (creating and destroying
- * events cost several microseconds per call). */
-static hb_event g_event_pool[5];
-static int g_event_pool_n = 0;
+/* Timing events are created once and reused (creating and destroying
+ * events costs several microseconds per call).  Every op runs under
+ * g_exec_lock; an op takes its events from the pool at g_event_next and
+ * hands them back when it completes, or leaves them taken while its
+ * completion is deferred (below). */
+static hb_event *g_event_pool;
+static int g_event_pool_n = 0, g_event_next = 0;
 
 static int events_open(event_set *ev, int count) {
   ev->n = 0;
-  while (g_event_pool_n < count) {
-    if (hb_event_create(&g_event_pool[g_event_pool_n]) != HB_OK) return -5;
-    ++g_event_pool_n;
+  if (g_event_next + count > g_event_pool_n) {
+    const int want = g_event_next + count;
+    hb_event *grown = (hb_event *)realloc(g_event_pool, (size_t)want * sizeof(hb_event));
+    if (!grown) return -5;
+    g_event_pool = grown;
+    while (g_event_pool_n < want) {
+      if (hb_event_create(&g_event_pool[g_event_pool_n]) != HB_OK) return -5;
+      ++g_event_pool_n;
+    }
   }
-  for (int i = 0; i < count; ++i) ev->e[i] = g_event_pool[i];
+  for (int i = 0; i < count; ++i) ev->e[i] = g_event_pool[g_event_next + i];
+  g_event_next += count;
   ev->n = count;
   return 0;
 }
 
-static void events_close(event_set *ev) { ev->n = 0; }
+static void events_close(event_set *ev) {
+  g_event_next -= ev->n;
+  ev->n = 0;
+}
 
 static double event_ms(const event_set *ev, int a, int b) {
   float ms = 0.0f;
   if (hb_event_elapsed_ms(&ms, ev->e[a], ev->e[b]) != HB_OK) return 0.0;
   return (double)ms;
+}
+
+/* ---- deferred completion inside a mailbox message ----------------------------
+ * The reference publishes a message's completion once, after flushing every
+ * request's outputs (reference src/dsp/commu.c:250-263).  Inside a message,
+ * a request whose tensors all live in HBM therefore does not wait for the
+ * GPU: its return code is final once its work is queued (every argument
+ * check runs before that), and its elapsed_us field is written when the
+ * message is flushed, after one stream synchronisation.  A request with a
+ * host-resident output (copied back to the host), a profile trailer or the
+ * CPU-control planes still completes before it returns. */
+enum { kMaxDeferred = 64 };
+typedef struct {
+  uint8_t *elapsed_dst; /* int32 elapsed_us field in the payload, or NULL */
+  void *state;          /* the request's int32 return code, for a failed flush */
+  event_set ev;
+  int first, last;      /* events bracketing the timed GPU work */
+  double extra_us;      /* host-side time added to elapsed_us (a prepack) */
+} deferred_op;
+
+static int g_in_message = 0;
+static void *g_request_state = NULL;
+static deferred_op g_deferred[kMaxDeferred];
+static int g_deferred_n = 0;
+
+static int flush_deferred_locked(void) {
+  if (g_deferred_n == 0) return 0;
+  const int rc = hb_stream_sync(htp_executor_stream());
+  for (int i = 0; i < g_deferred_n; ++i) {
+    deferred_op *d = &g_deferred[i];
+    if (rc != HB_OK) {
+      if (d->state) {
+        const int32_t code = -5;
+        memcpy(d->state, &code, sizeof(code));
+      }
+    } else if (d->elapsed_dst) {
+      const int32_t us = (int32_t)(event_ms(&d->ev, d->first, d->last) * 1e3 + d->extra_us);
+      memcpy(d->elapsed_dst, &us, sizeof(us));
+    }
+  }
+  g_deferred_n = 0;
+  g_event_next = 0;
+  return rc == HB_OK ? 0 : -5;
+}
+
+/* Completes the queued work of one request: defers it when the message
+ * allows, else synchronises, writes elapsed_us and hands the events back. */
+static int complete(event_set *ev, int first, int last, uint8_t *elapsed_dst, double extra_us, int deferrable) {
+  if (g_in_message && deferrable && g_deferred_n < kMaxDeferred) {
+    deferred_op *d = &g_deferred[g_deferred_n++];
+    d->elapsed_dst = elapsed_dst;
+    d->state = g_request_state;
+    d->ev = *ev;
+    d->first = first;
+    d->last = last;
+    d->extra_us = extra_us;
+    return 0; /* the events stay taken until the flush */
+  }
+  const int rc = hb_stream_sync(htp_executor_stream());
+  if (rc == HB_OK && elapsed_dst) {
+    const int32_t us = (int32_t)(event_ms(ev, first, last) * 1e3 + extra_us);
+    memcpy(elapsed_dst, &us, sizeof(us));
+  }
+  events_close(ev);
+  return rc == HB_OK ? 0 : -5;
+}
+
+void htp_executor_message_begin(void) {
+  pthread_mutex_lock(&g_exec_lock);
+  g_in_message = 1;
+  pthread_mutex_unlock(&g_exec_lock);
+}
+
+int htp_executor_message_request(struct OpComputeRequest *req, size_t req_size, void *state) {
+  pthread_mutex_lock(&g_exec_lock);
+  g_request_state = state;
+  pthread_mutex_unlock(&g_exec_lock);
+  const int rc = execute_op_simple(req, req_size);
+  pthread_mutex_lock(&g_exec_lock);
+  g_request_state = NULL;
+  pthread_mutex_unlock(&g_exec_lock);
+  return rc;
+}
+
+int htp_executor_flush(void) {
+  pthread_mutex_lock(&g_exec_lock);
+  const int rc = flush_deferred_locked();
+  pthread_mutex_unlock(&g_exec_lock);
+  return rc;
+}
+
+int htp_executor_message_end(void) {
+  pthread_mutex_lock(&g_exec_lock);
+  const int rc = flush_deferred_locked();
+  g_in_message = 0;
+  pthread_mutex_unlock(&g_exec_lock);
+  return rc;
 }
 
 /* ---- opcode 15 --------------------------------------------------------------- */
@@ -186,7 +327,7 @@ static int exec_w8a8(uint8_t *payload, size_t payload_size) {
    * built and has not been written since (the cache key holds the buffer's
    * write generation), so only a miss reads the header back (a blocking
    * copy). */
-  const uint64_t cst_sig = weight_signature(&cst);
+  const uint64_t cst_sig = weight_signature(&cst, (size_t)n * 8u + (size_t)k * 4u);
   if (!(cst.is_device && htp_weight_cache_peek(HTP_WEIGHT_W8A8, &cst, k, n, cst_sig))) {
     struct W8A8Header h;
     if (cst.is_device) {
@@ -243,13 +384,17 @@ static int exec_w8a8(uint8_t *payload, size_t payload_size) {
     return -5;
   }
   int hrc = hb_event_record(ev.e[0], s);
-  /* A single row goes through hb_w8a8_linear, which quantizes inside the
-   * weight-streaming kernel (its time is then reported as GEMM time). */
-  const int fused = !cpu_output && m == 1;
-  if (!hrc && !fused) hrc = hb_w8a8_quantize(q, scales, x, inv, m, k, s);
+  /* A plain request runs through hb_w8a8_linear, which takes the one-launch
+   * kernels that quantize their own rows where the shape allows (m == 1,
+   * 2-4 rows, 5-128 rows with short K) and quantize + GEMM otherwise; all
+   * its time is then reported as GEMM time.  A profiled or CPU-control
+   * request keeps quantization as its own launch so its phases are timed
+   * apart. */
+  const int split = cpu_output || profiled;
+  if (!hrc && split) hrc = hb_w8a8_quantize(q, scales, x, inv, m, k, s);
   if (!hrc) hrc = hb_event_record(ev.e[1], s);
   if (!hrc) {
-    if (fused) hrc = hb_w8a8_linear(y, x, packed, m, k, n, HB_W8A8_EPI_SCALE, ws, ws_bytes, s);
+    if (!split) hrc = hb_w8a8_linear(y, x, packed, m, k, n, HB_W8A8_EPI_SCALE, ws, ws_bytes, s);
     else if (cpu_output) hrc = hb_w8a8_gemm(raw, n, q, scales, packed, m, k, n, HB_W8A8_EPI_RAW, s);
     else hrc = hb_w8a8_gemm(y, n, q, scales, packed, m, k, n, HB_W8A8_EPI_SCALE, s);
   }
@@ -257,14 +402,21 @@ static int exec_w8a8(uint8_t *payload, size_t payload_size) {
   if (!hrc && cpu_output) hrc = hb_w8a8_planes_from_raw((uint8_t *)y, (const int32_t *)raw, m, n, s);
   if (!hrc) hrc = hb_event_record(ev.e[3], s);
   if (!hrc && (void *)y != (void *)out.dev) hrc = hb_memcpy_d2d(out.dev, y, out.bytes, s);
-  if (!hrc) hrc = hb_stream_sync(s);
   if (hrc) {
     events_close(&ev);
     return hrc == HB_E_INVAL ? -10 : -5;
   }
+  const double weight_s = built ? t_w1 - t_w0 : 0.0;
+  if (!split && out.is_device) {
+    htp_registry_touch(out.fd);
+    return complete(&ev, 0, 3, payload + offsetof(struct NativeW8A8Params, elapsed_us), weight_s * 1e6, 1);
+  }
+  if (hb_stream_sync(s) != HB_OK) {
+    events_close(&ev);
+    return -5;
+  }
   const double quant_ms = event_ms(&ev, 0, 1), gemm_ms = event_ms(&ev, 1, 2), out_ms = event_ms(&ev, 2, 3);
   events_close(&ev);
-  const double weight_s = built ? t_w1 - t_w0 : 0.0;
 
   if (cpu_output) {
     /* Publish row scales and one batch covering every row
@@ -332,7 +484,7 @@ static uintptr_t primary_address(const htp_view *v) {
  * multiplied directly (in place when already device-resident and aligned,
  * else from a cached device copy); otherwise through their cached F16 image. */
 static int run_f16(int kind, int qk0_type, htp_view *out, htp_view *act, htp_view *wgt, htp_view *bias, int m, int k,
-                   int n, int channels, int mode, int32_t *elapsed_us) {
+                   int n, int channels, int mode, uint8_t *elapsed_dst) {
   if (htp_executor_ensure_device() != 0) return -5;
   if (materialize(out) || materialize(act) || materialize(wgt) || (bias && materialize(bias))) return -5;
   hb_stream s = htp_executor_stream();
@@ -344,7 +496,7 @@ static int run_f16(int kind, int qk0_type, htp_view *out, htp_view *act, htp_vie
   if (direct && wgt->is_device && ((uintptr_t)wgt->dev & 15u) == 0)
     packed = wgt->dev;
   else
-    rc = htp_weight_cache_get(direct ? HTP_WEIGHT_QK0_RAW : kind, wgt, k, n, weight_signature(wgt), &packed, &built,
+    rc = htp_weight_cache_get(direct ? HTP_WEIGHT_QK0_RAW : kind, wgt, k, n, weight_signature(wgt, 0), &packed, &built,
                               s);
   if (rc) return rc;
   const double t_w1 = now_seconds();
@@ -378,13 +530,14 @@ static int run_f16(int kind, int qk0_type, htp_view *out, htp_view *act, htp_vie
                  : hb_f16_gemm_ws(y, x, (const uint16_t *)packed, b, m, k, n, channels, mode, ws, ws_bytes, s);
   if (!hrc) hrc = hb_event_record(ev.e[1], s);
   if (!hrc && (void *)y != (void *)out->dev) hrc = hb_memcpy_d2d(out->dev, y, out_bytes, s);
-  if (!hrc) hrc = hb_stream_sync(s);
-  const double gemm_ms = hrc ? 0.0 : event_ms(&ev, 0, 1);
-  events_close(&ev);
-  if (hrc) return hrc == HB_E_INVAL ? -11 : -5;
-  if (stage_out(out, s)) return -5;
+  if (hrc) {
+    events_close(&ev);
+    return hrc == HB_E_INVAL ? -11 : -5;
+  }
   htp_registry_touch(out->fd);
-  if (elapsed_us) *elapsed_us = (int32_t)(gemm_ms * 1e3 + (built ? (t_w1 - t_w0) * 1e6 : 0.0));
+  const double extra_us = built ? (t_w1 - t_w0) * 1e6 : 0.0;
+  if (complete(&ev, 0, 1, elapsed_dst, extra_us, out->is_device)) return -5;
+  if (stage_out(out, s)) return -5;
   return 0;
 }
 
@@ -410,15 +563,11 @@ static int exec_f16_epilogue(uint8_t *payload, size_t payload_size) {
   /* Kernel alignment contract: 128-byte aligned dst/activation/weight
    * (reference src/dsp/ops/mat_mul.c:947-949). */
   if ((primary_address(&out) | primary_address(&act) | primary_address(&wgt)) & 127u) return -12;
-  int32_t elapsed = 0;
-  rc = run_f16(HTP_WEIGHT_F16, 0, &out, &act, &wgt, p.bias.fd >= 0 ? &bias : NULL, p.m, p.k, p.n, p.channels,
-               p.mode, &elapsed);
-  if (rc) return rc;
-  memcpy(payload + offsetof(struct F16EpilogueParams, elapsed_us), &elapsed, sizeof(elapsed));
-  return 0;
+  return run_f16(HTP_WEIGHT_F16, 0, &out, &act, &wgt, p.bias.fd >= 0 ? &bias : NULL, p.m, p.k, p.n, p.channels,
+                 p.mode, payload + offsetof(struct F16EpilogueParams, elapsed_us));
 }
 
-static int exec_matmul_params(const struct MatMulParams *p, int32_t *elapsed_us, uint64_t *act_hash,
+static int exec_matmul_params(const struct MatMulParams *p, uint8_t *elapsed_dst, uint64_t *act_hash,
                               uint64_t *out_hash) {
   /* reference src/dsp/op_executor.cc:473-540, src/dsp/ops/mat_mul.c:1046-1049 */
   const int m = p->m, k = p->k, n = p->n;
@@ -435,7 +584,7 @@ static int exec_matmul_params(const struct MatMulParams *p, int32_t *elapsed_us,
     *act_hash = 0;
     if (act.host) *act_hash = htp_fnv1a64(act.host, act.bytes);
   }
-  rc = run_f16(HTP_WEIGHT_F16, 0, &out, &act, &wgt, NULL, m, k, n, n, 0, elapsed_us);
+  rc = run_f16(HTP_WEIGHT_F16, 0, &out, &act, &wgt, NULL, m, k, n, n, 0, elapsed_dst);
   if (rc) return rc;
   if (out_hash) {
     *out_hash = 0;
@@ -448,11 +597,10 @@ static int exec_matmul(uint8_t *payload, size_t payload_size) {
   if (payload_size < sizeof(struct MatMulParams)) return -1;
   struct MatMulParams p;
   memcpy(&p, payload, sizeof(p));
-  int32_t elapsed = 0;
-  const int rc = exec_matmul_params(&p, &elapsed, NULL, NULL);
-  if (rc == 0 && payload_size >= sizeof(struct MatMulProfileParams))
-    memcpy(payload + offsetof(struct MatMulProfileParams, elapsed_us), &elapsed, sizeof(elapsed));
-  return rc;
+  uint8_t *elapsed_dst =
+      payload_size >= sizeof(struct MatMulProfileParams) ? payload + offsetof(struct MatMulProfileParams, elapsed_us)
+                                                         : NULL;
+  return exec_matmul_params(&p, elapsed_dst, NULL, NULL);
 }
 
 /* Opcodes 2/3/4: Q4_0 / Q8_0 / IQ4_NL super-blocks.  m <= 16 multiplies the
@@ -478,15 +626,18 @@ static int exec_matmul_qk0(uint8_t *payload, size_t payload_size, int kind, int 
   if (!rc) rc = resolve(&p.weight, weight_size, &wgt, -1);
   if (rc) return rc;
   if ((primary_address(&out) | primary_address(&act) | primary_address(&wgt)) & 127u) return -1;
-  int32_t elapsed = 0;
-  return run_f16(kind, type, &out, &act, &wgt, NULL, m, k, n, n, 0, &elapsed);
+  /* elapsed_us is not written for these opcodes, as in the reference */
+  return run_f16(kind, type, &out, &act, &wgt, NULL, m, k, n, n, 0, NULL);
 }
 
 /* Direct (non-mailbox) opcode-1 entry used by htp_ops_mat_mul_permuted_w16a32[_trace]. */
 int htp_exec_matmul_w16a32(const struct MatMulParams *p, int32_t *elapsed_us, uint64_t *act_hash,
                            uint64_t *out_hash) {
   pthread_mutex_lock(&g_exec_lock);
-  const int rc = exec_matmul_params(p, elapsed_us, act_hash, out_hash);
+  const int saved = g_in_message; /* a direct call completes before it returns */
+  g_in_message = 0;
+  const int rc = exec_matmul_params(p, (uint8_t *)elapsed_us, act_hash, out_hash);
+  g_in_message = saved;
   pthread_mutex_unlock(&g_exec_lock);
   return rc;
 }
@@ -590,15 +741,13 @@ static int exec_model_aux(uint8_t *payload, size_t payload_size) {
                           p.other_count, p.activation, p.eps, ws, ws_bytes, s);
   if (!hrc) hrc = hb_event_record(ev.e[1], s);
   if (!hrc && (void *)y != (void *)out.dev) hrc = hb_memcpy_d2d(out.dev, y, out.bytes, s);
-  if (!hrc) hrc = hb_stream_sync(s);
-  const double ms = hrc ? 0.0 : event_ms(&ev, 0, 1);
-  events_close(&ev);
-  if (hrc) return hrc == HB_E_INVAL ? -1 : -5;
-  if (stage_out(&out, s)) return -5;
+  if (hrc) {
+    events_close(&ev);
+    return hrc == HB_E_INVAL ? -1 : -5;
+  }
   htp_registry_touch(out.fd);
-  const int32_t elapsed = (int32_t)(ms * 1e3);
-  memcpy(payload + offsetof(struct NativeAuxParams, elapsed_us), &elapsed, sizeof(elapsed));
-  return 0;
+  if (complete(&ev, 0, 1, payload + offsetof(struct NativeAuxParams, elapsed_us), 0.0, out.is_device)) return -5;
+  return stage_out(&out, s) ? -5 : 0;
 }
 
 /* ---- dispatcher ---------------------------------------------------------------- */

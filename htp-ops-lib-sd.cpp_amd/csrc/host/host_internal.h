@@ -61,10 +61,20 @@ int htp_weight_cache_enabled(void);
 
 /* ---- executor scratch (executor.c) --------------------------------------- */
 
-/* Device scratch owned by the executor, grown on demand (slot 0..3). */
+/* Device scratch owned by the executor, grown on demand (slot 0..4). */
 void *htp_executor_scratch(int slot, size_t bytes);
 hb_stream htp_executor_stream(void);
 int htp_executor_ensure_device(void);
+
+/* Mailbox messages: between begin and end, requests whose tensors all live
+ * in HBM complete without a stream synchronisation each; end (or flush)
+ * synchronises once, writes their elapsed_us fields, and on a GPU failure
+ * overwrites their return codes (`state`, an int32 in the request header)
+ * with -5. */
+void htp_executor_message_begin(void);
+int htp_executor_message_request(struct OpComputeRequest *req, size_t req_size, void *state);
+int htp_executor_flush(void);
+int htp_executor_message_end(void);
 
 /* ---- backend (backend.c) ------------------------------------------------- */
 

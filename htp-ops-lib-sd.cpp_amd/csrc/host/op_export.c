@@ -39,8 +39,11 @@ int htp_ops_rpc_mat_mul_permuted_w16a32_trace_session(htp_ops_session *session, 
 /* Opcode 16 (shared-message F16 GEMM with fused epilogue) is implemented. */
 int htp_ops_f16_epilogue_version(void) { return 1; }
 
-/* Opcodes 17-19 (native conv / attention / model aux) are not implemented
- * here; 0 keeps link compatibility without advertising them. */
+/* Opcode 19's DiT modes (9 LayerNorm + modulation, 10 gated residual, 11
+ * matrix RoPE, 12 strided SwiGLU, 13 SwiGLU beside the attention output) are
+ * implemented, so both DiT markers advertise them (reference
+ * src/host/op_export.c:45-48).  Opcodes 17 and 18 (native conv / attention)
+ * are not: the native-model marker stays 0. */
 int htp_ops_native_model_version(void) { return 0; }
-int htp_ops_dit_aux_version(void) { return 0; }
-int htp_ops_dit_concat_version(void) { return 0; }
+int htp_ops_dit_aux_version(void) { return 1; }
+int htp_ops_dit_concat_version(void) { return 1; }

@@ -1,52 +1,67 @@
 /*
- * Host session API with the reference's semantics (reference
- * src/host/session.c:14-382): explicit sessions, a process-wide default
- * session with legacy global wrappers, an active-session selector and the
- * channel token derived from a reserved session's index.  A session owns one
- * backend instance (htp_ops_open) instead of a FastRPC process domain.
+ * Host session API (contract: reference include/host/session.h:13-49).
+ *
+ * A session here is a thin record around one backend instance of this
+ * library (htp_ops_open): the backend holds the GPU state, the session only
+ * remembers which instance it owns, the caller's domain number, whether it
+ * took a reserved ordinal, and which lifecycle steps succeeded.
+ *
+ * Process-wide state is one registry: the legacy session that
+ * open_dsp_session() creates, the session selected for the legacy op
+ * wrappers (NULL selects the legacy session), and a bitmask of reserved
+ * ordinals.  A reserved session's ordinal is its id and names it in the
+ * channel token (ordinal << 32 | domain) that V2 map requests carry.
  */
+#include <pthread.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
 #include "htp_ops/session.h"
 
+enum { SESSION_BACKEND_UP = 1u << 0, SESSION_CHANNEL_UP = 1u << 1 };
+
 struct htp_ops_session {
-  remote_handle64 handle;
-  uint32_t session_id;
-  uint32_t session_index; /* reserved-session ordinal (0 = default session) */
-  uint32_t effective_domain_id;
-  int base_domain_id;
-  int reserved;
-  int backend_initialized;
-  int channel_initialized;
+  remote_handle64 backend; /* the backend instance this session owns */
+  int domain;              /* domain number given at open */
+  uint32_t ordinal;        /* reserved ordinal (1..31), 0 when not reserved */
+  unsigned flags;          /* SESSION_* */
 };
 
-#define INVALID_HANDLE ((remote_handle64)-1)
-#define MAX_RESERVED_SESSIONS 32
+#define NO_BACKEND ((remote_handle64)-1)
 
-static htp_ops_session *default_session = NULL;
-static htp_ops_session *active_session = NULL;
-static remote_handle64 legacy_handle = INVALID_HANDLE;
-static int reserved_in_use[MAX_RESERVED_SESSIONS];
+static struct {
+  pthread_mutex_t lock;
+  htp_ops_session *legacy;   /* opened by open_dsp_session() */
+  htp_ops_session *selected; /* backs the legacy wrappers; NULL = legacy */
+  uint32_t ordinals;         /* bit i set: reserved ordinal i is taken (bit 0 never) */
+} g_sessions = {PTHREAD_MUTEX_INITIALIZER, NULL, NULL, 0u};
 
-static uint32_t alloc_reserved_index(void) {
-  for (uint32_t i = 1; i < MAX_RESERVED_SESSIONS; ++i) {
-    if (!reserved_in_use[i]) {
-      reserved_in_use[i] = 1;
-      return i;
-    }
+static uint32_t take_ordinal(void) {
+  pthread_mutex_lock(&g_sessions.lock);
+  const uint32_t free_bits = ~g_sessions.ordinals & ~1u;
+  uint32_t ordinal = 0;
+  if (free_bits) {
+    ordinal = (uint32_t)__builtin_ctz(free_bits);
+    g_sessions.ordinals |= 1u << ordinal;
   }
-  return 0;
+  pthread_mutex_unlock(&g_sessions.lock);
+  return ordinal;
 }
 
-static void free_reserved_index(uint32_t i) {
-  if (i > 0 && i < MAX_RESERVED_SESSIONS) reserved_in_use[i] = 0;
+static void give_back_ordinal(uint32_t ordinal) {
+  if (ordinal == 0 || ordinal >= 32) return;
+  pthread_mutex_lock(&g_sessions.lock);
+  g_sessions.ordinals &= ~(1u << ordinal);
+  pthread_mutex_unlock(&g_sessions.lock);
 }
 
-static uint64_t channel_token(const htp_ops_session *s) {
-  if (!s || !s->reserved) return 0;
-  return ((uint64_t)s->session_index << 32) | s->effective_domain_id;
+static int usable(const htp_ops_session *s) { return s && s->backend != NO_BACKEND; }
+
+/* Runs one backend lifecycle call and records its outcome in the session's flags. */
+static int step(htp_ops_session *s, int err, unsigned flag, int set_on_success) {
+  if (err == AEE_SUCCESS) s->flags = set_on_success ? (s->flags | flag) : (s->flags & ~flag);
+  return err;
 }
 
 int htp_ops_session_open(htp_ops_session **out, int base_domain, const char *name, int reserve_new) {
@@ -54,21 +69,18 @@ int htp_ops_session_open(htp_ops_session **out, int base_domain, const char *nam
   *out = NULL;
   htp_ops_session *s = (htp_ops_session *)calloc(1, sizeof(*s));
   if (!s) return -1;
-  s->handle = INVALID_HANDLE;
-  s->base_domain_id = base_domain;
-  s->effective_domain_id = (uint32_t)base_domain;
-  s->reserved = reserve_new != 0;
-  if (s->reserved) {
-    s->session_index = alloc_reserved_index();
-    if (s->session_index == 0) {
-      fprintf(stderr, "htp_ops: no free reserved session index (max %d)\n", MAX_RESERVED_SESSIONS - 1);
+  s->backend = NO_BACKEND;
+  s->domain = base_domain;
+  if (reserve_new) {
+    s->ordinal = take_ordinal();
+    if (!s->ordinal) {
+      fprintf(stderr, "htp_ops: all 31 reserved session ordinals are taken\n");
       free(s);
       return -1;
     }
-    s->session_id = s->session_index;
   }
-  if (htp_ops_open(name, &s->handle) != AEE_SUCCESS) {
-    free_reserved_index(s->session_index);
+  if (htp_ops_open(name, &s->backend) != AEE_SUCCESS) {
+    give_back_ordinal(s->ordinal);
     free(s);
     return -1;
   }
@@ -76,118 +88,107 @@ int htp_ops_session_open(htp_ops_session **out, int base_domain, const char *nam
   return 0;
 }
 
-htp_ops_session *htp_ops_default_session(void) { return default_session; }
+htp_ops_session *htp_ops_default_session(void) { return g_sessions.legacy; }
 
 int htp_ops_session_init_backend(htp_ops_session *s) {
-  if (!s || s->handle == INVALID_HANDLE) return -1;
+  if (!usable(s)) return -1;
+  /* Reserved sessions of a multi-session process only map buffers. */
   const char *multi = getenv("SD_HTP_MULTI_SESSION");
-  int err;
-  if (s->reserved && multi && multi[0] != '0') {
-    err = htp_ops_init_mapping_backend(s->handle);
-  } else {
-    err = htp_ops_init_backend(s->handle);
-  }
-  if (err == AEE_SUCCESS) s->backend_initialized = 1;
-  return err;
+  const int mapping_only = s->ordinal && multi && multi[0] != '0';
+  return step(s, mapping_only ? htp_ops_init_mapping_backend(s->backend) : htp_ops_init_backend(s->backend),
+              SESSION_BACKEND_UP, 1);
 }
 
 int htp_ops_session_acquire_backend(htp_ops_session *s) {
-  if (!s || s->handle == INVALID_HANDLE) return -1;
-  const int err = htp_ops_init_backend(s->handle);
-  if (err == AEE_SUCCESS) s->backend_initialized = 1;
-  return err;
+  if (!usable(s)) return -1;
+  return step(s, htp_ops_init_backend(s->backend), SESSION_BACKEND_UP, 1);
 }
 
 int htp_ops_session_release_backend(htp_ops_session *s) {
-  if (!s || s->handle == INVALID_HANDLE) return -1;
-  const int err = htp_ops_release_backend(s->handle);
-  if (err == AEE_SUCCESS) s->backend_initialized = 0;
-  return err;
+  if (!usable(s)) return -1;
+  return step(s, htp_ops_release_backend(s->backend), SESSION_BACKEND_UP, 0);
 }
 
 int htp_ops_session_create_channel(htp_ops_session *s, int fd, unsigned int max_msg_size) {
-  if (!s || s->handle == INVALID_HANDLE) return -1;
-  const int err = htp_ops_create_channel(s->handle, fd, max_msg_size);
-  if (err == AEE_SUCCESS) s->channel_initialized = 1;
-  return err;
+  if (!usable(s)) return -1;
+  return step(s, htp_ops_create_channel(s->backend, fd, max_msg_size), SESSION_CHANNEL_UP, 1);
 }
 
 int htp_ops_session_create_channel_with_token(htp_ops_session *s, int fd, unsigned int max_msg_size) {
-  if (!s || s->handle == INVALID_HANDLE) return -1;
-  const int err = htp_ops_create_channel_with_token(s->handle, channel_token(s), fd, max_msg_size);
-  if (err == AEE_SUCCESS) s->channel_initialized = 1;
-  return err;
+  if (!usable(s)) return -1;
+  const uint64_t token = s->ordinal ? ((uint64_t)s->ordinal << 32) | (uint32_t)s->domain : 0u;
+  return step(s, htp_ops_create_channel_with_token(s->backend, token, fd, max_msg_size), SESSION_CHANNEL_UP, 1);
 }
 
 int htp_ops_session_destroy_channel(htp_ops_session *s) {
-  if (!s || s->handle == INVALID_HANDLE) return -1;
-  const int err = htp_ops_destroy_channel(s->handle);
-  if (err == AEE_SUCCESS) s->channel_initialized = 0;
-  return err;
+  if (!usable(s)) return -1;
+  return step(s, htp_ops_destroy_channel(s->backend), SESSION_CHANNEL_UP, 0);
 }
 
-remote_handle64 htp_ops_session_handle(const htp_ops_session *s) { return s ? s->handle : INVALID_HANDLE; }
+remote_handle64 htp_ops_session_handle(const htp_ops_session *s) { return s ? s->backend : NO_BACKEND; }
 
 int htp_ops_set_active_session(htp_ops_session *s) {
-  if (!s || s->handle == INVALID_HANDLE) return -1;
-  active_session = s;
+  if (!usable(s)) return -1;
+  g_sessions.selected = s;
   return 0;
 }
 
 int htp_ops_set_default_session(void) {
-  if (!default_session || default_session->handle == INVALID_HANDLE) return -1;
-  active_session = default_session;
+  if (!usable(g_sessions.legacy)) return -1;
+  g_sessions.selected = NULL;
   return 0;
 }
 
-uint32_t htp_ops_session_id(const htp_ops_session *s) { return s ? s->session_id : 0; }
-uint32_t htp_ops_session_domain(const htp_ops_session *s) { return s ? s->effective_domain_id : 0; }
-int htp_ops_session_is_reserved(const htp_ops_session *s) { return s && s->reserved; }
-int htp_ops_session_is_initialized(const htp_ops_session *s) { return s && s->backend_initialized; }
-int htp_ops_session_has_channel(const htp_ops_session *s) { return s && s->channel_initialized; }
+uint32_t htp_ops_session_id(const htp_ops_session *s) { return s ? s->ordinal : 0u; }
+uint32_t htp_ops_session_domain(const htp_ops_session *s) { return s ? (uint32_t)s->domain : 0u; }
+int htp_ops_session_is_reserved(const htp_ops_session *s) { return s && s->ordinal != 0; }
+int htp_ops_session_is_initialized(const htp_ops_session *s) { return s && (s->flags & SESSION_BACKEND_UP); }
+int htp_ops_session_has_channel(const htp_ops_session *s) { return s && (s->flags & SESSION_CHANNEL_UP); }
 
 void htp_ops_session_close(htp_ops_session *s) {
   if (!s) return;
-  if (s->handle != INVALID_HANDLE) {
-    if (s->channel_initialized) (void)htp_ops_destroy_channel(s->handle);
-    htp_ops_close(s->handle);
+  if (s->backend != NO_BACKEND) {
+    /* closing the backend stops its channel as well */
+    (void)htp_ops_close(s->backend);
   }
-  if (s->reserved) free_reserved_index(s->session_index);
-  if (active_session == s) active_session = default_session == s ? NULL : default_session;
+  give_back_ordinal(s->ordinal);
+  /* a closed session can no longer back the legacy wrappers */
+  if (g_sessions.selected == s) g_sessions.selected = NULL;
+  if (g_sessions.legacy == s) g_sessions.legacy = NULL;
   free(s);
 }
 
 remote_handle64 get_global_handle(void) {
-  if (active_session) return active_session->handle;
-  return default_session ? default_session->handle : legacy_handle;
+  const htp_ops_session *s = g_sessions.selected ? g_sessions.selected : g_sessions.legacy;
+  return s ? s->backend : NO_BACKEND;
 }
 
 int open_dsp_session(int domain_id, int unsigned_pd_enabled) {
-  (void)unsigned_pd_enabled;
-  if (default_session) return 0;
-  const int err = htp_ops_session_open(&default_session, domain_id, NULL, 0);
+  (void)unsigned_pd_enabled; /* no protection domains on the GPU */
+  if (g_sessions.legacy) return 0;
+  htp_ops_session *s = NULL;
+  const int err = htp_ops_session_open(&s, domain_id, NULL, 0);
   if (err == 0) {
-    legacy_handle = default_session->handle;
-    active_session = default_session;
+    g_sessions.legacy = s;
+    g_sessions.selected = NULL;
   }
   return err;
 }
 
 void close_dsp_session(void) {
-  htp_ops_session_close(default_session);
-  default_session = NULL;
-  active_session = NULL;
-  legacy_handle = INVALID_HANDLE;
+  htp_ops_session_close(g_sessions.legacy);
+  g_sessions.legacy = NULL;
+  g_sessions.selected = NULL;
 }
 
 void init_htp_backend(void) {
-  if (default_session) (void)htp_ops_session_init_backend(default_session);
+  if (g_sessions.legacy) (void)htp_ops_session_init_backend(g_sessions.legacy);
 }
 
-int release_htp_backend(void) { return htp_ops_session_release_backend(default_session); }
+int release_htp_backend(void) { return htp_ops_session_release_backend(g_sessions.legacy); }
 
 int create_htp_message_channel(int fd, unsigned int max_msg_size) {
-  return htp_ops_session_create_channel(default_session, fd, max_msg_size);
+  return htp_ops_session_create_channel(g_sessions.legacy, fd, max_msg_size);
 }
 
-int destroy_htp_message_channel(void) { return htp_ops_session_destroy_channel(default_session); }
+int destroy_htp_message_channel(void) { return htp_ops_session_destroy_channel(g_sessions.legacy); }

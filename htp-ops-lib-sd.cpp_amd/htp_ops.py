@@ -411,12 +411,20 @@ class Graph:
         return _GraphCapture(cls(), stream)
 
     def launch(self, stream=None):
+        if not self.ptr:
+            raise HtpOpsError("graph launched after destroy()")
         check(lib().hb_graph_launch(self.ptr, stream), "hb_graph_launch")
+
+    def destroy(self):
+        """Frees the instantiated graph now (callers destroy a graph before
+        freeing the buffers its launches use; __del__ is only a fallback)."""
+        if self.ptr:
+            ptr, self.ptr = self.ptr, None
+            check(lib().hb_graph_destroy(ptr), "hb_graph_destroy")
 
     def __del__(self):
         try:
-            if self.ptr:
-                lib().hb_graph_destroy(self.ptr)
+            self.destroy()
         except Exception:
             pass
 

@@ -145,8 +145,8 @@ def test_capability_markers():
     lib = htp_ops.lib()
     assert lib.htp_ops_f16_epilogue_version() == 1
     assert lib.htp_ops_native_model_version() == 0
-    assert lib.htp_ops_dit_aux_version() == 0
-    assert lib.htp_ops_dit_concat_version() == 0
+    assert lib.htp_ops_dit_aux_version() == 1      # opcode 19 modes 9-13 are implemented
+    assert lib.htp_ops_dit_concat_version() == 1
 
 
 def test_wire_helpers_sizes():

@@ -37,7 +37,14 @@ def rpc(nbytes, device):
 
 
 @pytest.mark.parametrize("device", [False, True])
-@pytest.mark.parametrize("m,k,n", [(77, 768, 3072), (1, 4096, 1024), (300, 96, 512)])
+@pytest.mark.parametrize("m,k,n", [
+    (77, 768, 3072),   # C1: the one-launch small kernel (quantizes its own rows)
+    (1, 4096, 1024),   # one row: quantization inside the weight stream
+    (3, 4096, 2048),   # 2-4 rows fused
+    (16, 4096, 4096),  # few rows: quantize + decode GEMM
+    (64, 1536, 1024),  # 5-128 rows, short K
+    (300, 96, 512),    # quantize + tiled GEMM
+])
 def test_opcode15_bit_exact(hip, orc, device, m, k, n):
     x, blob = w8a8_inputs(orc, m, k, n, seed=m + n, inv=True, sums=True)
     out, act, cst = rpc(m * n * 4 + 256, device), rpc(m * k * 4 + 512, device), rpc(blob.nbytes + 1024, device)
@@ -106,6 +113,39 @@ def test_opcode15_weight_cache_follows_rewrites(hip, orc):
         ref = orc.linear(x, blob, k, n)
         assert np.array_equal(out.read(np.float32, m * n).reshape(m, n), ref)
     assert h.lib().htp_ops_amd_invalidate_weights(cst.fd) >= 1
+
+
+@pytest.mark.parametrize("section", ["inverse", "scale", "weights"])
+def test_opcode15_host_blob_rewritten_in_place(hip, orc, section):
+    """The reference reads the constants on every call, so rewriting part of a
+    host-resident blob in place (no map put, no invalidate call) must change
+    the next result: the smoothing vector, the per-column scales, or one
+    weight byte far from the blob's ends."""
+    m, k, n = 8, 1536, 1024
+    x, blob = w8a8_inputs(orc, m, k, n, seed=51, inv=True)
+    out, act, cst = rpc(m * n * 4, False), rpc(m * k * 4, False), rpc(blob.nbytes, False)
+    act.write(x)
+    cst.write(blob)
+    params = h.w8a8_params((out.fd, 0), (act.fd, 0), (cst.fd, 0), m, k, n)
+    assert h.execute(15, params)[0] == 0
+    assert np.array_equal(out.read(np.float32, m * n).reshape(m, n), orc.linear(x, blob, k, n))
+    new = blob.copy()
+    if section == "inverse":
+        off = 128 + k * n + 8 * n
+        new[off:off + 4 * k] = np.frombuffer(orc.uniform(k, 0.25, 4.0, 52).tobytes(), np.uint8)
+    elif section == "scale":
+        off = 128 + k * n
+        new[off:off + 4 * n] = np.frombuffer(orc.uniform(n, 1e-3, 1e-2, 53).tobytes(), np.uint8)
+    else:
+        off = 128 + k * n // 2 + 4093
+        new[off] = np.uint8((int(new[off]) + 77) & 0xff)
+    # written straight into the rpcmem memory, as a caller does (the library sees no write)
+    end = off + (4 * k if section == "inverse" else 4 * n if section == "scale" else 1)
+    cst.host_view()[off:end] = new[off:end]
+    assert h.execute(15, params)[0] == 0
+    ref = orc.linear(x, new, k, n)
+    assert not np.array_equal(ref, orc.linear(x, blob, k, n))
+    assert np.array_equal(out.read(np.float32, m * n).reshape(m, n).view(np.uint32), ref.view(np.uint32))
 
 
 def test_opcode15_device_blob_header_after_cache_hit(hip, orc):
@@ -248,3 +288,44 @@ def test_test_ops_on_gpu_backend(hip):
     scope = ctypes.c_int32()
     assert lib.htp_ops_test_ops(handle, ctypes.byref(scope)) == 0 and scope.value == 1
     assert lib.htp_ops_close(handle) == 0
+
+
+def test_mailbox_device_requests_complete_once_per_message(hip, orc):
+    """Several opcode-15 requests on HBM tensors in one message: the executor
+    synchronises once for the message, yet every output is complete and
+    every elapsed_us field is written when the completion flag is seen."""
+    lib = h.lib()
+    assert lib.open_dsp_session(3, 1) == 0
+    lib.init_htp_backend()
+    chan = h.RpcBuffer(4096)
+    assert lib.create_htp_message_channel(chan.fd, 4096) == 0
+    cases = [(1024, 1536, 3072, 61), (1, 4096, 2048, 62), (77, 768, 3072, 63), (300, 1536, 1536, 64)]
+    bufs, reqs, refs = [], [], []
+    for m, k, n, seed in cases:
+        x, blob = w8a8_inputs(orc, m, k, n, seed=seed, inv=True)
+        out, act, cst = rpc(m * n * 4, True), rpc(m * k * 4, True), rpc(blob.nbytes, True)
+        act.write(x)
+        cst.write(blob)
+        bufs.append((out, act, cst))
+        reqs.append((h.REQUEST_TYPE_OP_COMPUTE,
+                     h.compute_request(15, h.w8a8_params((out.fd, 0), (act.fd, 0), (cst.fd, 0), m, k, n))))
+        refs.append(orc.linear(x, blob, k, n))
+    view = chan.host_view()
+    for rep in range(2):
+        for out, _, _ in bufs:
+            out.write(np.zeros(out.nbytes // 4, np.float32))
+        done, offs = post(view, reqs, 4096)
+        assert [h.request_state(done, offs, i) for i in range(len(cases))] == [0] * len(cases)
+        for i, ((m, k, n, _), (out, _, _), ref) in enumerate(zip(cases, bufs, refs)):
+            got = out.read(np.float32, m * n).reshape(m, n)
+            assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (rep, i)
+            elapsed = struct.unpack_from("<i", h.request_data(done, offs, i), 4 + 36)[0]
+            assert elapsed >= 0
+        # the largest request takes well over a microsecond of GPU time
+        assert struct.unpack_from("<i", h.request_data(done, offs, 0), 4 + 36)[0] >= 1
+    assert lib.destroy_htp_message_channel() == 0
+    lib.close_dsp_session()
+    chan.free()
+    for trio in bufs:
+        for b in trio:
+            b.free()
