@@ -11,6 +11,7 @@
 // which equals acc - (sums << 7) modulo 2^32 for every input.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cstdint>
 #include <cstdlib>
@@ -428,6 +429,273 @@ __global__ __launch_bounds__(64 * WM *WN) void w8a8_gemm_tiles(void *__restrict_
       }
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// Streaming tiled GEMM (persistent): one workgroup per CU walks its share of
+// BM x BN output tiles with one continuous operand ring, so the next tile's
+// first k-steps are in flight while a tile finishes.
+//
+// Two kinds of waves, because a wave's loads and stores complete in issue
+// order for its s_waitcnt count: a wave that has issued output stores cannot
+// wait for a later DMA stage without also waiting for those stores.
+//  - ND DMA waves issue every operand DMA (global_load_lds, 1 KB lane-ordered
+//    blocks) and the tile parameters, wait for their own DMA only, and publish
+//    each stage with the workgroup barrier.  They keep S - 3 stages in flight
+//    while the compute waves work on the stage before, and do little else:
+//    the scalar unit is shared by every wave of the CU.
+//  - WM x WN compute waves never load from global memory.  Each step they
+//    read the next step's fragments from LDS while the current step's MFMAs
+//    run.  Operands are swapped in the MFMA (weights as src0), so a lane holds
+//    4 consecutive output columns of one row.  At a tile's end they apply the
+//    epilogue in registers, regroup each 8-row x 32-column piece through a
+//    wave-private LDS buffer so that one store writes 8 whole 128-byte lines,
+//    and store without waiting: the stores drain during the next tile's main
+//    loop.  The stores are non-temporal, so the output does not evict the
+//    operands the other CUs of the XCD still read from L2.
+//  - The epilogue parameters of a tile (corr and sw of its BN columns, the row
+//    scales of its BM rows) arrive in LDS by DMA with the tile's first k-step,
+//    double-buffered by tile parity: DMA wave 0 loads corr and sw (16 bytes per
+//    lane), DMA wave d loads rows 64d..64d+63 of the scales (4 bytes per lane,
+//    rows past m clamped).
+//  - Stores are buffer stores bounded by the tile's valid rows; columns past
+//    n get an out-of-range offset.
+//  - The XCD that runs a workgroup (blockIdx % 8) owns a contiguous chunk of
+//    the tiles in 4-row-block groups; its workgroups take consecutive tiles of
+//    the chunk, so the A and B blocks they share stay in that XCD's L2.
+// Requires gridDim.x % 8 == 0 and kp / 64 >= S - 1 (a tile's parameter
+// buffer is rewritten only after the tile two before it has finished).
+// ---------------------------------------------------------------------------
+
+__device__ inline void grouped_tile(int p, int tiles_m, int tiles_n, int &tm, int &tn) {
+  constexpr int G = 4;
+  const int first_m = (p / (G * tiles_n)) * G;
+  const int gsize = min(tiles_m - first_m, G);
+  const int in_group = p % (G * tiles_n);
+  tm = first_m + in_group % gsize;
+  tn = in_group / gsize;
+}
+
+// Operand and parameter DMA of the streaming kernel's DMA wave d (of ND):
+// one stage per issue(), in step order across the workgroup's tiles.  TAG
+// (the kernel's epilogue) gives each kernel instantiation its own type:
+// hipcc's host pass drops the launch stub of a second kernel that shares
+// this device-only type with another.
+template <int BM, int BN, int ND, bool SCALES, int TAG>
+struct StreamDma {
+  static constexpr int ABLK = BM / 16, BBLK = BN / 16, NB = ABLK + BBLK, PW = NB / ND;
+  static_assert(NB % ND == 0 && (!SCALES || BM / 64 <= ND), "DMA split");
+  const int8_t *src[PW];
+  const int8_t *pcs, *psc;  // corr|sw block (wave 0) and scale rows of this wave
+  int tile, kt, slot;
+
+  // parameter DMA instructions of wave d per tile
+  __device__ static constexpr int param_ops(int d) { return (d == 0 ? 1 : 0) + (SCALES && d < BM / 64 ? 1 : 0); }
+
+  // Points the DMA at tile (tm, tn): operand blocks (clamped into A and B)
+  // and this wave's parameter blocks.
+  __device__ void point(int tm, int tn, const int8_t *q, const int8_t *wpack, const float *scales, const float *sw,
+                        const int32_t *corr, int m, int n, int ktc, int d, int lane) {
+    const int mblocks = (m + 15) / 16, nblocks = n / 16;
+#pragma unroll
+    for (int i = 0; i < PW; ++i) {
+      const int b = i * ND + d;
+      if (b < ABLK) {
+        const int mb = min(tm * ABLK + b, mblocks - 1);
+        src[i] = q + (size_t)mb * ktc * kFragBytes + lane * 16;
+      } else {
+        const int nb = min(tn * BBLK + (b - ABLK), nblocks - 1);
+        src[i] = wpack + (size_t)nb * ktc * kFragBytes + lane * 16;
+      }
+    }
+    // lanes 0..31: corr of the tile's columns, 32..63: sw; n % 16 == 0, so a
+    // group of 4 columns lies wholly inside or wholly past n (then clamped)
+    const int col = min(tn * BN + 4 * (lane & 31), n - 4);
+    pcs = lane < 32 ? (const int8_t *)(corr + col) : (const int8_t *)(sw + col);
+    psc = SCALES ? (const int8_t *)(scales + min(tm * BM + 64 * d + lane, m - 1)) : nullptr;
+  }
+
+  // Issues the DMA of the next stage into ring slot `slot` (and, at a tile's
+  // first k-step, the tile's parameters into buffer tile & 1).
+  __device__ void issue(int8_t *lds, int stage_bytes, int8_t *params, int pbuf, int ktc, int S, int d) {
+    int8_t *dst = lds + slot * stage_bytes;
+#pragma unroll
+    for (int i = 0; i < PW; ++i)
+      __builtin_amdgcn_global_load_lds(src[i] + (size_t)kt * kFragBytes, HB_LDS_PTR(dst + (i * ND + d) * kFragBytes),
+                                       16, 0, 0);
+    if (kt == 0) {
+      int8_t *pb = params + (tile & 1) * pbuf;
+      if (d == 0) __builtin_amdgcn_global_load_lds(pcs, HB_LDS_PTR(pb), 16, 0, 0);
+      if (SCALES && d < BM / 64) __builtin_amdgcn_global_load_lds(psc, HB_LDS_PTR(pb + kFragBytes + d * 256), 4, 0, 0);
+    }
+    if (++kt == ktc) kt = 0;
+    if (++slot == S) slot = 0;
+  }
+};
+
+__device__ inline __amdgpu_buffer_rsrc_t stream_out_rsrc(void *y, int ldy, int row0, int rows) {
+  return __builtin_amdgcn_make_buffer_rsrc((uint32_t *)y + (size_t)row0 * ldy, 0,
+                                           (uint32_t)rows * (uint32_t)ldy * 4u, 0x00020000);
+}
+
+template <int BM, int BN, int WM, int WN, int ND, int S, int EPI>
+__global__ __launch_bounds__(64 * (WM * WN + ND), 1) void w8a8_gemm_stream(void *__restrict__ y, int ldy,
+                                                                          const int8_t *__restrict__ q,
+                                                                          const float *__restrict__ scales,
+                                                                          const int8_t *__restrict__ wpack,
+                                                                          const float *__restrict__ sw,
+                                                                          const int32_t *__restrict__ corr, int m,
+                                                                          int n, int kp, int tiles_m, int tiles_n) {
+  constexpr int NW = WM * WN;  // compute waves 0..NW-1; DMA waves NW..NW+ND-1
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int FM = WTM / 16, FN = WTN / 16;
+  constexpr int ABLK = BM / 16;
+  constexpr int NB = ABLK + BN / 16;
+  constexpr int STAGE = NB * kFragBytes;
+  // parameters per tile: [corr | sw] (BN*8 bytes), then the row scales (BM*4 bytes)
+  static_assert(BN * 8 == kFragBytes && BM * 4 == kFragBytes, "parameter blocks of one kilobyte");
+  constexpr bool SCALES = EPI != HB_W8A8_EPI_RAW;
+  constexpr int PBUF = 2 * kFragBytes;
+  // per compute wave: 8 rows of 32 output values, rows padded by 16 bytes
+  constexpr int TROW = 32 * 4 + 16, TBUF = 8 * TROW;
+  static_assert(FN % 2 == 0, "column blocks in pairs (32 columns, one 128-byte line)");
+  using Dma = StreamDma<BM, BN, ND, SCALES, EPI>;
+  __shared__ __attribute__((aligned(1024))) int8_t lds[S * STAGE + 2 * PBUF + NW * TBUF];
+  int8_t *params = lds + S * STAGE;
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int ktc = kp / kKStep;
+
+  // This workgroup's tiles: chunk [c0, c1) of the grouped order belongs to its XCD.
+  const int total = tiles_m * tiles_n;
+  const int xcd = blockIdx.x % 8, slot = blockIdx.x / 8, nslots = gridDim.x / 8;
+  const int per = (total + 7) / 8;
+  const int c0 = min(total, xcd * per), c1 = min(total, c0 + per);
+  const int ntile = c0 + slot < c1 ? (c1 - c0 - slot + nslots - 1) / nslots : 0;
+  if (ntile == 0) return;
+  const int steps = ntile * ktc;
+
+  if (wave >= NW) {
+    // --------------------------------- DMA wave ---------------------------------
+    // Stage g + 1 has landed once at most (S - 3) * PW of this wave's DMA
+    // instructions are outstanding, while the S - 3 stages after it have
+    // been issued: each has at least PW instructions (a tile's first stage
+    // has the parameter DMA besides), so the count waits for stage g + 1 and
+    // possibly a parameter load after it.  With fewer stages left: vmcnt(0).
+    const int d = wave - NW;
+    Dma dma;
+    dma.tile = -1;
+    dma.kt = 0;
+    dma.slot = 0;
+#define STREAM_ISSUE()                                                                 \
+  do {                                                                                 \
+    if (dma.kt == 0) {                                                                 \
+      int tm_, tn_;                                                                    \
+      grouped_tile(c0 + slot + (++dma.tile) * nslots, tiles_m, tiles_n, tm_, tn_);     \
+      dma.point(tm_, tn_, q, wpack, scales, sw, corr, m, n, ktc, d, lane);             \
+    }                                                                                  \
+    dma.issue(lds, STAGE, params, PBUF, ktc, S, d);                                    \
+  } while (0)
+    static_assert(S >= 4, "at least one stage in flight behind the awaited one");
+    for (int st = 0; st < S - 1 && st < steps; ++st) STREAM_ISSUE();
+    if (S - 1 <= steps) wait_vmcnt<(S - 2) * Dma::PW>(); else wait_vmcnt<0>();
+    block_barrier();  // stage 0 published
+    for (int g = 0; g < steps; ++g) {
+      if (g + S - 2 < steps) wait_vmcnt<(S - 3) * Dma::PW>();
+      else if (g + 1 < steps) wait_vmcnt<0>();
+      block_barrier();  // stage g + 1 published; every compute wave is done with stage g - 1
+      if (g + S - 1 < steps) STREAM_ISSUE();  // into the slot stage g - 1 held
+    }
+#undef STREAM_ISSUE
+    return;
+  }
+
+  // ------------------------------- compute wave -------------------------------
+  const int wm = wave / WN, wn = wave % WN;
+  hb_i32x4 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = hb_i32x4{0, 0, 0, 0};
+  hb_i32x4 fa[2][FM], fb[2][FN];
+  const int aoff = (wm * FM) * kFragBytes + lane * 16, boff = (ABLK + wn * FN) * kFragBytes + lane * 16;
+  int8_t *tb = params + 2 * PBUF + wave * TBUF;
+  // regrouping: a lane of the MFMA layout holds row lane%16, columns 4*(lane/16)..+3
+  // of a 16x16 block; it writes them at row lane%8 of the 8-row piece, and reads back
+  // row lane/8, columns 4*(lane%8)..+3 of the 32-column pair
+  const int tw = (lane & 7) * TROW + (lane >> 4) * 16, tr = (lane >> 3) * TROW + (lane & 7) * 16;
+  block_barrier();  // stage 0 published
+#pragma unroll
+  for (int i = 0; i < FM; ++i) fa[0][i] = *(const hb_i32x4 *)(lds + aoff + i * kFragBytes);
+#pragma unroll
+  for (int j = 0; j < FN; ++j) fb[0][j] = *(const hb_i32x4 *)(lds + boff + j * kFragBytes);
+  int r = 0, kt = 0, rd_slot = 1 % S;  // tile and k-step of the step; slot of the next fragments
+
+  // One step g with fragments fa[P]/fb[P]; the next step's go to fa[1-P]/fb[1-P].
+#define STREAM_STEP(P)                                                                                       \
+  {                                                                                                          \
+    const int gg = g + (P);                                                                                  \
+    block_barrier();                                                                                         \
+    if (gg + 1 < steps) {                                                                                    \
+      const int8_t *base = lds + rd_slot * STAGE;                                                            \
+      if (++rd_slot == S) rd_slot = 0;                                                                       \
+      _Pragma("unroll") for (int i = 0; i < FM; ++i) fa[1 - (P)][i] =                                        \
+          *(const hb_i32x4 *)(base + aoff + i * kFragBytes);                                                 \
+      _Pragma("unroll") for (int j = 0; j < FN; ++j) fb[1 - (P)][j] =                                        \
+          *(const hb_i32x4 *)(base + boff + j * kFragBytes);                                                 \
+    }                                                                                                        \
+    _Pragma("unroll") for (int i = 0; i < FM; ++i) _Pragma("unroll") for (int j = 0; j < FN; ++j) acc[i][j] =  \
+        __builtin_amdgcn_mfma_i32_16x16x64_i8(fb[P][j], fa[P][i], acc[i][j], 0, 0, 0);                     \
+    if (++kt == ktc) {                                                                                       \
+      /* epilogue of tile r: parameters from LDS (they arrived with its first stage) */                      \
+      int tm, tn;                                                                                            \
+      grouped_tile(c0 + slot + r * nslots, tiles_m, tiles_n, tm, tn);                                        \
+      const int8_t *par = params + (r & 1) * PBUF;                                                           \
+      const __amdgpu_buffer_rsrc_t rsrc = stream_out_rsrc(y, ldy, tm * BM, min(BM, m - tm * BM));            \
+      _Pragma("unroll") for (int jp = 0; jp < FN / 2; ++jp) {                                                \
+        /* each lane stores columns col .. col+3 of rows 8h + lane/8 of the pair */                          \
+        const int col = tn * BN + wn * WTN + jp * 32 + 4 * (lane & 7);                                       \
+        _Pragma("unroll") for (int i = 0; i < FM; ++i) {                                                     \
+          /* parameters re-read per piece: short live ranges (registers are tight) */                        \
+          const int c0_ = wn * WTN + jp * 32 + 4 * (lane >> 4), c1_ = c0_ + 16;                              \
+          asm volatile("" ::: "memory");                                                                     \
+          const hb_i32x4 cc0 = *(const hb_i32x4 *)(par + c0_ * 4), cc1 = *(const hb_i32x4 *)(par + c1_ * 4); \
+          const hb_f32x4 sc0 = *(const hb_f32x4 *)(par + BN * 4 + c0_ * 4);                                 \
+          const hb_f32x4 sc1 = *(const hb_f32x4 *)(par + BN * 4 + c1_ * 4);                                 \
+          const float sv =                                                                                   \
+              SCALES ? *(const float *)(par + kFragBytes + (wm * WTM + i * 16 + (lane & 15)) * 4) : 0.0f;    \
+          hb_u32x4 o0, o1;                                                                                   \
+          _Pragma("unroll") for (int e = 0; e < 4; ++e) {                                                    \
+            o0[e] = epilogue_bits<EPI>(acc[i][2 * jp][e], cc0[e], sc0[e], sv);                               \
+            o1[e] = epilogue_bits<EPI>(acc[i][2 * jp + 1][e], cc1[e], sc1[e], sv);                           \
+          }                                                                                                  \
+          _Pragma("unroll") for (int h = 0; h < 2; ++h) {                                                    \
+            if (((lane >> 3) & 1) == h) {                                                                    \
+              *(hb_u32x4 *)(tb + tw) = o0;                                                                   \
+              *(hb_u32x4 *)(tb + tw + 64) = o1;                                                              \
+            }                                                                                                \
+            /* other lanes wrote tb: the read must not reuse this lane's earlier read (the wave's */         \
+            /* LDS operations execute in order, so no wait is needed) */                                     \
+            asm volatile("" ::: "memory");                                                                   \
+            const hb_u32x4 v = *(const hb_u32x4 *)(tb + tr);                                                 \
+            const int rl = wm * WTM + i * 16 + 8 * h + (lane >> 3);                                          \
+            const uint32_t off = col < n ? ((uint32_t)rl * (uint32_t)ldy + (uint32_t)col) * 4u : 0xfffffff0u; \
+            __builtin_amdgcn_raw_buffer_store_b128(v, rsrc, off, 0, 2);                                      \
+          }                                                                                                  \
+          acc[i][2 * jp] = hb_i32x4{0, 0, 0, 0};                                                             \
+          acc[i][2 * jp + 1] = hb_i32x4{0, 0, 0, 0};                                                         \
+        }                                                                                                    \
+      }                                                                                                      \
+      kt = 0;                                                                                                \
+      ++r;                                                                                                   \
+    }                                                                                                        \
+  }
+
+  for (int g = 0; g < steps; g += 2) {
+    STREAM_STEP(0)
+    if (g + 1 < steps) STREAM_STEP(1)
+  }
+#undef STREAM_STEP
 }
 
 // ---------------------------------------------------------------------------
@@ -1061,6 +1329,10 @@ struct TileShape {
 constexpr TileShape kTileShapes[] = {
     {128, 192, 2, 100}, {256, 192, 1, 90}, {128, 128, 2, 92}, {256, 256, 1, 100}, {64, 64, 4, 60}};
 constexpr int kNumShapes = 5;
+// Index kNumShapes selects the streaming kernel (w8a8_gemm_stream, 256 x 128
+// tiles, one persistent workgroup per CU).
+constexpr int kStreamShape = kNumShapes;
+constexpr int kStreamBM = 256, kStreamBN = 128, kStreamStages = 6;
 
 // -1: automatic.  Set by hb_w8a8_force_tile; HTP_OPS_AMD_W8A8_TILE gives
 // the initial value.
@@ -1071,7 +1343,7 @@ int forced_tile_shape() {
   if (forced == -2) {
     const char *v = getenv("HTP_OPS_AMD_W8A8_TILE");
     forced = (v && *v) ? atoi(v) : -1;
-    if (forced < -1 || forced >= kNumShapes) forced = -1;
+    if (forced < -1 || forced > kStreamShape) forced = -1;
     int expected = -2;
     if (!g_forced_tile.compare_exchange_strong(expected, forced)) forced = expected;
   }
@@ -1093,10 +1365,30 @@ int compute_units() {
 
 // Picks the shape minimising (rounds of resident workgroups) x (work per
 // round per CU) / eff; ties go to the earlier entry of kTileShapes.
-int pick_tile_shape(int m, int n) {
+// The streaming kernel needs kp / 64 >= kStreamStages - 1 (its parameter
+// double buffer).
+bool stream_applies(int kp) { return kp / kKStep >= kStreamStages - 1; }
+
+int stream_mode() {
+  static const int mode = getenv("HTP_OPS_AMD_W8A8_STREAM") ? atoi(getenv("HTP_OPS_AMD_W8A8_STREAM")) : -1;
+  return mode;
+}
+
+int pick_tile_shape(int m, int n, int kp) {
   const int forced = forced_tile_shape();
-  if (forced >= 0 && (kTileShapes[forced].bn != 192 || n % 192 == 0)) return forced;
+  if (forced == kStreamShape && stream_applies(kp)) return kStreamShape;
+  if (forced >= 0 && forced < kNumShapes && (kTileShapes[forced].bn != 192 || n % 192 == 0)) return forced;
   const int cus = compute_units();
+  const long long stream_tiles = (long long)((m + kStreamBM - 1) / kStreamBM) * ((n + kStreamBN - 1) / kStreamBN);
+  // The streaming kernel when its tiles spread evenly over the CUs (it keeps
+  // one workgroup per CU for the whole launch, so a partial last round costs a
+  // whole tile): measured against the automatic tiled choice, in us,
+  // 4096x6144x1536 41.9 vs 46.9, 2048x4096x4096 36.9 vs 40.1, 1024x4096x4096
+  // 30.2 vs 31.7, 4096x1536x6144 50.0 vs 50.4; with uneven rounds it loses
+  // (4096x1536x4608, 2.25 tiles per CU: 46.4 vs 40.5; 2048x4096x6144, 1.5:
+  // 60.8 vs 54.0).  HTP_OPS_AMD_W8A8_STREAM=1 / 0 forces it on / off.
+  const bool stream_even = stream_tiles <= cus || stream_tiles % cus == 0;
+  if (stream_mode() != 0 && stream_applies(kp) && (stream_mode() == 1 || stream_even)) return kStreamShape;
   int best = 0;
   long long best_cost = -1;
   for (int i = 0; i < kNumShapes; ++i) {
@@ -1116,7 +1408,16 @@ int pick_tile_shape(int m, int n) {
 template <int EPI>
 int launch_tiles(void *y, int ldy, const int8_t *q, const float *scales, const int8_t *wpack, const float *sw,
                  const int32_t *corr, int m, int n, int kp, hipStream_t st) {
-  const int shape = pick_tile_shape(m, n);
+  const int shape = pick_tile_shape(m, n, kp);
+  if (shape == kStreamShape) {
+    const int tiles_m = (m + kStreamBM - 1) / kStreamBM, tiles_n = (n + kStreamBN - 1) / kStreamBN;
+    const int tiles = tiles_m * tiles_n;
+    const int grid = std::min(compute_units(), (tiles + 7) / 8 * 8) / 8 * 8;
+    if (grid < 8) return hb_invalid("w8a8_gemm_stream grid");
+    hipLaunchKernelGGL((w8a8_gemm_stream<kStreamBM, kStreamBN, 4, 2, 4, kStreamStages, EPI>), dim3(grid), dim3(768),
+                       0, st, y, ldy, q, scales, wpack, sw, corr, m, n, kp, tiles_m, tiles_n);
+    return hb_check_launch("w8a8_gemm_stream");
+  }
   const TileShape t = kTileShapes[shape];
   const int grid = ((m + t.bm - 1) / t.bm) * ((n + t.bn - 1) / t.bn);
   switch (shape) {
@@ -1491,7 +1792,7 @@ int hb_w8a8_linear(float *d_y, const float *d_x, const void *d_packed, int m, in
 }
 
 int hb_w8a8_force_tile(int index) {
-  if (index < -1 || index >= kNumShapes) return hb_invalid("hb_w8a8_force_tile index");
+  if (index < -1 || index > kStreamShape) return hb_invalid("hb_w8a8_force_tile index");
   forced_tile_shape();  // settle the environment default first
   return g_forced_tile.exchange(index);
 }

@@ -137,7 +137,7 @@ def test_w8a8_linear_bit_exact(hip, orc, m, k, n):
     np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
 
 
-@pytest.mark.parametrize("tile", range(5))
+@pytest.mark.parametrize("tile", range(6))
 @pytest.mark.parametrize("m,k,n", [(261, 224, 960), (300, 1536, 576)])
 def test_w8a8_every_tile_shape_bit_exact(hip, orc, tile, m, k, n):
     """Each tiled kernel instantiation, pinned in turn, with M, N and K tails
@@ -161,6 +161,68 @@ def test_w8a8_every_tile_shape_bit_exact(hip, orc, tile, m, k, n):
     ref = orc.linear(x, blob, k, n)
     got = y.read(np.float32, m * n).reshape(m, n)
     np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+STREAM_TILE = 5  # hb_w8a8_force_tile index of the persistent streaming kernel
+
+
+@pytest.mark.parametrize("m,k,n", [
+    (4096, 1536, 6144),  # headline: three 256x128 tiles per workgroup, one 16x16 block stored per k-step
+    (1000, 320, 1088),   # fewest k-steps the kernel takes (5: four blocks stored per step); ragged M and N tiles
+    (5000, 512, 4160),   # uneven tiles per workgroup (2 or 3), two blocks per step
+    (777, 480, 2112),    # K % 64 == 32 (zero-padded k-step), 4 x 17 tiles: many workgroups without a tile
+    (2304, 1088, 2112),  # 17 k-steps (one block per step, the last step stores none)
+])
+@pytest.mark.parametrize("epi", ["raw", "scale", "gelu"])
+def test_w8a8_stream_kernel_bit_exact(hip, orc, m, k, n, epi):
+    """The streaming kernel pinned: raw int32 accumulators and SCALE outputs
+    bit-exact, GELU within 1e-5 relative of the oracle's GELU."""
+    x, _, blob = make_w8a8(orc, m, k, n, seed=m + k + n, inv_kind="uniform", sums_kind="random", outliers=0.01,
+                           scale_lo=1e-3 if epi == "gelu" else 1e-4, scale_hi=1e-2 if epi == "gelu" else 1e-3)
+    packed = hip.w8a8_prepack(upload_blob(hip, blob), k, n)
+    xd = hip.DeviceBuffer.from_array(x)
+    q, s = hip.w8a8_quantize(xd, packed.ptr + hip.w8a8_packed_offset(k, n, hip.SECTION_INV), m, k)
+    y = hip.DeviceBuffer(m * n * 4)
+    y.fill(0xA5)
+    epilogue = {"raw": hip.EPI_RAW, "scale": hip.EPI_SCALE, "gelu": hip.EPI_SCALE_GELU}[epi]
+    prev = hip.w8a8_force_tile(STREAM_TILE)
+    try:
+        hip.w8a8_gemm(y, q, s, packed, m, k, n, epilogue)
+        hip.sync()
+    finally:
+        hip.w8a8_force_tile(prev)
+    inv = np.frombuffer(blob[128 + k * n + 8 * n:].tobytes(), np.float32)[:k]
+    if epi == "raw":
+        u, _ = orc.quantize(x, inv)
+        np.testing.assert_array_equal(y.read(np.int32, m * n).reshape(m, n), orc.accumulate(u, blob, k, n))
+        return
+    ref = orc.linear(x, blob, k, n)
+    got = y.read(np.float32, m * n).reshape(m, n)
+    if epi == "scale":
+        np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
+    else:
+        np.testing.assert_allclose(got, orc.gelu_tanh_array(ref), rtol=1e-5, atol=1e-30)
+
+
+def test_w8a8_stream_kernel_row_stride(hip, orc):
+    """Output rows with a stride past n (ldy > n): nothing outside the n
+    columns of each row is written."""
+    m, k, n, ldy = 600, 768, 1024, 1040
+    x, _, blob = make_w8a8(orc, m, k, n, seed=77, inv_kind="uniform", sums_kind="random")
+    packed = hip.w8a8_prepack(upload_blob(hip, blob), k, n)
+    xd = hip.DeviceBuffer.from_array(x)
+    q, s = hip.w8a8_quantize(xd, packed.ptr + hip.w8a8_packed_offset(k, n, hip.SECTION_INV), m, k)
+    y = hip.DeviceBuffer(m * ldy * 4)
+    y.fill(0xA5)
+    prev = hip.w8a8_force_tile(STREAM_TILE)
+    try:
+        hip.w8a8_gemm(y, q, s, packed, m, k, n, hip.EPI_SCALE, ldy=ldy)
+        hip.sync()
+    finally:
+        hip.w8a8_force_tile(prev)
+    got = y.read(np.uint32, m * ldy).reshape(m, ldy)
+    np.testing.assert_array_equal(got[:, :n], orc.linear(x, blob, k, n).view(np.uint32))
+    assert (got[:, n:] == 0xA5A5A5A5).all()
 
 
 # One row: hb_w8a8_linear quantizes inside the weight-streaming kernel
