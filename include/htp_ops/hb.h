@@ -121,8 +121,9 @@ int hb_w8a8_gemm(void *d_y, int ldy, const int8_t *d_q, const float *d_scales, c
                  int n, int epilogue, hb_stream s);
 
 /* Tuning and test hook: pins the tiled kernel's shape for every later call
- * (index into 128x192, 256x192, 128x128, 256x256, 64x64; shapes 192 wide
- * apply only when n % 192 == 0) or restores automatic choice with -1.
+ * (index into 128x192, 256x192, 128x128, 256x256, 64x64, then 5: the
+ * persistent streaming kernel with 256x128 tiles, for k >= 320; shapes 192
+ * wide apply only when n % 192 == 0) or restores automatic choice with -1.
  * Returns the previous setting.  Results are identical for every shape.
  * The environment variable HTP_OPS_AMD_W8A8_TILE gives the initial value. */
 int hb_w8a8_force_tile(int index);
