@@ -64,7 +64,8 @@ int hb_init(int device) {
     if (err != hipSuccess) return hb_fail(err, "hipStreamCreateWithFlags");
     g_streams[device] = st;
   }
-  return HB_OK;
+  // the no-allocation entry point's static workspace on this device
+  return hb_w8a8_static_setup(device);
 }
 
 hb_stream hb_default_stream(void) { return (hb_stream)hb_resolve_stream(nullptr); }

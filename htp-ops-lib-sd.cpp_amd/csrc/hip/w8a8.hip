@@ -1791,6 +1791,57 @@ int hb_w8a8_linear(float *d_y, const float *d_x, const void *d_packed, int m, in
   return hb_w8a8_gemm(d_y, n, q, scales, d_packed, m, k, n, epilogue, s);
 }
 
+// ---- no-allocation variant of hb_w8a8_linear ------------------------------------
+// Its workspace is this file-scope device array (one copy per GPU, held until
+// the process ends).  In host code the name `scratch` only stands in for the
+// symbol: its device address on the current GPU comes from
+// hipGetSymbolAddress, taken once per device (hb_init calls
+// hb_w8a8_static_setup) and used wherever host code passes the memory on.
+
+}  // extern "C"
+
+namespace {
+static __device__ __align__(256) uint8_t scratch[HB_W8A8_STATIC_SCRATCH_BYTES];
+constexpr int kMaxStaticDevices = 16;
+std::atomic<void *> g_scratch_ptr[kMaxStaticDevices];
+}  // namespace
+
+extern "C" {
+
+int hb_w8a8_static_setup(int device) {
+  if (device < 0 || device >= kMaxStaticDevices) return hb_invalid("hb_w8a8_static_setup device");
+  if (g_scratch_ptr[device].load(std::memory_order_acquire) != nullptr) return HB_OK;
+  int cur = -1;
+  hipError_t err = hipGetDevice(&cur);
+  if (err != hipSuccess) return hb_fail(err, "hipGetDevice");
+  if (cur != device) return hb_invalid("hb_w8a8_static_setup: device is not current");
+  void *ptr = nullptr;
+  err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (err != hipSuccess) return hb_fail(err, "hipGetSymbolAddress(scratch)");
+  if (ptr == nullptr || ((uintptr_t)ptr % 256) != 0) return hb_invalid("hb_w8a8_static_setup: scratch address");
+  g_scratch_ptr[device].store(ptr, std::memory_order_release);
+  return HB_OK;
+}
+
+int hb_w8a8_linear_noalloc(float *d_y, const float *d_x, const void *d_packed, int m, int k, int n, int epilogue,
+                           hb_stream s) {
+  if (m < 1 || k < 32 || k % 32) return hb_invalid("hb_w8a8_linear_noalloc shape");
+  const size_t need = hb_w8a8_workspace_bytes(m, k);
+  if (need > (size_t)HB_W8A8_STATIC_SCRATCH_BYTES)
+    return hb_invalid("hb_w8a8_linear_noalloc: m x k needs more than the 32 MiB static workspace");
+  int dev = -1;
+  const hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return hb_fail(err, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxStaticDevices) return hb_invalid("hb_w8a8_linear_noalloc device");
+  void *ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (ptr == nullptr) {  // first call on a device that hb_init did not set up
+    const int rc = hb_w8a8_static_setup(dev);
+    if (rc != HB_OK) return rc;
+    ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  }
+  return hb_w8a8_linear(d_y, d_x, d_packed, m, k, n, epilogue, ptr, HB_W8A8_STATIC_SCRATCH_BYTES, s);
+}
+
 int hb_w8a8_force_tile(int index) {
   if (index < -1 || index > kStreamShape) return hb_invalid("hb_w8a8_force_tile index");
   forced_tile_shape();  // settle the environment default first

@@ -69,6 +69,8 @@ _SIGNATURES = {
     "hb_w8a8_linear": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_void_p,
                                 _c_size_t, _c_void_p]),
     "hb_w8a8_planes_from_raw": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
+    "hb_w8a8_static_setup": (_c_int, [_c_int]),
+    "hb_w8a8_linear_noalloc": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_void_p]),
     "hb_w8a8_force_tile": (_c_int, [_c_int]),
     # F16
     "hb_f16_packed_bytes": (_c_size_t, [_c_int, _c_int]),

@@ -137,6 +137,23 @@ int hb_w8a8_force_tile(int index);
 int hb_w8a8_linear(float *d_y, const float *d_x, const void *d_packed, int m, int k, int n, int epilogue,
                    void *d_workspace, size_t workspace_bytes, hb_stream s);
 
+/* No counterpart in the reference: hb_w8a8_linear for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  The same computation and bits as
+ * hb_w8a8_linear, with its workspace in a library-owned static device array
+ * of HB_W8A8_STATIC_SCRATCH_BYTES (32 MiB) per GPU, held until the process
+ * ends; hb_w8a8_workspace_bytes(m, k) must not exceed it (e.g. 4096 x 6144
+ * fits, 4096 x 8192 does not), else HB_E_INVAL.  Allocates nothing: no
+ * hipMalloc, no allocating library call.  Every call on one GPU shares that
+ * GPU's array, so calls that overlap on one GPU (other streams, other
+ * threads) race; calls in one stream are ordered.  hb_init(device) prepares
+ * the device's array (hb_w8a8_static_setup); a first call on a device that
+ * was not initialised prepares it then. */
+#define HB_W8A8_STATIC_SCRATCH_BYTES (32u << 20)
+int hb_w8a8_static_setup(int device); /* with `device` current */
+int hb_w8a8_linear_noalloc(float *d_y, const float *d_x, const void *d_packed, int m, int k, int n, int epilogue,
+                           hb_stream s);
+
 /* CPU-control variant: raw accumulator byte planes in the reference's export
  * format (reference linear_w8a8.c:209-227) written over the f32 output tensor. */
 int hb_w8a8_planes_from_raw(uint8_t *d_out, const int32_t *d_raw, int m, int n, hb_stream s);
