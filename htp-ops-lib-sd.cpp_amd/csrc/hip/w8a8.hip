@@ -558,6 +558,11 @@ __global__ __launch_bounds__(64 * (WM * WN + ND), 1) void w8a8_gemm_stream(void 
   constexpr int PBUF = 2 * kFragBytes;
   // per compute wave: 8 rows of 32 output values, rows padded by 16 bytes
   constexpr int TROW = 32 * 4 + 16, TBUF = 8 * TROW;
+#ifndef HB_STREAM_SPLIT
+#define HB_STREAM_SPLIT 2
+#endif
+  // row blocks of a step multiplied before the step's barrier
+  constexpr int SPLIT = HB_STREAM_SPLIT < FM ? HB_STREAM_SPLIT : FM;
   static_assert(FN % 2 == 0, "column blocks in pairs (32 columns, one 128-byte line)");
   using Dma = StreamDma<BM, BN, ND, SCALES, EPI>;
   __shared__ __attribute__((aligned(1024))) int8_t lds[S * STAGE + 2 * PBUF + NW * TBUF];
@@ -632,11 +637,19 @@ __global__ __launch_bounds__(64 * (WM * WN + ND), 1) void w8a8_gemm_stream(void 
   int r = 0, kt = 0, rd_slot = 1 % S;  // tile and k-step of the step; slot of the next fragments
 
   // One step g with fragments fa[P]/fb[P]; the next step's go to fa[1-P]/fb[1-P].
+#define STREAM_MFMA(P, I0, I1)                                                                               \
+  _Pragma("unroll") for (int i = (I0); i < (I1); ++i) _Pragma("unroll") for (int j = 0; j < FN; ++j) acc[i][j] = \
+      __builtin_amdgcn_mfma_i32_16x16x64_i8(fb[P][j], fa[P][i], acc[i][j], 0, 0, 0);
 #define STREAM_STEP(P)                                                                                       \
   {                                                                                                          \
-    const int gg = g + (P);                                                                                  \
+                                                                                                             \
+    STREAM_MFMA(P, 0, SPLIT)                                                                                 \
+    __builtin_amdgcn_sched_barrier(0);                                                                       \
     block_barrier();                                                                                         \
-    if (gg + 1 < steps) {                                                                                    \
+    __builtin_amdgcn_sched_barrier(0);                                                                       \
+    {                                                                                                        \
+      /* unconditional (after the last step it reads a stale slot, unused): a branch here */                 \
+      /* would make the compiler wait for these reads before the MFMAs below */                              \
       const int8_t *base = lds + rd_slot * STAGE;                                                            \
       if (++rd_slot == S) rd_slot = 0;                                                                       \
       _Pragma("unroll") for (int i = 0; i < FM; ++i) fa[1 - (P)][i] =                                        \
@@ -644,8 +657,9 @@ __global__ __launch_bounds__(64 * (WM * WN + ND), 1) void w8a8_gemm_stream(void 
       _Pragma("unroll") for (int j = 0; j < FN; ++j) fb[1 - (P)][j] =                                        \
           *(const hb_i32x4 *)(base + boff + j * kFragBytes);                                                 \
     }                                                                                                        \
-    _Pragma("unroll") for (int i = 0; i < FM; ++i) _Pragma("unroll") for (int j = 0; j < FN; ++j) acc[i][j] =  \
-        __builtin_amdgcn_mfma_i32_16x16x64_i8(fb[P][j], fa[P][i], acc[i][j], 0, 0, 0);                     \
+    __builtin_amdgcn_sched_barrier(0);                                                                       \
+    STREAM_MFMA(P, SPLIT, FM)                                                                                \
+    __builtin_amdgcn_sched_barrier(0);                                                                       \
     if (++kt == ktc) {                                                                                       \
       /* epilogue of tile r: parameters from LDS (they arrived with its first stage) */                      \
       int tm, tn;                                                                                            \
@@ -696,6 +710,7 @@ __global__ __launch_bounds__(64 * (WM * WN + ND), 1) void w8a8_gemm_stream(void 
     if (g + 1 < steps) STREAM_STEP(1)
   }
 #undef STREAM_STEP
+#undef STREAM_MFMA
 }
 
 // ---------------------------------------------------------------------------
