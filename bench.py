@@ -46,7 +46,7 @@ PEAK_INT8_TOPS = 5000.0   # MI355X dense INT8 MFMA
 PEAK_HBM_GBPS = 8000.0    # MI355X HBM3E
 HEADLINE = (4096, 1536, 6144)
 SETTLE_MS = 80.0          # untimed GPU time before each timed sequence (clock ramp)
-TRAFFIC_FILE = os.path.join(REPO, "profiles", "w8a8_gemm_tiles_4096x1536x6144_traffic.md")
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "w8a8_gemm_stream_4096x1536x6144_traffic.md")
 COPY_PROBE_BYTES = 256 << 20
 CHUNKS = 20               # timed steps are split into this many event-bracketed chunks (median reported)
 USE_GRAPHS = True         # --no-graph: no graph capture or replay anywhere (for traced runs)
@@ -276,6 +276,65 @@ def e2e_opcode15(m, k, n, reps=10):
         out[where] = {"ms_median": round(statistics.median(times) * 1e3, 4), "elapsed_us_field": elapsed_us}
         for b in bufs:
             b.free()
+    return out
+
+
+def e2e_mailbox(cases, reps=20):
+    """Opcode 15 through the message channel, as sd.cpp drives it: the request
+    is written into the channel buffer, the state word's v0 is raised, and the
+    caller spins until the executor's polling thread publishes v1 (after the
+    request's kernels have completed).  One single-request message per rep on
+    rpcmem buffers in HBM; the median over `reps` after 3 untimed reps."""
+    lib = hip.lib()
+    if lib.open_dsp_session(3, 1) != 0:
+        raise RuntimeError("open_dsp_session failed: " + hip.last_error())
+    lib.init_htp_backend()
+    cap = 4096
+    chan = hip.RpcBuffer(cap)
+    if lib.create_htp_message_channel(chan.fd, cap) != 0:
+        raise RuntimeError("create_htp_message_channel failed: " + hip.last_error())
+    view = chan.host_view()
+    rng = np.random.default_rng(98)
+    out = {}
+    try:
+        for name, (m, k, n) in cases.items():
+            x = rng.standard_normal((m, k), dtype=np.float32)
+            w = rng.integers(-127, 128, (n, k), dtype=np.int8)
+            blob = hip.pack_constants(w, rng.uniform(1e-4, 1e-3, n).astype(np.float32))
+            bufs = [hip.RpcBuffer(m * n * 4, device=True), hip.RpcBuffer(m * k * 4, device=True),
+                    hip.RpcBuffer(blob.nbytes, device=True)]
+            bufs[1].write(x)
+            bufs[2].write(blob)
+            req = hip.compute_request(hip.OP_MAT_MUL_NATIVE_W8A8,
+                                      hip.w8a8_params((bufs[0].fd, 0), (bufs[1].fd, 0), (bufs[2].fd, 0), m, k, n))
+            msg, offs = hip.build_message([(hip.REQUEST_TYPE_OP_COMPUTE, req)], cap)
+            body = np.frombuffer(bytes(msg[8:offs[-1]]), np.uint8)
+            times = []
+            for i in range(reps + 3):
+                view[8:offs[-1]] = body
+                view[:8] = 0
+                t0 = time.perf_counter()
+                view[0] = 1
+                deadline = t0 + 10.0
+                while view[1] != 1:
+                    if time.perf_counter() > deadline:
+                        raise RuntimeError(f"mailbox request {name} did not complete")
+                t1 = time.perf_counter()
+                if i >= 3:
+                    times.append(t1 - t0)
+            done = bytes(view[:offs[-1]].tobytes())
+            state = hip.request_state(done, offs, 0)
+            if state != 0:
+                raise RuntimeError(f"mailbox request {name} returned {state}")
+            elapsed_us = int.from_bytes(hip.request_data(done, offs, 0)[4 + 36:4 + 40], "little", signed=True)
+            out[name] = {"shape": f"M={m} K={k} N={n}", "us_median": round(statistics.median(times) * 1e6, 1),
+                         "us_min": round(min(times) * 1e6, 1), "elapsed_us_field": elapsed_us, "reps": reps}
+            for b in bufs:
+                b.free()
+    finally:
+        lib.destroy_htp_message_channel()
+        lib.close_dsp_session()
+        chan.free()
     return out
 
 
@@ -586,12 +645,14 @@ def f16_mlp_case(steps, warmup, m=77, k=768, n=3072, rotate=6):
     return out
 
 
-def traffic_probe(steps=12):
+def traffic_probe(steps=12, configs=False):
     """Workload of the counter passes (FETCH_SIZE, WRITE_SIZE, MFMA busy
     cycles): a plain elementwise copy of COPY_PROBE_BYTES (torch's unary
     kernel, reads and writes each byte once) for calibration, then the
     headline opcode-15 steps and the M=1 decode calls on rotated sets, without
-    the clock-settling runs (every dispatch is serialized under counters)."""
+    the clock-settling runs (every dispatch is serialized under counters).
+    With configs: then the C3 chain's three layers, the C4 QKV and O layers,
+    C5's M=1 down projection and the C2 F16 text MLP, `steps` calls each."""
     import torch
 
     src = torch.empty(COPY_PROBE_BYTES // 4, dtype=torch.float32, device="cuda:0").normal_()
@@ -606,7 +667,22 @@ def traffic_probe(steps=12):
     r = run_w8a8(m, k, n, steps, 2, 6, outliers=0.01, settle_ms=0.0)
     del r
     r = run_w8a8(1, 4096, 14336, steps, 2, 6, scale=(5e-5, 5e-4), settle_ms=0.0)
-    print(f"counter probe done: decode {r['ms_per_step'] * 1e3:.2f} us", flush=True)
+    print(f"counter probe: decode {r['ms_per_step'] * 1e3:.2f} us", flush=True)
+    if configs:
+        for name, (m, k, n, outl, sc, epi) in {
+                "C3 qkv": (4096, 1536, 4608, 0.01, (1e-4, 1e-3), None),
+                "C3 up gelu": (4096, 1536, 6144, 0.01, (1e-4, 1e-3), hip.EPI_SCALE_GELU),
+                "C3 down": (4096, 6144, 1536, 0.01, (1e-4, 1e-3), None),
+                "C4 qkv": (2048, 4096, 6144, 0.0, (5e-5, 5e-4), None),
+                "C4 o": (2048, 4096, 4096, 0.0, (5e-5, 5e-4), None),
+                "C5 M=1 down": (1, 14336, 4096, 0.0, (5e-5, 5e-4), None)}.items():
+            r = run_w8a8(m, k, n, steps, 2, 4, outliers=outl, scale=sc, settle_ms=0.0, epilogue=epi)
+            print(f"counter probe: {name} ({hip.w8a8_gemm_kernel(m, k, n)}) {r['ms_per_step'] * 1e3:.2f} us",
+                  flush=True)
+            del r
+        r = f16_mlp_case(steps, 2)
+        print(f"counter probe: C2 f16 text MLP {r}", flush=True)
+    print("counter probe done", flush=True)
 
 
 def _short(name):
@@ -656,6 +732,8 @@ def main():
     ap.add_argument("--no-graph", action="store_true",
                     help="no HIP graph capture or replay (every timing stream-ordered); for profiler-traced runs")
     ap.add_argument("--traffic-probe", action="store_true")
+    ap.add_argument("--probe-configs", action="store_true",
+                    help="with --traffic-probe: also the C3/C4 layers, C5 M=1 down and the C2 F16 MLP")
     ap.add_argument("--profile-summary", metavar="DIR")
     args = ap.parse_args()
     if args.profile_summary:
@@ -669,7 +747,7 @@ def main():
     global USE_GRAPHS
     USE_GRAPHS = not args.no_graph
     if args.traffic_probe:
-        traffic_probe()
+        traffic_probe(configs=args.probe_configs)
         return
 
     hip.init(0)
@@ -714,7 +792,7 @@ def main():
                   ("" if r["graph_ms_per_step"] is None else
                    f"; graph replay of the same steps: {r['graph_ms_per_step'] * 1e3:.3f} us/step, "
                    f"GEMM {r['graph_gemm_ms_mean'] * 1e3:.3f} us"),
-        "roofline": {"kernel": "w8a8_gemm_tiles", "bound": "mfma", "achieved": round(gemm_tops, 2),
+        "roofline": {"kernel": hip.w8a8_gemm_kernel(m, k, n), "bound": "mfma", "achieved": round(gemm_tops, 2),
                      "peak": PEAK_INT8_TOPS, "unit": "TOPS", "frac": round(gemm_tops / PEAK_INT8_TOPS, 4),
                      "traffic": read_traffic(), "gemm_us": round(r["gemm_ms_mean"] * 1e3, 3),
                      "gemm_gbps": round(gemm_bytes(m, k, n) / (r["gemm_ms_mean"] * 1e-3) / 1e9, 1),
@@ -727,6 +805,9 @@ def main():
     line["decode_m1"] = decode_case(1, 4096, 14336, args.steps, args.warmup, 6)
     progress(f"decode M=1 {line['decode_m1']['us_per_call']} us")
     line["e2e_opcode15"] = e2e_opcode15(m, k, n)
+    line["e2e_mailbox"] = e2e_mailbox({"headline": (m, k, n), "decode_m1": (1, 4096, 14336)})
+    progress(f"mailbox e2e {line['e2e_mailbox']['headline']['us_median']} us / "
+             f"{line['e2e_mailbox']['decode_m1']['us_median']} us")
     if args.config == "all":
         line["configs"] = all_configs(args.steps, args.warmup, with_cpu=not args.no_cpu)
     if not args.no_cpu and rank == 0:

@@ -1730,6 +1730,14 @@ int hb_w8a8_gemm(void *d_y, int ldy, const int8_t *d_q, const float *d_scales, c
   }
 }
 
+int hb_w8a8_gemm_choice(int m, int k, int n) {
+  if (m < 1 || k < 32 || k % 32 || n < 16 || n % 16) return hb_invalid("hb_w8a8_gemm_choice shape");
+  if (m <= 16) return HB_W8A8_CHOICE_DECODE;
+  const int rtiles = (m + 15) / 16;
+  if (rtiles <= 5 && 4LL * ((m + 63) / 64) * (n / 64) <= compute_units()) return HB_W8A8_CHOICE_DECODE_TILES;
+  return pick_tile_shape(m, n, (int)kp_of(k));
+}
+
 int hb_w8a8_linear(float *d_y, const float *d_x, const void *d_packed, int m, int k, int n, int epilogue,
                    void *d_workspace, size_t workspace_bytes, hb_stream s) {
   if (!d_workspace || workspace_bytes < hb_w8a8_workspace_bytes(m, k))

@@ -72,6 +72,7 @@ _SIGNATURES = {
     "hb_w8a8_static_setup": (_c_int, [_c_int]),
     "hb_w8a8_linear_noalloc": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_void_p]),
     "hb_w8a8_force_tile": (_c_int, [_c_int]),
+    "hb_w8a8_gemm_choice": (_c_int, [_c_int, _c_int, _c_int]),
     # F16
     "hb_f16_packed_bytes": (_c_size_t, [_c_int, _c_int]),
     "hb_qk0_block_bytes": (_c_size_t, [_c_int]),
@@ -325,6 +326,23 @@ def w8a8_force_tile(index):
     if prev < -1:
         check(prev, "hb_w8a8_force_tile")
     return prev
+
+
+W8A8_CHOICE_DECODE, W8A8_CHOICE_DECODE_TILES, W8A8_STREAM_TILE = -1, -2, 5
+
+
+def w8a8_gemm_kernel(m, k, n):
+    """Name of the kernel hb_w8a8_gemm runs for this shape."""
+    choice = lib().hb_w8a8_gemm_choice(m, k, n)
+    if choice == W8A8_CHOICE_DECODE:
+        return "w8a8_gemm_decode (weight streaming)"
+    if choice == W8A8_CHOICE_DECODE_TILES:
+        return "w8a8_gemm_decode<16,8> (per 16-row tile)"
+    if choice == W8A8_STREAM_TILE:
+        return "w8a8_gemm_stream"
+    check(choice, "hb_w8a8_gemm_choice")
+    bm, bn = W8A8_TILE_SHAPES[choice]
+    return f"w8a8_gemm_tiles<{bm},{bn}>"
 
 
 def w8a8_planes_from_raw(out_dev, raw_dev, m, n):

@@ -128,6 +128,17 @@ int hb_w8a8_gemm(void *d_y, int ldy, const int8_t *d_q, const float *d_scales, c
  * The environment variable HTP_OPS_AMD_W8A8_TILE gives the initial value. */
 int hb_w8a8_force_tile(int index);
 
+/* Which kernel hb_w8a8_gemm runs for this shape (after hb_w8a8_force_tile and
+ * the environment): HB_W8A8_CHOICE_DECODE (m <= 16, weight-streaming decode
+ * kernel), HB_W8A8_CHOICE_DECODE_TILES (17-80 rows over few output tiles: the
+ * decode kernel per 16-row tile), or the tile index as hb_w8a8_force_tile
+ * numbers them (5: the persistent streaming kernel); HB_E_INVAL on an
+ * invalid shape.  A measurement and test hook; no counterpart in the
+ * reference. */
+#define HB_W8A8_CHOICE_DECODE (-1)
+#define HB_W8A8_CHOICE_DECODE_TILES (-2)
+int hb_w8a8_gemm_choice(int m, int k, int n);
+
 /* Full opcode-15 computation: quantize + GEMM + epilogue (workspace from hb_w8a8_workspace_bytes).
  * With the SCALE or SCALE_GELU epilogue, 16-byte aligned x and y and K a
  * multiple of 32, small problems run as one launch that quantizes its own

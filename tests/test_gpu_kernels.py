@@ -225,6 +225,26 @@ def test_w8a8_stream_kernel_row_stride(hip, orc):
     assert (got[:, n:] == 0xA5A5A5A5).all()
 
 
+def test_w8a8_gemm_choice_names_the_kernel(hip):
+    """hb_w8a8_gemm_choice reports the path hb_w8a8_gemm takes: the decode
+    kernel up to 16 rows, the per-row-tile decode kernel for few output
+    tiles, the streaming kernel at the headline (768 tiles, 3 per CU), a
+    pinned tile shape, and HB_E_INVAL for a bad shape."""
+    lib = hip.lib()
+    assert lib.hb_w8a8_gemm_choice(1, 4096, 14336) == hip.W8A8_CHOICE_DECODE
+    assert lib.hb_w8a8_gemm_choice(16, 14336, 4096) == hip.W8A8_CHOICE_DECODE
+    assert lib.hb_w8a8_gemm_choice(32, 4096, 4096) == hip.W8A8_CHOICE_DECODE_TILES
+    assert lib.hb_w8a8_gemm_choice(4096, 1536, 6144) == hip.W8A8_STREAM_TILE
+    assert hip.w8a8_gemm_kernel(4096, 1536, 6144) == "w8a8_gemm_stream"
+    prev = hip.w8a8_force_tile(0)
+    try:
+        assert lib.hb_w8a8_gemm_choice(4096, 1536, 6144) == 0
+        assert hip.w8a8_gemm_kernel(4096, 1536, 6144) == "w8a8_gemm_tiles<128,192>"
+    finally:
+        hip.w8a8_force_tile(prev)
+    assert lib.hb_w8a8_gemm_choice(0, 1536, 6144) == -22
+
+
 # One row: hb_w8a8_linear quantizes inside the weight-streaming kernel
 # (one variant per kp range: <= 4096, <= 8192, <= 16384; for kp <= 4096 and
 # at least one block per CU, two column blocks per workgroup).
