@@ -362,7 +362,11 @@ def decode_case(m, k, n, steps, warmup, rotate):
             "graph_us_per_call": None if r["graph_ms_per_step"] is None else round(r["graph_ms_per_step"] * 1e3, 3)}
 
 
-def all_configs(steps, warmup, with_cpu=False):
+def all_configs(steps, warmup, with_cpu=False, only=None):
+    """Every BASELINE configuration; `only`: a set of case names to run alone."""
+    def wanted(name):
+        return only is None or name in only
+
     out = {}
     for name, (m, k, n, outl, sc) in {
             "C1_77x768x3072": (77, 768, 3072, 0.0, (1e-4, 1e-3)),
@@ -371,6 +375,8 @@ def all_configs(steps, warmup, with_cpu=False):
             "C3_down_4096x6144x1536": (4096, 6144, 1536, 0.01, (1e-4, 1e-3)),
             "C4_qkv_2048x4096x6144": (2048, 4096, 6144, 0.0, (5e-5, 5e-4)),
             "C4_o_2048x4096x4096": (2048, 4096, 4096, 0.0, (5e-5, 5e-4))}.items():
+        if not wanted(name):
+            continue
         progress(f"start {name}")
         r = run_w8a8(m, k, n, steps, warmup, 4, outliers=outl, scale=sc,
                      epilogue=hip.EPI_SCALE_GELU if "gelu" in name else None)
@@ -381,15 +387,20 @@ def all_configs(steps, warmup, with_cpu=False):
         progress(f"done {name}: {out[name]['us']} us")
     for m in (1, 4, 16):
         for k, n in ((4096, 14336), (14336, 4096)):
+            if not wanted(f"C5_M{m}_{k}x{n}"):
+                continue
             progress(f"start C5 M={m} {k}x{n}")
             out[f"C5_M{m}_{k}x{n}"] = decode_case(m, k, n, steps, warmup, 6)
             progress(f"done C5 M={m} {k}x{n}: {out[f'C5_M{m}_{k}x{n}']['us_per_call']} us")
-    progress("start C2")
-    out["C2_f16_text_mlp_77x768x3072x768"] = f16_mlp_case(steps, warmup)
-    progress("start opcode 19")
-    out["opcode19_aux"] = aux_cases(steps, warmup, with_cpu=with_cpu)
-    progress("start opcodes 2/3/4")
-    out["opcodes_2_3_4_qk0"] = qk0_cases(steps, warmup)
+    if wanted("C2_f16_text_mlp_77x768x3072x768"):
+        progress("start C2")
+        out["C2_f16_text_mlp_77x768x3072x768"] = f16_mlp_case(steps, warmup)
+    if wanted("opcode19_aux"):
+        progress("start opcode 19")
+        out["opcode19_aux"] = aux_cases(steps, warmup, with_cpu=with_cpu)
+    if wanted("opcodes_2_3_4_qk0"):
+        progress("start opcodes 2/3/4")
+        out["opcodes_2_3_4_qk0"] = qk0_cases(steps, warmup)
     progress("done all configs")
     return out
 
@@ -645,14 +656,17 @@ def f16_mlp_case(steps, warmup, m=77, k=768, n=3072, rotate=6):
     return out
 
 
-def traffic_probe(steps=12, configs=False):
+def traffic_probe(steps=12, configs=False, only=None):
     """Workload of the counter passes (FETCH_SIZE, WRITE_SIZE, MFMA busy
     cycles): a plain elementwise copy of COPY_PROBE_BYTES (torch's unary
     kernel, reads and writes each byte once) for calibration, then the
     headline opcode-15 steps and the M=1 decode calls on rotated sets, without
     the clock-settling runs (every dispatch is serialized under counters).
     With configs: then the C3 chain's three layers, the C4 QKV and O layers,
-    C5's M=1 down projection and the C2 F16 text MLP, `steps` calls each."""
+    C5's M=1 down projection, the C2 F16 text MLP and the F16 MLP at DiT size
+    (4096x1536x6144, the ring kernel), `steps` calls each;
+    `only`: a set of those case names (the headline and decode runs are then
+    skipped too)."""
     import torch
 
     src = torch.empty(COPY_PROBE_BYTES // 4, dtype=torch.float32, device="cuda:0").normal_()
@@ -663,25 +677,33 @@ def traffic_probe(steps=12, configs=False):
     del src, dst
     torch.cuda.empty_cache()
     hip.init(0)
-    m, k, n = HEADLINE
-    r = run_w8a8(m, k, n, steps, 2, 6, outliers=0.01, settle_ms=0.0)
-    del r
-    r = run_w8a8(1, 4096, 14336, steps, 2, 6, scale=(5e-5, 5e-4), settle_ms=0.0)
-    print(f"counter probe: decode {r['ms_per_step'] * 1e3:.2f} us", flush=True)
-    if configs:
+    if only is None:
+        m, k, n = HEADLINE
+        r = run_w8a8(m, k, n, steps, 2, 6, outliers=0.01, settle_ms=0.0)
+        del r
+        r = run_w8a8(1, 4096, 14336, steps, 2, 6, scale=(5e-5, 5e-4), settle_ms=0.0)
+        print(f"counter probe: decode {r['ms_per_step'] * 1e3:.2f} us", flush=True)
+    if configs or only is not None:
         for name, (m, k, n, outl, sc, epi) in {
-                "C3 qkv": (4096, 1536, 4608, 0.01, (1e-4, 1e-3), None),
-                "C3 up gelu": (4096, 1536, 6144, 0.01, (1e-4, 1e-3), hip.EPI_SCALE_GELU),
-                "C3 down": (4096, 6144, 1536, 0.01, (1e-4, 1e-3), None),
-                "C4 qkv": (2048, 4096, 6144, 0.0, (5e-5, 5e-4), None),
-                "C4 o": (2048, 4096, 4096, 0.0, (5e-5, 5e-4), None),
-                "C5 M=1 down": (1, 14336, 4096, 0.0, (5e-5, 5e-4), None)}.items():
+                "C3_qkv_4096x1536x4608": (4096, 1536, 4608, 0.01, (1e-4, 1e-3), None),
+                "C3_up_gelu_4096x1536x6144": (4096, 1536, 6144, 0.01, (1e-4, 1e-3), hip.EPI_SCALE_GELU),
+                "C3_down_4096x6144x1536": (4096, 6144, 1536, 0.01, (1e-4, 1e-3), None),
+                "C4_qkv_2048x4096x6144": (2048, 4096, 6144, 0.0, (5e-5, 5e-4), None),
+                "C4_o_2048x4096x4096": (2048, 4096, 4096, 0.0, (5e-5, 5e-4), None),
+                "C5_M1_14336x4096": (1, 14336, 4096, 0.0, (5e-5, 5e-4), None)}.items():
+            if only is not None and name not in only:
+                continue
             r = run_w8a8(m, k, n, steps, 2, 4, outliers=outl, scale=sc, settle_ms=0.0, epilogue=epi)
             print(f"counter probe: {name} ({hip.w8a8_gemm_kernel(m, k, n)}) {r['ms_per_step'] * 1e3:.2f} us",
                   flush=True)
             del r
-        r = f16_mlp_case(steps, 2)
-        print(f"counter probe: C2 f16 text MLP {r}", flush=True)
+        if only is None or "C2_f16_text_mlp_77x768x3072x768" in only:
+            r = f16_mlp_case(steps, 2)
+            print(f"counter probe: C2 f16 text MLP {r}", flush=True)
+        if only is None or "F16_mlp_4096x1536x6144" in only:
+            # the F16 driver at DiT MLP size: the ring kernel (f16_gemm_ring)
+            r = f16_mlp_case(steps, 2, m=4096, k=1536, n=6144, rotate=2)
+            print(f"counter probe: F16 MLP 4096x1536x6144 {r}", flush=True)
     print("counter probe done", flush=True)
 
 
@@ -691,7 +713,9 @@ def _short(name):
 
 
 def profile_summary(directory):
-    """Markdown summary of the rocprofv3 CSV files under directory."""
+    """Markdown summary of the rocprofv3 CSV files under directory: kernel
+    stats, per-dispatch durations grouped by kernel and grid (one group per
+    shape a kernel ran at), and counters grouped the same way."""
     lines = []
     for path in sorted(glob.glob(os.path.join(directory, "**", "*kernel_stats.csv"), recursive=True)):
         lines.append(f"### kernel stats ({os.path.relpath(path, directory)})\n")
@@ -703,18 +727,31 @@ def profile_summary(directory):
                              f"{float(row['MinNs']) / 1e3:.3f} | {float(row['MaxNs']) / 1e3:.3f} | "
                              f"{float(row['Percentage']):.2f} |")
         lines.append("")
+    for path in sorted(glob.glob(os.path.join(directory, "**", "*kernel_trace.csv"), recursive=True)):
+        groups = {}
+        with open(path) as f:
+            for row in csv.DictReader(f):
+                key = (_short(row["Kernel_Name"]), int(row["Grid_Size_X"]), int(row["Workgroup_Size_X"]))
+                groups.setdefault(key, []).append((int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) / 1e3)
+        lines.append(f"### dispatches by kernel and grid ({os.path.relpath(path, directory)})\n")
+        lines.append("| kernel | grid (threads) | workgroup | calls | mean us | median us |")
+        lines.append("|---|---|---|---|---|---|")
+        for (kernel, grid, wg), durs in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+            lines.append(f"| `{kernel}` | {grid} | {wg} | {len(durs)} | {statistics.fmean(durs):.3f} | "
+                         f"{statistics.median(durs):.3f} |")
+        lines.append("")
     counters = {}
     for path in sorted(glob.glob(os.path.join(directory, "**", "*counter_collection.csv"), recursive=True)):
         with open(path) as f:
             for row in csv.DictReader(f):
-                key = (_short(row["Kernel_Name"]), row["Counter_Name"])
+                key = (_short(row["Kernel_Name"]), int(row["Grid_Size"]), row["Counter_Name"])
                 counters.setdefault(key, []).append(float(row["Counter_Value"]))
     if counters:
-        lines.append("### counters, mean per dispatch\n")
-        lines.append("| kernel | counter | mean | dispatches |")
-        lines.append("|---|---|---|---|")
-        for (kernel, counter), vals in sorted(counters.items()):
-            lines.append(f"| `{kernel}` | {counter} | {statistics.fmean(vals):.1f} | {len(vals)} |")
+        lines.append("### counters, mean per dispatch, by kernel and grid\n")
+        lines.append("| kernel | grid (threads) | counter | mean | dispatches |")
+        lines.append("|---|---|---|---|---|")
+        for (kernel, grid, counter), vals in sorted(counters.items()):
+            lines.append(f"| `{kernel}` | {grid} | {counter} | {statistics.fmean(vals):.1f} | {len(vals)} |")
         lines.append("")
     print("\n".join(lines))
 
@@ -734,6 +771,10 @@ def main():
     ap.add_argument("--traffic-probe", action="store_true")
     ap.add_argument("--probe-configs", action="store_true",
                     help="with --traffic-probe: also the C3/C4 layers, C5 M=1 down and the C2 F16 MLP")
+    ap.add_argument("--only", metavar="NAMES",
+                    help="comma-separated case names: with --config all, run and print only those cases (e.g. "
+                         "C3_qkv_4096x1536x4608,C5_M4_14336x4096); with --traffic-probe, only those probe cases "
+                         "(the same names)")
     ap.add_argument("--profile-summary", metavar="DIR")
     args = ap.parse_args()
     if args.profile_summary:
@@ -747,7 +788,7 @@ def main():
     global USE_GRAPHS
     USE_GRAPHS = not args.no_graph
     if args.traffic_probe:
-        traffic_probe(configs=args.probe_configs)
+        traffic_probe(configs=args.probe_configs, only=None if not args.only else set(args.only.split(",")))
         return
 
     hip.init(0)
@@ -761,6 +802,10 @@ def main():
         return
     if args.config == "qk0":
         print(json.dumps({"opcodes_2_3_4_qk0": qk0_cases(args.steps, args.warmup)}), flush=True)
+        return
+    if args.config == "all" and args.only:
+        print(json.dumps({"configs": all_configs(args.steps, args.warmup, with_cpu=not args.no_cpu,
+                                                 only=set(args.only.split(",")))}), flush=True)
         return
     m, k, n = HEADLINE
     r = run_w8a8(m, k, n, args.steps, args.warmup, args.rotate, outliers=0.01)
