@@ -276,6 +276,9 @@ __device__ inline float gelu_tanh(float z) {
   return __fmul_rn(z, sig);
 }
 
+// DPP row shifts (within 16-lane rows): lane i takes lane i - 8 / lane i + 8.
+constexpr int kDppRowShr8 = 0x118, kDppRowShl8 = 0x108;
+
 // Bits of one output element: int32 raw accumulator, or the scaled f32.
 template <int EPI>
 __device__ inline uint32_t epilogue_bits(int32_t acc, int32_t corr, float sw, float s) {
@@ -447,12 +450,15 @@ __global__ __launch_bounds__(64 * WM *WN) void w8a8_gemm_tiles(void *__restrict_
 //  - WM x WN compute waves never load from global memory.  Each step they
 //    read the next step's fragments from LDS while the current step's MFMAs
 //    run.  Operands are swapped in the MFMA (weights as src0), so a lane holds
-//    4 consecutive output columns of one row.  At a tile's end they apply the
-//    epilogue in registers, regroup each 8-row x 32-column piece through a
-//    wave-private LDS buffer so that one store writes 8 whole 128-byte lines,
-//    and store without waiting: the stores drain during the next tile's main
-//    loop.  The stores are non-temporal, so the output does not evict the
-//    operands the other CUs of the XCD still read from L2.
+//    4 consecutive output columns of one row.  Accumulators start at the
+//    tile's column corrections.  At a tile's end the compute waves scale in
+//    registers and store straight from the MFMA layout (16 rows x 64 bytes per
+//    store; the two stores of a 32-column pair fill whole 128-byte lines),
+//    without waiting: the stores drain during the next tile's main loop.  The
+//    epilogue is VALU and LDS work on the waves that issue the MFMAs, so it
+//    reads each parameter once (no LDS regroup, no per-piece re-reads).  The
+//    stores are non-temporal, so the output does not evict the operands the
+//    other CUs of the XCD still read from L2.
 //  - The epilogue parameters of a tile (corr and sw of its BN columns, the row
 //    scales of its BM rows) arrive in LDS by DMA with the tile's first k-step,
 //    double-buffered by tile parity: DMA wave 0 loads corr and sw (16 bytes per
@@ -556,8 +562,6 @@ __global__ __launch_bounds__(64 * (WM * WN + ND), 1) void w8a8_gemm_stream(void 
   static_assert(BN * 8 == kFragBytes && BM * 4 == kFragBytes, "parameter blocks of one kilobyte");
   constexpr bool SCALES = EPI != HB_W8A8_EPI_RAW;
   constexpr int PBUF = 2 * kFragBytes;
-  // per compute wave: 8 rows of 32 output values, rows padded by 16 bytes
-  constexpr int TROW = 32 * 4 + 16, TBUF = 8 * TROW;
 #ifndef HB_STREAM_SPLIT
 #define HB_STREAM_SPLIT 2
 #endif
@@ -565,7 +569,7 @@ __global__ __launch_bounds__(64 * (WM * WN + ND), 1) void w8a8_gemm_stream(void 
   constexpr int SPLIT = HB_STREAM_SPLIT < FM ? HB_STREAM_SPLIT : FM;
   static_assert(FN % 2 == 0, "column blocks in pairs (32 columns, one 128-byte line)");
   using Dma = StreamDma<BM, BN, ND, SCALES, EPI>;
-  __shared__ __attribute__((aligned(1024))) int8_t lds[S * STAGE + 2 * PBUF + NW * TBUF];
+  __shared__ __attribute__((aligned(1024))) int8_t lds[S * STAGE + 2 * PBUF];
   int8_t *params = lds + S * STAGE;
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -617,19 +621,22 @@ __global__ __launch_bounds__(64 * (WM * WN + ND), 1) void w8a8_gemm_stream(void 
 
   // ------------------------------- compute wave -------------------------------
   const int wm = wave / WN, wn = wave % WN;
+  // A lane of the MFMA layout holds output row lane%16 and columns
+  // 4*(lane/16)..+3 of each 16x16 block.  The accumulators of a tile start at
+  // its column corrections (corr), so the epilogue has no correction to add
+  // (32-bit wrapping sums: the same bits as adding it at the end).
   hb_i32x4 acc[FM][FN];
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j) acc[i][j] = hb_i32x4{0, 0, 0, 0};
   hb_i32x4 fa[2][FM], fb[2][FN];
   const int aoff = (wm * FM) * kFragBytes + lane * 16, boff = (ABLK + wn * FN) * kFragBytes + lane * 16;
-  int8_t *tb = params + 2 * PBUF + wave * TBUF;
-  // regrouping: a lane of the MFMA layout holds row lane%16, columns 4*(lane/16)..+3
-  // of a 16x16 block; it writes them at row lane%8 of the 8-row piece, and reads back
-  // row lane/8, columns 4*(lane%8)..+3 of the 32-column pair
-  const int tw = (lane & 7) * TROW + (lane >> 4) * 16, tr = (lane >> 3) * TROW + (lane & 7) * 16;
-  block_barrier();  // stage 0 published
+  const int lcol = wn * WTN + 4 * (lane >> 4);  // tile column of this lane in block 0
+  const int scol = 16 * ((lane >> 3) & 1) + 4 * (lane >> 4);  // column in a 32-column pair after the DPP trade
+  block_barrier();  // stage 0 (and tile 0's parameters) published
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const hb_i32x4 cc = *(const hb_i32x4 *)(params + (lcol + j * 16) * 4);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) acc[i][j] = cc;
+  }
 #pragma unroll
   for (int i = 0; i < FM; ++i) fa[0][i] = *(const hb_i32x4 *)(lds + aoff + i * kFragBytes);
 #pragma unroll
@@ -661,44 +668,47 @@ __global__ __launch_bounds__(64 * (WM * WN + ND), 1) void w8a8_gemm_stream(void 
     STREAM_MFMA(P, SPLIT, FM)                                                                                \
     __builtin_amdgcn_sched_barrier(0);                                                                       \
     if (++kt == ktc) {                                                                                       \
-      /* epilogue of tile r: parameters from LDS (they arrived with its first stage) */                      \
+      /* epilogue of tile r: parameters from LDS (they arrived with its first stage); each lane */            \
+      /* stores its 4 columns of a row, 16 rows x 64 bytes per store, whole 128-byte lines per */             \
+      /* column-block pair */                                                                                 \
       int tm, tn;                                                                                            \
       grouped_tile(c0 + slot + r * nslots, tiles_m, tiles_n, tm, tn);                                        \
       const int8_t *par = params + (r & 1) * PBUF;                                                           \
       const __amdgpu_buffer_rsrc_t rsrc = stream_out_rsrc(y, ldy, tm * BM, min(BM, m - tm * BM));            \
+      float sv[FM];                                                                                          \
+      _Pragma("unroll") for (int i = 0; i < FM; ++i) sv[i] =                                                 \
+          SCALES ? *(const float *)(par + kFragBytes + (wm * WTM + i * 16 + (lane & 15)) * 4) : 0.0f;        \
+      /* each 16-row x 32-column piece leaves in two stores of 8 whole 128-byte lines: the upper */         \
+      /* 8 lanes of every 16-lane row trade their block-0 values for block 1 of the lanes 8 below */        \
+      /* (DPP), so a lane then holds row lane%8 (+8 in the second store) of the piece, columns */             \
+      /* 16*(lane/8%2) + 4*(lane/16)..+3 of the pair */                                                      \
       _Pragma("unroll") for (int jp = 0; jp < FN / 2; ++jp) {                                                \
-        /* each lane stores columns col .. col+3 of rows 8h + lane/8 of the pair */                          \
-        const int col = tn * BN + wn * WTN + jp * 32 + 4 * (lane & 7);                                       \
+        const hb_f32x4 sc0 = *(const hb_f32x4 *)(par + BN * 4 + (lcol + jp * 32) * 4);                      \
+        const hb_f32x4 sc1 = *(const hb_f32x4 *)(par + BN * 4 + (lcol + jp * 32 + 16) * 4);                 \
+        const int pc = tn * BN + wn * WTN + jp * 32 + scol;                                                  \
         _Pragma("unroll") for (int i = 0; i < FM; ++i) {                                                     \
-          /* parameters re-read per piece: short live ranges (registers are tight) */                        \
-          const int c0_ = wn * WTN + jp * 32 + 4 * (lane >> 4), c1_ = c0_ + 16;                              \
-          asm volatile("" ::: "memory");                                                                     \
-          const hb_i32x4 cc0 = *(const hb_i32x4 *)(par + c0_ * 4), cc1 = *(const hb_i32x4 *)(par + c1_ * 4); \
-          const hb_f32x4 sc0 = *(const hb_f32x4 *)(par + BN * 4 + c0_ * 4);                                 \
-          const hb_f32x4 sc1 = *(const hb_f32x4 *)(par + BN * 4 + c1_ * 4);                                 \
-          const float sv =                                                                                   \
-              SCALES ? *(const float *)(par + kFragBytes + (wm * WTM + i * 16 + (lane & 15)) * 4) : 0.0f;    \
-          hb_u32x4 o0, o1;                                                                                   \
+          hb_u32x4 o0, o1, lo, hi;                                                                           \
           _Pragma("unroll") for (int e = 0; e < 4; ++e) {                                                    \
-            o0[e] = epilogue_bits<EPI>(acc[i][2 * jp][e], cc0[e], sc0[e], sv);                               \
-            o1[e] = epilogue_bits<EPI>(acc[i][2 * jp + 1][e], cc1[e], sc1[e], sv);                           \
+            o0[e] = epilogue_bits<EPI>(acc[i][2 * jp][e], 0, sc0[e], sv[i]);                                 \
+            o1[e] = epilogue_bits<EPI>(acc[i][2 * jp + 1][e], 0, sc1[e], sv[i]);                             \
           }                                                                                                  \
-          _Pragma("unroll") for (int h = 0; h < 2; ++h) {                                                    \
-            if (((lane >> 3) & 1) == h) {                                                                    \
-              *(hb_u32x4 *)(tb + tw) = o0;                                                                   \
-              *(hb_u32x4 *)(tb + tw + 64) = o1;                                                              \
-            }                                                                                                \
-            /* other lanes wrote tb: the read must not reuse this lane's earlier read (the wave's */         \
-            /* LDS operations execute in order, so no wait is needed) */                                     \
-            asm volatile("" ::: "memory");                                                                   \
-            const hb_u32x4 v = *(const hb_u32x4 *)(tb + tr);                                                 \
-            const int rl = wm * WTM + i * 16 + 8 * h + (lane >> 3);                                          \
-            const uint32_t off = col < n ? ((uint32_t)rl * (uint32_t)ldy + (uint32_t)col) * 4u : 0xfffffff0u; \
-            __builtin_amdgcn_raw_buffer_store_b128(v, rsrc, off, 0, 2);                                      \
+          _Pragma("unroll") for (int e = 0; e < 4; ++e) {                                                    \
+            lo[e] = (uint32_t)__builtin_amdgcn_update_dpp((int)o0[e], (int)o1[e], kDppRowShr8, 0xf, 0xc, false); \
+            hi[e] = (uint32_t)__builtin_amdgcn_update_dpp((int)o1[e], (int)o0[e], kDppRowShl8, 0xf, 0x3, false); \
           }                                                                                                  \
-          acc[i][2 * jp] = hb_i32x4{0, 0, 0, 0};                                                             \
-          acc[i][2 * jp + 1] = hb_i32x4{0, 0, 0, 0};                                                         \
+          const uint32_t r0 = (uint32_t)(wm * WTM + i * 16 + (lane & 7));                                    \
+          const uint32_t off0 = pc < n ? (r0 * (uint32_t)ldy + (uint32_t)pc) * 4u : 0xfffffff0u;             \
+          const uint32_t off1 = pc < n ? ((r0 + 8u) * (uint32_t)ldy + (uint32_t)pc) * 4u : 0xfffffff0u;      \
+          __builtin_amdgcn_raw_buffer_store_b128(lo, rsrc, off0, 0, 2);                                      \
+          __builtin_amdgcn_raw_buffer_store_b128(hi, rsrc, off1, 0, 2);                                      \
         }                                                                                                    \
+      }                                                                                                      \
+      /* the next tile's accumulators start at its corrections (its parameters arrived with the */           \
+      /* stage published at this step's barrier; after the last tile they are unused) */                      \
+      const int8_t *npar = params + ((r + 1) & 1) * PBUF;                                                    \
+      _Pragma("unroll") for (int j = 0; j < FN; ++j) {                                                       \
+        const hb_i32x4 cc = *(const hb_i32x4 *)(npar + (lcol + j * 16) * 4);                                 \
+        _Pragma("unroll") for (int i = 0; i < FM; ++i) acc[i][j] = cc;                                       \
       }                                                                                                      \
       kt = 0;                                                                                                \
       ++r;                                                                                                   \
