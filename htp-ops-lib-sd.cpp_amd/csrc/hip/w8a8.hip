@@ -490,8 +490,9 @@ __device__ inline void grouped_tile(int p, int tiles_m, int tiles_n, int &tm, in
 template <int BM, int BN, int ND, bool SCALES, int TAG>
 struct StreamDma {
   static constexpr int ABLK = BM / 16, BBLK = BN / 16, NB = ABLK + BBLK, PW = NB / ND;
-  static_assert(NB % ND == 0 && (!SCALES || BM / 64 <= ND), "DMA split");
-  const int8_t *src[PW];
+  // instruction i of wave d fills block i * ND + d: activation blocks for i < ABLK / ND
+  static_assert(NB % ND == 0 && ABLK % ND == 0 && (!SCALES || BM / 64 <= ND), "DMA split");
+  uint32_t soff[PW];        // byte offset of each block's k-step 0 in its operand (uniform)
   const int8_t *pcs, *psc;  // corr|sw block (wave 0) and scale rows of this wave
   int tile, kt, slot;
 
@@ -506,13 +507,8 @@ struct StreamDma {
 #pragma unroll
     for (int i = 0; i < PW; ++i) {
       const int b = i * ND + d;
-      if (b < ABLK) {
-        const int mb = min(tm * ABLK + b, mblocks - 1);
-        src[i] = q + (size_t)mb * ktc * kFragBytes + lane * 16;
-      } else {
-        const int nb = min(tn * BBLK + (b - ABLK), nblocks - 1);
-        src[i] = wpack + (size_t)nb * ktc * kFragBytes + lane * 16;
-      }
+      const int blk = i < ABLK / ND ? min(tm * ABLK + b, mblocks - 1) : min(tn * BBLK + (b - ABLK), nblocks - 1);
+      soff[i] = (uint32_t)blk * (uint32_t)ktc * (uint32_t)kFragBytes;
     }
     // lanes 0..31: corr of the tile's columns, 32..63: sw; n % 16 == 0, so a
     // group of 4 columns lies wholly inside or wholly past n (then clamped)
@@ -522,13 +518,17 @@ struct StreamDma {
   }
 
   // Issues the DMA of the next stage into ring slot `slot` (and, at a tile's
-  // first k-step, the tile's parameters into buffer tile & 1).
-  __device__ void issue(int8_t *lds, int stage_bytes, int8_t *params, int pbuf, int ktc, int S, int d) {
+  // first k-step, the tile's parameters into buffer tile & 1).  Operand
+  // blocks are buffer loads (ra: activations, rb: packed weights) whose block
+  // offset is scalar and whose lane offset is one constant register, so the
+  // issue costs no vector instructions on the SIMDs the MFMAs run on.
+  __device__ void issue(int8_t *lds, int stage_bytes, int8_t *params, int pbuf, int ktc, int S, int d,
+                        __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb, uint32_t l16) {
     int8_t *dst = lds + slot * stage_bytes;
 #pragma unroll
     for (int i = 0; i < PW; ++i)
-      __builtin_amdgcn_global_load_lds(src[i] + (size_t)kt * kFragBytes, HB_LDS_PTR(dst + (i * ND + d) * kFragBytes),
-                                       16, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(i < ABLK / ND ? ra : rb, HB_LDS_PTR(dst + (i * ND + d) * kFragBytes), 16,
+                                               l16, soff[i] + (uint32_t)kt * (uint32_t)kFragBytes, 0, 0);
     if (kt == 0) {
       int8_t *pb = params + (tile & 1) * pbuf;
       if (d == 0) __builtin_amdgcn_global_load_lds(pcs, HB_LDS_PTR(pb), 16, 0, 0);
@@ -592,6 +592,10 @@ __global__ __launch_bounds__(64 * (WM * WN + ND), 1) void w8a8_gemm_stream(void 
     // has the parameter DMA besides), so the count waits for stage g + 1 and
     // possibly a parameter load after it.  With fewer stages left: vmcnt(0).
     const int d = wave - NW;
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)q, 0, (uint32_t)((m + 15) / 16) * (uint32_t)kp * 16u, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc((void *)wpack, 0, (uint32_t)n * (uint32_t)kp,
+                                                                        0x00020000);
     Dma dma;
     dma.tile = -1;
     dma.kt = 0;
@@ -603,7 +607,7 @@ __global__ __launch_bounds__(64 * (WM * WN + ND), 1) void w8a8_gemm_stream(void 
       grouped_tile(c0 + slot + (++dma.tile) * nslots, tiles_m, tiles_n, tm_, tn_);     \
       dma.point(tm_, tn_, q, wpack, scales, sw, corr, m, n, ktc, d, lane);             \
     }                                                                                  \
-    dma.issue(lds, STAGE, params, PBUF, ktc, S, d);                                    \
+    dma.issue(lds, STAGE, params, PBUF, ktc, S, d, ra, rb, (uint32_t)lane * 16u);      \
   } while (0)
     static_assert(S >= 4, "at least one stage in flight behind the awaited one");
     for (int st = 0; st < S - 1 && st < steps; ++st) STREAM_ISSUE();
