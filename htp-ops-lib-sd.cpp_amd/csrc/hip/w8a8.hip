@@ -856,6 +856,16 @@ __global__ __launch_bounds__(64 * WAVES, MINW) void w8a8_decode_fused(void *__re
       a[j] = make_float4(__uint_as_float(xv[0]), __uint_as_float(xv[1]), __uint_as_float(xv[2]), __uint_as_float(xv[3]));
       iv[j] = make_float4(__uint_as_float(iw[0]), __uint_as_float(iw[1]), __uint_as_float(iw[2]), __uint_as_float(iw[3]));
     }
+    // every wave's row requests enter the memory pipeline before any weight
+    // request (no wait for them): otherwise a late wave's share of the row
+    // queues behind the other waves' weight tiles and holds up the
+    // quantization, which needs the whole row.  Long rows (more than two
+    // float4 per thread) are a large part of a workgroup's bytes: there the
+    // weight stream is not held back for them.
+    if constexpr (VX <= 2) {
+      __builtin_amdgcn_sched_barrier(0);
+      block_barrier();
+    }
     const uint32_t wv = ((uint32_t)nb * (uint32_t)kc + (uint32_t)(wib * VW)) * kFragBytes + (uint32_t)lane * 16u;
 #pragma unroll
     for (int i = 0; i < VW; ++i) {
@@ -870,6 +880,10 @@ __global__ __launch_bounds__(64 * WAVES, MINW) void w8a8_decode_fused(void *__re
       const int v = min(tid + T * j, nvec - 1);
       a[j] = ((const float4 *)x)[v];
       iv[j] = ((const float4 *)inv)[v];
+    }
+    if constexpr (VX <= 2) {
+      __builtin_amdgcn_sched_barrier(0);
+      block_barrier();  // the row before the weights, as above
     }
     const int8_t *wb = wpack + (size_t)nb * kc * kFragBytes + lane * 16;
 #pragma unroll
@@ -1051,6 +1065,9 @@ __global__ __launch_bounds__(1024) void w8a8_decode_even(void *__restrict__ y, c
       __builtin_amdgcn_make_buffer_rsrc((void *)wpack, 0, (uint32_t)nblocks * (uint32_t)kc * kFragBytes, 0x00020000);
   const hb_u32x4 xv = __builtin_amdgcn_raw_buffer_load_b128(rx, (uint32_t)tid * 16u, 0, 0);
   const hb_u32x4 iw = __builtin_amdgcn_raw_buffer_load_b128(ri, (uint32_t)tid * 16u, 0, 0);
+  // every wave's row requests ahead of all weight requests (as in w8a8_decode_fused)
+  __builtin_amdgcn_sched_barrier(0);
+  block_barrier();
   const uint32_t wv =
       mine ? ((uint32_t)nb * (uint32_t)kc + (uint32_t)(wis * VW)) * kFragBytes + (uint32_t)lane * 16u : 0x80000000u;
   hb_i32x4 b[VW];
