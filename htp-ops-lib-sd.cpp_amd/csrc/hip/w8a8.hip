@@ -461,9 +461,10 @@ __global__ __launch_bounds__(64 * WM *WN) void w8a8_gemm_tiles(void *__restrict_
 //    other CUs of the XCD still read from L2.
 //  - The epilogue parameters of a tile (corr and sw of its BN columns, the row
 //    scales of its BM rows) arrive in LDS by DMA with the tile's first k-step,
-//    double-buffered by tile parity: DMA wave 0 loads corr and sw (16 bytes per
-//    lane), DMA wave d loads rows 64d..64d+63 of the scales (4 bytes per lane,
-//    rows past m clamped).
+//    double-buffered by tile parity: DMA waves 0.. load corr then sw, one
+//    kilobyte each (16 bytes per lane; two waves for 192-column tiles), DMA
+//    wave d loads rows 64d..64d+63 of the scales (4 bytes per lane, rows past
+//    m clamped).
 //  - Stores are buffer stores bounded by the tile's valid rows; columns past
 //    n get an out-of-range offset.
 //  - The XCD that runs a workgroup (blockIdx % 8) owns a contiguous chunk of
@@ -491,13 +492,13 @@ template <int BM, int BN, int ND, bool SCALES, int TAG>
 struct StreamDma {
   static constexpr int ABLK = BM / 16, BBLK = BN / 16, NB = ABLK + BBLK, PW = NB / ND;
   // instruction i of wave d fills block i * ND + d: activation blocks for i < ABLK / ND
-  static_assert(NB % ND == 0 && ABLK % ND == 0 && (!SCALES || BM / 64 <= ND), "DMA split");
+  // a tile's parameter buffer: [corr | sw] (BN*8 bytes in PCS one-kilobyte
+  // chunks, the last one padded), then the BM row scales at PSC
+  static constexpr int PCS = (BN * 8 + kFragBytes - 1) / kFragBytes, PSC = PCS * kFragBytes;
+  static_assert(NB % ND == 0 && ABLK % ND == 0 && (!SCALES || BM / 64 <= ND) && PCS <= ND, "DMA split");
   uint32_t soff[PW];        // byte offset of each block's k-step 0 in its operand (uniform)
-  const int8_t *pcs, *psc;  // corr|sw block (wave 0) and scale rows of this wave
+  const int8_t *pcs, *psc;  // this wave's corr|sw chunk (waves below PCS) and scale rows
   int tile, kt, slot;
-
-  // parameter DMA instructions of wave d per tile
-  __device__ static constexpr int param_ops(int d) { return (d == 0 ? 1 : 0) + (SCALES && d < BM / 64 ? 1 : 0); }
 
   // Points the DMA at tile (tm, tn): operand blocks (clamped into A and B)
   // and this wave's parameter blocks.
@@ -510,10 +511,13 @@ struct StreamDma {
       const int blk = i < ABLK / ND ? min(tm * ABLK + b, mblocks - 1) : min(tn * BBLK + (b - ABLK), nblocks - 1);
       soff[i] = (uint32_t)blk * (uint32_t)ktc * (uint32_t)kFragBytes;
     }
-    // lanes 0..31: corr of the tile's columns, 32..63: sw; n % 16 == 0, so a
-    // group of 4 columns lies wholly inside or wholly past n (then clamped)
-    const int col = min(tn * BN + 4 * (lane & 31), n - 4);
-    pcs = lane < 32 ? (const int8_t *)(corr + col) : (const int8_t *)(sw + col);
+    // 16-byte piece c = 64d + lane of [corr | sw]: corr of columns 4c..4c+3
+    // for c < BN/4, then sw; pieces past BN/2 (padding) repeat the last sw
+    // piece.  n % 16 == 0, so a group of 4 columns lies wholly inside or
+    // wholly past n (then clamped).
+    const int c = min(64 * d + lane, BN / 2 - 1);
+    const int col = min(tn * BN + 4 * (c < BN / 4 ? c : c - BN / 4), n - 4);
+    pcs = c < BN / 4 ? (const int8_t *)(corr + col) : (const int8_t *)(sw + col);
     psc = SCALES ? (const int8_t *)(scales + min(tm * BM + 64 * d + lane, m - 1)) : nullptr;
   }
 
@@ -531,8 +535,8 @@ struct StreamDma {
                                                l16, soff[i] + (uint32_t)kt * (uint32_t)kFragBytes, 0, 0);
     if (kt == 0) {
       int8_t *pb = params + (tile & 1) * pbuf;
-      if (d == 0) __builtin_amdgcn_global_load_lds(pcs, HB_LDS_PTR(pb), 16, 0, 0);
-      if (SCALES && d < BM / 64) __builtin_amdgcn_global_load_lds(psc, HB_LDS_PTR(pb + kFragBytes + d * 256), 4, 0, 0);
+      if (d < PCS) __builtin_amdgcn_global_load_lds(pcs, HB_LDS_PTR(pb + d * kFragBytes), 16, 0, 0);
+      if (SCALES && d < BM / 64) __builtin_amdgcn_global_load_lds(psc, HB_LDS_PTR(pb + PSC + d * 256), 4, 0, 0);
     }
     if (++kt == ktc) kt = 0;
     if (++slot == S) slot = 0;
@@ -558,10 +562,11 @@ __global__ __launch_bounds__(64 * (WM * WN + ND), 1) void w8a8_gemm_stream(void 
   constexpr int ABLK = BM / 16;
   constexpr int NB = ABLK + BN / 16;
   constexpr int STAGE = NB * kFragBytes;
-  // parameters per tile: [corr | sw] (BN*8 bytes), then the row scales (BM*4 bytes)
-  static_assert(BN * 8 == kFragBytes && BM * 4 == kFragBytes, "parameter blocks of one kilobyte");
+  // parameters per tile: [corr | sw] (BN*8 bytes, padded to whole kilobytes), then the row scales
+  static_assert(BM * 4 == kFragBytes, "one kilobyte of row scales");
   constexpr bool SCALES = EPI != HB_W8A8_EPI_RAW;
-  constexpr int PBUF = 2 * kFragBytes;
+  constexpr int PSC = StreamDma<BM, BN, ND, SCALES, EPI>::PSC;
+  constexpr int PBUF = PSC + kFragBytes;
 #ifndef HB_STREAM_SPLIT
 #define HB_STREAM_SPLIT 2
 #endif
@@ -681,7 +686,7 @@ __global__ __launch_bounds__(64 * (WM * WN + ND), 1) void w8a8_gemm_stream(void 
       const __amdgpu_buffer_rsrc_t rsrc = stream_out_rsrc(y, ldy, tm * BM, min(BM, m - tm * BM));            \
       float sv[FM];                                                                                          \
       _Pragma("unroll") for (int i = 0; i < FM; ++i) sv[i] =                                                 \
-          SCALES ? *(const float *)(par + kFragBytes + (wm * WTM + i * 16 + (lane & 15)) * 4) : 0.0f;        \
+          SCALES ? *(const float *)(par + PSC + (wm * WTM + i * 16 + (lane & 15)) * 4) : 0.0f;               \
       /* each 16-row x 32-column piece leaves in two stores of 8 whole 128-byte lines: the upper */         \
       /* 8 lanes of every 16-lane row trade their block-0 values for block 1 of the lanes 8 below */        \
       /* (DPP), so a lane then holds row lane%8 (+8 in the second store) of the piece, columns */             \
@@ -1376,9 +1381,13 @@ constexpr TileShape kTileShapes[] = {
     {128, 192, 2, 100}, {256, 192, 1, 90}, {128, 128, 2, 92}, {256, 256, 1, 100}, {64, 64, 4, 60}};
 constexpr int kNumShapes = 5;
 // Index kNumShapes selects the streaming kernel (w8a8_gemm_stream, 256 x 128
-// tiles, one persistent workgroup per CU).
-constexpr int kStreamShape = kNumShapes;
+// tiles, one persistent workgroup per CU); index kNumShapes + 1 its 256 x 192
+// form (5 stages of 28 KB), for shapes whose 192-column tiles fill whole
+// rounds of CUs.  The GELU epilogue keeps the 128-column form (the wider one
+// runs out of registers there).
+constexpr int kStreamShape = kNumShapes, kStreamWideShape = kNumShapes + 1;
 constexpr int kStreamBM = 256, kStreamBN = 128, kStreamStages = 6;
+constexpr int kStreamWideBN = 192, kStreamWideStages = 5;
 
 // -1: automatic.  Set by hb_w8a8_force_tile; HTP_OPS_AMD_W8A8_TILE gives
 // the initial value.
@@ -1389,7 +1398,7 @@ int forced_tile_shape() {
   if (forced == -2) {
     const char *v = getenv("HTP_OPS_AMD_W8A8_TILE");
     forced = (v && *v) ? atoi(v) : -1;
-    if (forced < -1 || forced > kStreamShape) forced = -1;
+    if (forced < -1 || forced > kStreamWideShape) forced = -1;
     int expected = -2;
     if (!g_forced_tile.compare_exchange_strong(expected, forced)) forced = expected;
   }
@@ -1414,6 +1423,7 @@ int compute_units() {
 // The streaming kernel needs kp / 64 >= kStreamStages - 1 (its parameter
 // double buffer).
 bool stream_applies(int kp) { return kp / kKStep >= kStreamStages - 1; }
+bool stream_wide_applies(int n, int kp) { return n % kStreamWideBN == 0 && kp / kKStep >= kStreamWideStages - 1; }
 
 int stream_mode() {
   static const int mode = getenv("HTP_OPS_AMD_W8A8_STREAM") ? atoi(getenv("HTP_OPS_AMD_W8A8_STREAM")) : -1;
@@ -1422,6 +1432,7 @@ int stream_mode() {
 
 int pick_tile_shape(int m, int n, int kp) {
   const int forced = forced_tile_shape();
+  if (forced == kStreamWideShape && stream_wide_applies(n, kp)) return kStreamWideShape;
   if (forced == kStreamShape && stream_applies(kp)) return kStreamShape;
   if (forced >= 0 && forced < kNumShapes && (kTileShapes[forced].bn != 192 || n % 192 == 0)) return forced;
   const int cus = compute_units();
@@ -1434,6 +1445,13 @@ int pick_tile_shape(int m, int n, int kp) {
   // (4096x1536x4608, 2.25 tiles per CU: 46.4 vs 40.5; 2048x4096x6144, 1.5:
   // 60.8 vs 54.0).  HTP_OPS_AMD_W8A8_STREAM=1 / 0 forces it on / off.
   const bool stream_even = stream_tiles <= cus || stream_tiles % cus == 0;
+  // The 192-column form when its tiles fill whole rounds (fewer tiles than CUs
+  // leave CUs idle): 4096x1536x6144 42.4 vs 43.1 us; at 4096x6144x1536
+  // (128 tiles) it would take 44.1 vs 35.2.
+  const long long wide_tiles =
+      (long long)((m + kStreamBM - 1) / kStreamBM) * ((n + kStreamWideBN - 1) / kStreamWideBN);
+  if (stream_mode() != 0 && stream_wide_applies(n, kp) && wide_tiles >= cus && wide_tiles % cus == 0)
+    return kStreamWideShape;
   if (stream_mode() != 0 && stream_applies(kp) && (stream_mode() == 1 || stream_even)) return kStreamShape;
   int best = 0;
   long long best_cost = -1;
@@ -1454,7 +1472,20 @@ int pick_tile_shape(int m, int n, int kp) {
 template <int EPI>
 int launch_tiles(void *y, int ldy, const int8_t *q, const float *scales, const int8_t *wpack, const float *sw,
                  const int32_t *corr, int m, int n, int kp, hipStream_t st) {
-  const int shape = pick_tile_shape(m, n, kp);
+  int shape = pick_tile_shape(m, n, kp);
+  if (shape == kStreamWideShape) {
+    if constexpr (EPI == HB_W8A8_EPI_SCALE_GELU) {
+      shape = stream_applies(kp) ? kStreamShape : 0;
+    } else {
+      const int tiles_m = (m + kStreamBM - 1) / kStreamBM, tiles_n = (n + kStreamWideBN - 1) / kStreamWideBN;
+      const int tiles = tiles_m * tiles_n;
+      const int grid = std::min(compute_units(), (tiles + 7) / 8 * 8) / 8 * 8;
+      if (grid < 8) return hb_invalid("w8a8_gemm_stream grid");
+      hipLaunchKernelGGL((w8a8_gemm_stream<kStreamBM, kStreamWideBN, 4, 2, 4, kStreamWideStages, EPI>), dim3(grid),
+                         dim3(768), 0, st, y, ldy, q, scales, wpack, sw, corr, m, n, kp, tiles_m, tiles_n);
+      return hb_check_launch("w8a8_gemm_stream");
+    }
+  }
   if (shape == kStreamShape) {
     const int tiles_m = (m + kStreamBM - 1) / kStreamBM, tiles_n = (n + kStreamBN - 1) / kStreamBN;
     const int tiles = tiles_m * tiles_n;
@@ -1897,7 +1928,7 @@ int hb_w8a8_linear_noalloc(float *d_y, const float *d_x, const void *d_packed, i
 }
 
 int hb_w8a8_force_tile(int index) {
-  if (index < -1 || index > kStreamShape) return hb_invalid("hb_w8a8_force_tile index");
+  if (index < -1 || index > kStreamWideShape) return hb_invalid("hb_w8a8_force_tile index");
   forced_tile_shape();  // settle the environment default first
   return g_forced_tile.exchange(index);
 }

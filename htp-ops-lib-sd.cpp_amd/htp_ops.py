@@ -328,7 +328,7 @@ def w8a8_force_tile(index):
     return prev
 
 
-W8A8_CHOICE_DECODE, W8A8_CHOICE_DECODE_TILES, W8A8_STREAM_TILE = -1, -2, 5
+W8A8_CHOICE_DECODE, W8A8_CHOICE_DECODE_TILES, W8A8_STREAM_TILE, W8A8_STREAM_WIDE_TILE = -1, -2, 5, 6
 
 
 def w8a8_gemm_kernel(m, k, n):
@@ -339,7 +339,9 @@ def w8a8_gemm_kernel(m, k, n):
     if choice == W8A8_CHOICE_DECODE_TILES:
         return "w8a8_gemm_decode<16,8> (per 16-row tile)"
     if choice == W8A8_STREAM_TILE:
-        return "w8a8_gemm_stream"
+        return "w8a8_gemm_stream<256,128>"
+    if choice == W8A8_STREAM_WIDE_TILE:
+        return "w8a8_gemm_stream<256,192>"
     check(choice, "hb_w8a8_gemm_choice")
     bm, bn = W8A8_TILE_SHAPES[choice]
     return f"w8a8_gemm_tiles<{bm},{bn}>"

@@ -122,8 +122,10 @@ int hb_w8a8_gemm(void *d_y, int ldy, const int8_t *d_q, const float *d_scales, c
 
 /* Tuning and test hook: pins the tiled kernel's shape for every later call
  * (index into 128x192, 256x192, 128x128, 256x256, 64x64, then 5: the
- * persistent streaming kernel with 256x128 tiles, for k >= 320; shapes 192
- * wide apply only when n % 192 == 0) or restores automatic choice with -1.
+ * persistent streaming kernel with 256x128 tiles, for k >= 320, and 6: the
+ * same with 256x192 tiles, for k >= 256, except with the GELU epilogue, which
+ * runs shape 5 instead; shapes 192 wide apply only when n % 192 == 0) or
+ * restores automatic choice with -1.
  * Returns the previous setting.  Results are identical for every shape.
  * The environment variable HTP_OPS_AMD_W8A8_TILE gives the initial value. */
 int hb_w8a8_force_tile(int index);
@@ -132,7 +134,8 @@ int hb_w8a8_force_tile(int index);
  * the environment): HB_W8A8_CHOICE_DECODE (m <= 16, weight-streaming decode
  * kernel), HB_W8A8_CHOICE_DECODE_TILES (17-80 rows over few output tiles: the
  * decode kernel per 16-row tile), or the tile index as hb_w8a8_force_tile
- * numbers them (5: the persistent streaming kernel); HB_E_INVAL on an
+ * numbers them (5 and 6: the persistent streaming kernel with 128- and
+ * 192-column tiles; with the GELU epilogue 6 runs as 5); HB_E_INVAL on an
  * invalid shape.  A measurement and test hook; no counterpart in the
  * reference. */
 #define HB_W8A8_CHOICE_DECODE (-1)

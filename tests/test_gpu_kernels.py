@@ -164,6 +164,7 @@ def test_w8a8_every_tile_shape_bit_exact(hip, orc, tile, m, k, n):
 
 
 STREAM_TILE = 5  # hb_w8a8_force_tile index of the persistent streaming kernel
+STREAM_WIDE_TILE = 6  # ... of its 256x192-tile form
 
 
 @pytest.mark.parametrize("m,k,n", [
@@ -177,6 +178,24 @@ STREAM_TILE = 5  # hb_w8a8_force_tile index of the persistent streaming kernel
 def test_w8a8_stream_kernel_bit_exact(hip, orc, m, k, n, epi):
     """The streaming kernel pinned: raw int32 accumulators and SCALE outputs
     bit-exact, GELU within 1e-5 relative of the oracle's GELU."""
+    check_stream(hip, orc, STREAM_TILE, m, k, n, epi)
+
+
+@pytest.mark.parametrize("m,k,n", [
+    (4096, 1536, 6144),  # headline: two 256x192 tiles per workgroup
+    (2048, 4096, 6144),  # C4 QKV: one tile per workgroup, 64 k-steps
+    (1000, 256, 1152),   # fewest k-steps the 5-stage form takes (4); ragged M tiles
+    (777, 480, 2304),    # K % 64 == 32 (zero-padded k-step), ragged M
+    (5000, 1088, 4032),  # 17 k-steps, 20 x 21 tiles: 1 or 2 per workgroup
+])
+@pytest.mark.parametrize("epi", ["raw", "scale", "gelu"])
+def test_w8a8_stream_wide_kernel_bit_exact(hip, orc, m, k, n, epi):
+    """The 192-column streaming form pinned (GELU runs the 128-column form):
+    the same bits as the oracle."""
+    check_stream(hip, orc, STREAM_WIDE_TILE, m, k, n, epi)
+
+
+def check_stream(hip, orc, tile, m, k, n, epi):
     x, _, blob = make_w8a8(orc, m, k, n, seed=m + k + n, inv_kind="uniform", sums_kind="random", outliers=0.01,
                            scale_lo=1e-3 if epi == "gelu" else 1e-4, scale_hi=1e-2 if epi == "gelu" else 1e-3)
     packed = hip.w8a8_prepack(upload_blob(hip, blob), k, n)
@@ -185,7 +204,7 @@ def test_w8a8_stream_kernel_bit_exact(hip, orc, m, k, n, epi):
     y = hip.DeviceBuffer(m * n * 4)
     y.fill(0xA5)
     epilogue = {"raw": hip.EPI_RAW, "scale": hip.EPI_SCALE, "gelu": hip.EPI_SCALE_GELU}[epi]
-    prev = hip.w8a8_force_tile(STREAM_TILE)
+    prev = hip.w8a8_force_tile(tile)
     try:
         hip.w8a8_gemm(y, q, s, packed, m, k, n, epilogue)
         hip.sync()
@@ -204,17 +223,18 @@ def test_w8a8_stream_kernel_bit_exact(hip, orc, m, k, n, epi):
         np.testing.assert_allclose(got, orc.gelu_tanh_array(ref), rtol=1e-5, atol=1e-30)
 
 
-def test_w8a8_stream_kernel_row_stride(hip, orc):
+@pytest.mark.parametrize("tile,n", [(STREAM_TILE, 1024), (STREAM_WIDE_TILE, 1152)])
+def test_w8a8_stream_kernel_row_stride(hip, orc, tile, n):
     """Output rows with a stride past n (ldy > n): nothing outside the n
     columns of each row is written."""
-    m, k, n, ldy = 600, 768, 1024, 1040
+    m, k, ldy = 600, 768, n + 16
     x, _, blob = make_w8a8(orc, m, k, n, seed=77, inv_kind="uniform", sums_kind="random")
     packed = hip.w8a8_prepack(upload_blob(hip, blob), k, n)
     xd = hip.DeviceBuffer.from_array(x)
     q, s = hip.w8a8_quantize(xd, packed.ptr + hip.w8a8_packed_offset(k, n, hip.SECTION_INV), m, k)
     y = hip.DeviceBuffer(m * ldy * 4)
     y.fill(0xA5)
-    prev = hip.w8a8_force_tile(STREAM_TILE)
+    prev = hip.w8a8_force_tile(tile)
     try:
         hip.w8a8_gemm(y, q, s, packed, m, k, n, hip.EPI_SCALE, ldy=ldy)
         hip.sync()
@@ -234,8 +254,10 @@ def test_w8a8_gemm_choice_names_the_kernel(hip):
     assert lib.hb_w8a8_gemm_choice(1, 4096, 14336) == hip.W8A8_CHOICE_DECODE
     assert lib.hb_w8a8_gemm_choice(16, 14336, 4096) == hip.W8A8_CHOICE_DECODE
     assert lib.hb_w8a8_gemm_choice(32, 4096, 4096) == hip.W8A8_CHOICE_DECODE_TILES
-    assert lib.hb_w8a8_gemm_choice(4096, 1536, 6144) == hip.W8A8_STREAM_TILE
-    assert hip.w8a8_gemm_kernel(4096, 1536, 6144) == "w8a8_gemm_stream"
+    assert lib.hb_w8a8_gemm_choice(4096, 1536, 6144) == hip.W8A8_STREAM_WIDE_TILE
+    assert hip.w8a8_gemm_kernel(4096, 1536, 6144) == "w8a8_gemm_stream<256,192>"
+    # 192-column tiles only where they fill whole rounds of CUs
+    assert hip.w8a8_gemm_kernel(4096, 6144, 1536) == "w8a8_gemm_stream<256,128>"
     prev = hip.w8a8_force_tile(0)
     try:
         assert lib.hb_w8a8_gemm_choice(4096, 1536, 6144) == 0
