@@ -320,8 +320,9 @@ W8A8_TILE_SHAPES = ((128, 192), (256, 192), (128, 128), (256, 256), (64, 64))
 
 
 def w8a8_force_tile(index):
-    """Pins the tiled W8A8 kernel's shape (index into W8A8_TILE_SHAPES, -1 =
-    automatic); returns the previous setting."""
+    """Pins the W8A8 GEMM kernel (an index into W8A8_TILE_SHAPES for the tiled
+    kernel, W8A8_STREAM_TILE or W8A8_STREAM_WIDE_TILE for the streaming kernel,
+    -1 = automatic); returns the previous setting."""
     prev = lib().hb_w8a8_force_tile(index)
     if prev < -1:
         check(prev, "hb_w8a8_force_tile")
