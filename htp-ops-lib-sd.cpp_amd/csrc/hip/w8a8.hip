@@ -555,7 +555,8 @@ __global__ __launch_bounds__(64 * (WM * WN + ND), 1) void w8a8_gemm_stream(void 
                                                                           const int8_t *__restrict__ wpack,
                                                                           const float *__restrict__ sw,
                                                                           const int32_t *__restrict__ corr, int m,
-                                                                          int n, int kp, int tiles_m, int tiles_n) {
+                                                                          int n, int kp, int tiles_m, int tiles_n,
+                                                                          int stagger) {
   constexpr int NW = WM * WN;  // compute waves 0..NW-1; DMA waves NW..NW+ND-1
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int FM = WTM / 16, FN = WTN / 16;
@@ -588,6 +589,13 @@ __global__ __launch_bounds__(64 * (WM * WN + ND), 1) void w8a8_gemm_stream(void 
   const int ntile = c0 + slot < c1 ? (c1 - c0 - slot + nslots - 1) / nslots : 0;
   if (ntile == 0) return;
   const int steps = ntile * ktc;
+  // Workgroups of odd slot start `stagger` ticks of the 100 MHz real-time
+  // counter late, so their tile ends, and the output store bursts that
+  // follow, fall between those of the even slots.
+  if (stagger > 0 && (slot & 1)) {
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    while (__builtin_amdgcn_s_memrealtime() - t0 < (uint64_t)stagger) __builtin_amdgcn_s_sleep(8);
+  }
 
   if (wave >= NW) {
     // --------------------------------- DMA wave ---------------------------------
@@ -1469,6 +1477,26 @@ int pick_tile_shape(int m, int n, int kp) {
   return best;
 }
 
+// Start delay (ticks of the 100 MHz real-time counter) of the streaming
+// kernel's odd-slot workgroups.  With two or more tiles per workgroup the
+// delayed half reaches its tile ends while the other half multiplies, so the
+// two halves' output store bursts no longer share the HBM write bandwidth.
+// Measured (GEMM alone, us, one box; delay 0 / best):
+//   256x192 tiles: 4096x1536x6144 (2 rounds) 46.9 / 42.7 at 5 us,
+//   4096x2048x6144 54.7 / 51.3, 8192x1536x3072 46.9 / 42.6,
+//   4096x1536x12288 (4 rounds) 90.5 / 81.5;
+//   256x128 tiles: 4096x1536x4096 (2 rounds) 31.6 / 30.1 at 4 us;
+// with one round every delay only adds (2048x4096x6144 43.7 -> 44.3 at 5 us,
+// 2048x4096x4096 32.3 -> 33.5) and the 3-round GELU case gains under 1 us.
+// HTP_OPS_AMD_W8A8_STAGGER=ticks overrides the choice (measurement hook).
+int stream_stagger(int tiles, int grid, int bn) {
+  const char *env = getenv("HTP_OPS_AMD_W8A8_STAGGER");
+  if (env && *env && atoi(env) >= 0) return atoi(env);
+  const int rounds = tiles % grid == 0 ? tiles / grid : 0;
+  if (bn == kStreamWideBN) return rounds >= 2 ? 500 : 0;
+  return rounds == 2 ? 400 : 0;
+}
+
 template <int EPI>
 int launch_tiles(void *y, int ldy, const int8_t *q, const float *scales, const int8_t *wpack, const float *sw,
                  const int32_t *corr, int m, int n, int kp, hipStream_t st) {
@@ -1482,7 +1510,8 @@ int launch_tiles(void *y, int ldy, const int8_t *q, const float *scales, const i
       const int grid = std::min(compute_units(), (tiles + 7) / 8 * 8) / 8 * 8;
       if (grid < 8) return hb_invalid("w8a8_gemm_stream grid");
       hipLaunchKernelGGL((w8a8_gemm_stream<kStreamBM, kStreamWideBN, 4, 2, 4, kStreamWideStages, EPI>), dim3(grid),
-                         dim3(768), 0, st, y, ldy, q, scales, wpack, sw, corr, m, n, kp, tiles_m, tiles_n);
+                         dim3(768), 0, st, y, ldy, q, scales, wpack, sw, corr, m, n, kp, tiles_m, tiles_n,
+                         stream_stagger(tiles, grid, kStreamWideBN));
       return hb_check_launch("w8a8_gemm_stream");
     }
   }
@@ -1492,7 +1521,8 @@ int launch_tiles(void *y, int ldy, const int8_t *q, const float *scales, const i
     const int grid = std::min(compute_units(), (tiles + 7) / 8 * 8) / 8 * 8;
     if (grid < 8) return hb_invalid("w8a8_gemm_stream grid");
     hipLaunchKernelGGL((w8a8_gemm_stream<kStreamBM, kStreamBN, 4, 2, 4, kStreamStages, EPI>), dim3(grid), dim3(768),
-                       0, st, y, ldy, q, scales, wpack, sw, corr, m, n, kp, tiles_m, tiles_n);
+                       0, st, y, ldy, q, scales, wpack, sw, corr, m, n, kp, tiles_m, tiles_n,
+                       stream_stagger(tiles, grid, kStreamBN));
     return hb_check_launch("w8a8_gemm_stream");
   }
   const TileShape t = kTileShapes[shape];
