@@ -29,10 +29,13 @@
 #define QTIMER_HZ 19200000.0
 
 static pthread_mutex_t g_exec_lock = PTHREAD_MUTEX_INITIALIZER;
-/* Device scratch slots: 0 W8A8 workspace (opcode 19: a realigned weight), 1 raw
- * accumulators or a realigned bias, 2 realigned activations, 3 realigned
- * output, 4 F16 split-K partials or opcode-19 group-norm partials. */
-enum { kScratchSlots = 5 };
+/* Device scratch slots: 0 W8A8 workspace (opcode 19: a realigned weight; QKV:
+ * a realigned bias), 1 raw accumulators, a realigned bias or the QKV GEMM
+ * output, 2 realigned activations, 3 realigned output, 4 F16 split-K partials
+ * or opcode-19 group-norm partials, 5 / 6 realigned QKV q_norm / k_norm, 7 a
+ * realigned rotary table, 8-10 realigned QKV outputs.  A slot is allocated on
+ * first use. */
+enum { kScratchSlots = 11 };
 static void *g_scratch[kScratchSlots];
 static size_t g_scratch_size[kScratchSlots];
 static __thread int t_device_ready = 0;
@@ -647,6 +650,252 @@ int htp_exec_matmul_w16a32(const struct MatMulParams *p, int32_t *elapsed_us, ui
   return rc;
 }
 
+/* ---- opcodes 8/10/11/12 ------------------------------------------------------ */
+
+/* One projection of a QKV request: the image or text half of the dual opcodes,
+ * or the whole of opcodes 8 and 11. */
+typedef struct {
+  htp_view act, wgt, bias, q_norm, k_norm;
+  int has_bias, tokens, out_offset, rope_offset;
+} qkv_part;
+
+static int qkv_resolve_part(qkv_part *p, const struct RpcmemBufAddr *act, const struct RpcmemBufAddr *wgt,
+                            const struct RpcmemBufAddr *bias, int bias_required, const struct RpcmemBufAddr *q_norm,
+                            const struct RpcmemBufAddr *k_norm, int tokens, int input_dim, size_t weight_bytes,
+                            size_t bias_bytes, size_t norm_bytes) {
+  size_t act_bytes;
+  if (!checked_mul((size_t)tokens, (size_t)input_dim * sizeof(float), &act_bytes)) return -1;
+  p->tokens = tokens;
+  p->has_bias = bias_required || bias->fd >= 0;
+  /* an unmapped buffer reaches the reference kernel as NULL, which it rejects */
+  int rc = resolve(act, act_bytes, &p->act, -1);
+  if (!rc) rc = resolve(wgt, weight_bytes, &p->wgt, -1);
+  if (!rc && p->has_bias) rc = resolve(bias, bias_bytes, &p->bias, -1);
+  if (!rc) rc = resolve(q_norm, norm_bytes, &p->q_norm, -1);
+  if (!rc) rc = resolve(k_norm, norm_bytes, &p->k_norm, -1);
+  if (rc) return rc;
+  /* 128-byte activation and weight (reference src/dsp/ops/mat_mul.c:1385-1388) */
+  if ((primary_address(&p->act) | primary_address(&p->wgt)) & 127u) return -1;
+  return 0;
+}
+
+/* A device pointer to write an output view through: the view itself when
+ * 16-byte aligned, else scratch slot `slot` (copied back by the caller). */
+static void *qkv_output(const htp_view *v, int slot) {
+  if (((uintptr_t)v->dev & 15u) == 0) return v->dev;
+  return htp_executor_scratch(slot, v->bytes);
+}
+
+/* Validated request -> queued GEMM + post-processing for each part.
+ * rope: pe view or NULL; rope_count the token bound of the rotation. */
+static int run_qkv(htp_view out[3], qkv_part *parts, int n_parts, htp_view *pe, int rope_count, int input_dim,
+                   int n_heads, int head_dim, int token_tiles, uint8_t *elapsed_dst) {
+  if (htp_executor_ensure_device() != 0) return -5;
+  for (int i = 0; i < 3; ++i)
+    if (materialize(&out[i])) return -5;
+  if (pe && materialize(pe)) return -5;
+  for (int i = 0; i < n_parts; ++i) {
+    qkv_part *p = &parts[i];
+    if (materialize(&p->act) || materialize(&p->wgt) || materialize(&p->q_norm) || materialize(&p->k_norm) ||
+        (p->has_bias && materialize(&p->bias)))
+      return -5;
+  }
+  hb_stream s = htp_executor_stream();
+  const int ncols = 3 * n_heads * head_dim;
+  /* weights first: a build synchronises, which stays outside the timed region */
+  void *packed[2] = {NULL, NULL};
+  double extra_us = 0.0;
+  for (int i = 0; i < n_parts; ++i) {
+    int built = 0;
+    const double t0 = now_seconds();
+    const int rc = htp_weight_cache_get(HTP_WEIGHT_F16, &parts[i].wgt, input_dim, ncols,
+                                        weight_signature(&parts[i].wgt, 0), &packed[i], &built, s);
+    if (rc) return rc;
+    if (built) extra_us += (now_seconds() - t0) * 1e6;
+  }
+  int max_tokens = 0;
+  for (int i = 0; i < n_parts; ++i) max_tokens = parts[i].tokens > max_tokens ? parts[i].tokens : max_tokens;
+  float *raw = (float *)htp_executor_scratch(1, (size_t)max_tokens * (size_t)ncols * sizeof(float));
+  size_t ws_max = 0;
+  for (int i = 0; i < n_parts; ++i) {
+    const size_t b = hb_f16_workspace_bytes(parts[i].tokens, input_dim, ncols);
+    ws_max = b > ws_max ? b : ws_max;
+  }
+  void *ws = ws_max ? htp_executor_scratch(4, ws_max) : NULL;
+  uint16_t *dst[3];
+  for (int i = 0; i < 3; ++i) dst[i] = (uint16_t *)qkv_output(&out[i], 8 + i);
+  if (!raw || (ws_max && !ws) || !dst[0] || !dst[1] || !dst[2]) return -5;
+  const float *d_pe = NULL;
+  if (pe) {
+    if (stage_in(pe, s)) return -5;
+    d_pe = (const float *)aligned_input(pe, 16, 7, s);
+    if (!d_pe) return -5;
+  }
+  event_set ev;
+  if (events_open(&ev, 2)) {
+    events_close(&ev);
+    return -5;
+  }
+  int hrc = 0;
+  for (int i = 0; i < n_parts && !hrc; ++i) {
+    qkv_part *p = &parts[i];
+    if (stage_in(&p->act, s) || stage_in(&p->q_norm, s) || stage_in(&p->k_norm, s) ||
+        (p->has_bias && stage_in(&p->bias, s))) {
+      hrc = HB_E_HIP;
+      break;
+    }
+    const float *x = (const float *)aligned_input(&p->act, 16, 2, s);
+    const float *qn = (const float *)aligned_input(&p->q_norm, 4, 5, s);
+    const float *kn = (const float *)aligned_input(&p->k_norm, 4, 6, s);
+    const float *b = p->has_bias ? (const float *)aligned_input(&p->bias, 4, 0, s) : NULL;
+    if (!x || !qn || !kn || (p->has_bias && !b)) {
+      hrc = HB_E_HIP;
+      break;
+    }
+    if (i == 0) hrc = hb_event_record(ev.e[0], s);
+    if (!hrc)
+      hrc = hb_f16_gemm_ws(raw, x, (const uint16_t *)packed[i], NULL, p->tokens, input_dim, ncols, ncols, 0, ws,
+                           ws_max, s);
+    if (!hrc)
+      hrc = hb_qkv_post(dst[0], dst[1], dst[2], raw, b, qn, kn, d_pe, p->rope_offset, rope_count, p->tokens, n_heads,
+                        head_dim, token_tiles, p->out_offset, s);
+  }
+  if (!hrc) hrc = hb_event_record(ev.e[1], s);
+  for (int i = 0; i < 3 && !hrc; ++i)
+    if ((void *)dst[i] != out[i].dev) hrc = hb_memcpy_d2d(out[i].dev, dst[i], out[i].bytes, s);
+  if (hrc) {
+    events_close(&ev);
+    return hrc == HB_E_INVAL ? -1 : -5;
+  }
+  for (int i = 0; i < 3; ++i) htp_registry_touch(out[i].fd);
+  const int device_outputs = out[0].is_device && out[1].is_device && out[2].is_device;
+  if (complete(&ev, 0, 1, elapsed_dst, extra_us, device_outputs)) return -5;
+  for (int i = 0; i < 3; ++i)
+    if (stage_out(&out[i], s)) return -5;
+  return 0;
+}
+
+/* Output views of q / k_out / v: n_heads * token_tiles * head_dim * 32 fp16
+ * each, 128-byte aligned (reference src/dsp/ops/mat_mul.c:1385-1388). */
+static int qkv_resolve_outputs(htp_view out[3], const struct RpcmemBufAddr *q, const struct RpcmemBufAddr *k,
+                               const struct RpcmemBufAddr *v, size_t bytes) {
+  int rc = resolve(q, bytes, &out[0], -1);
+  if (!rc) rc = resolve(k, bytes, &out[1], -1);
+  if (!rc) rc = resolve(v, bytes, &out[2], -1);
+  if (rc) return rc;
+  if ((primary_address(&out[0]) | primary_address(&out[1]) | primary_address(&out[2])) & 127u) return -1;
+  return 0;
+}
+
+/* Sizes shared by the four opcodes: output bytes for `token_tiles`, weight,
+ * bias and norm bytes (reference src/dsp/op_executor.cc:244-272, :554-572). */
+static int qkv_sizes(int token_tiles, int input_dim, int n_heads, int head_dim, size_t *qkv_bytes,
+                     size_t *weight_bytes, size_t *bias_bytes, size_t *norm_bytes) {
+  const size_t cols = (size_t)n_heads * (size_t)head_dim * 3u;
+  if (!checked_mul((size_t)token_tiles * (size_t)n_heads, (size_t)head_dim / 32u * 1024u * 2u, qkv_bytes) ||
+      !checked_mul((size_t)input_dim, cols * 2u, weight_bytes))
+    return -1;
+  *bias_bytes = cols * sizeof(float);
+  *norm_bytes = (size_t)head_dim * sizeof(float);
+  return 0;
+}
+
+/* Opcodes 8 and 11 (reference src/dsp/op_executor.cc:542-595, :645-705). */
+static int exec_qkv_single(uint8_t *payload, size_t payload_size, int rope) {
+  const size_t need = rope ? sizeof(struct QkvMulRmsPackedRopeParams) : sizeof(struct QkvMulRmsPackedParams);
+  if (payload_size < need) return -1;
+  struct QkvMulRmsPackedRopeParams p;
+  memset(&p, 0, sizeof(p));
+  if (rope) {
+    memcpy(&p, payload, sizeof(p));
+  } else {
+    struct QkvMulRmsPackedParams b;
+    memcpy(&b, payload, sizeof(b));
+    p.q = b.q, p.k_out = b.k_out, p.v = b.v, p.activation = b.activation, p.weight = b.weight, p.bias = b.bias;
+    p.q_norm = b.q_norm, p.k_norm = b.k_norm;
+    p.tokens = b.tokens, p.input_dim = b.input_dim, p.n_heads = b.n_heads, p.head_dim = b.head_dim;
+  }
+  if (p.tokens <= 0 || p.input_dim <= 0 || !htp_packed_shape_supported(p.n_heads, p.n_heads, p.head_dim, 1) ||
+      p.input_dim % 32 || (rope && (p.rope_token_offset < 0 || p.rope_token_count <= 0)))
+    return -1;
+  const int token_tiles = (p.tokens + 31) / 32;
+  size_t qkv_bytes, weight_bytes, bias_bytes, norm_bytes, pe_bytes = 0;
+  if (qkv_sizes(token_tiles, p.input_dim, p.n_heads, p.head_dim, &qkv_bytes, &weight_bytes, &bias_bytes,
+                &norm_bytes) ||
+      (rope && !checked_mul((size_t)p.rope_token_count, (size_t)p.head_dim / 2u * 4u * sizeof(float), &pe_bytes)))
+    return -1;
+  htp_view out[3], pe;
+  qkv_part part;
+  memset(&part, 0, sizeof(part));
+  int rc = qkv_resolve_outputs(out, &p.q, &p.k_out, &p.v, qkv_bytes);
+  if (!rc) rc = qkv_resolve_part(&part, &p.activation, &p.weight, &p.bias, !rope, &p.q_norm, &p.k_norm, p.tokens,
+                                 p.input_dim, weight_bytes, bias_bytes, norm_bytes);
+  if (rc) return rc;
+  /* an unmapped rotary table leaves the rows unrotated (reference
+   * src/dsp/ops/mat_mul.c:1212-1214 returns on a NULL table) */
+  const int have_pe = rope && resolve(&p.rope_pe, pe_bytes, &pe, -1) == 0;
+  part.rope_offset = p.rope_token_offset;
+  uint8_t *elapsed = payload + (rope ? offsetof(struct QkvMulRmsPackedRopeParams, elapsed_us)
+                                     : offsetof(struct QkvMulRmsPackedParams, elapsed_us));
+  return run_qkv(out, &part, 1, have_pe ? &pe : NULL, p.rope_token_count, p.input_dim, p.n_heads, p.head_dim,
+                 token_tiles, elapsed);
+}
+
+/* Opcodes 10 and 12: image tokens (a multiple of 32) then text tokens in one
+ * packed output, each half with its own activation, weight, bias and norms
+ * (reference src/dsp/op_executor.cc:597-643, :707-770, src/dsp/ops/mat_mul.c:1515-1583). */
+static int exec_qkv_dual(uint8_t *payload, size_t payload_size, int rope) {
+  const size_t need = rope ? sizeof(struct QkvMulRmsPackedDualRopeParams) : sizeof(struct QkvMulRmsPackedDualParams);
+  if (payload_size < need) return -1;
+  struct QkvMulRmsPackedDualRopeParams p;
+  memset(&p, 0, sizeof(p));
+  if (rope) {
+    memcpy(&p, payload, sizeof(p));
+  } else {
+    /* the dual payload is the dual RoPE payload without rope_pe and the offsets */
+    struct QkvMulRmsPackedDualParams b;
+    memcpy(&b, payload, sizeof(b));
+    memcpy(&p, &b, offsetof(struct QkvMulRmsPackedDualParams, image_tokens));
+    p.image_tokens = b.image_tokens, p.text_tokens = b.text_tokens, p.input_dim = b.input_dim;
+    p.n_heads = b.n_heads, p.head_dim = b.head_dim;
+  }
+  if (p.image_tokens <= 0 || p.text_tokens <= 0 || p.image_tokens % 32 || p.input_dim <= 0 || p.input_dim % 32 ||
+      !htp_packed_shape_supported(p.n_heads, p.n_heads, p.head_dim, 1) ||
+      p.text_tokens > INT32_MAX - p.image_tokens ||
+      (rope && (p.image_rope_token_offset < 0 || p.text_rope_token_offset < 0)))
+    return -1;
+  const int combined = p.image_tokens + p.text_tokens;
+  const int token_tiles = (combined + 31) / 32;
+  size_t qkv_bytes, weight_bytes, bias_bytes, norm_bytes, pe_bytes = 0;
+  if (qkv_sizes(token_tiles, p.input_dim, p.n_heads, p.head_dim, &qkv_bytes, &weight_bytes, &bias_bytes,
+                &norm_bytes))
+    return -1;
+  if (rope) {
+    const int64_t a = (int64_t)p.image_rope_token_offset + p.image_tokens;
+    const int64_t b = (int64_t)p.text_rope_token_offset + p.text_tokens;
+    if (!checked_mul((size_t)(a > b ? a : b), (size_t)p.head_dim / 2u * 4u * sizeof(float), &pe_bytes)) return -1;
+  }
+  htp_view out[3], pe;
+  qkv_part parts[2];
+  memset(parts, 0, sizeof(parts));
+  int rc = qkv_resolve_outputs(out, &p.q, &p.k_out, &p.v, qkv_bytes);
+  if (!rc) rc = qkv_resolve_part(&parts[0], &p.image_activation, &p.image_weight, &p.image_bias, 0, &p.image_q_norm,
+                                 &p.image_k_norm, p.image_tokens, p.input_dim, weight_bytes, bias_bytes, norm_bytes);
+  if (!rc) rc = qkv_resolve_part(&parts[1], &p.text_activation, &p.text_weight, &p.text_bias, 0, &p.text_q_norm,
+                                 &p.text_k_norm, p.text_tokens, p.input_dim, weight_bytes, bias_bytes, norm_bytes);
+  if (rc) return rc;
+  const int have_pe = rope && resolve(&p.rope_pe, pe_bytes, &pe, -1) == 0;
+  parts[0].out_offset = 0;
+  parts[1].out_offset = p.image_tokens;
+  parts[0].rope_offset = p.image_rope_token_offset;
+  parts[1].rope_offset = p.text_rope_token_offset;
+  uint8_t *elapsed = payload + (rope ? offsetof(struct QkvMulRmsPackedDualRopeParams, elapsed_us)
+                                     : offsetof(struct QkvMulRmsPackedDualParams, elapsed_us));
+  /* both halves rotate tokens below image_tokens + text_tokens */
+  return run_qkv(out, parts, 2, have_pe ? &pe : NULL, combined, p.input_dim, p.n_heads, p.head_dim, token_tiles,
+                 elapsed);
+}
+
 /* ---- opcode 19 ------------------------------------------------------------------- */
 
 /* A device pointer with 4-byte alignment for an optional input view (NULL view: NULL). */
@@ -779,6 +1028,10 @@ int execute_op_simple(struct OpComputeRequest *req, size_t req_size) {
       rc = exec_matmul_qk0(payload, payload_size, HTP_WEIGHT_IQ4_NL, HB_GGML_IQ4_NL);
       break;
     case HTP_OPS_MODEL_AUX_F32: rc = exec_model_aux(payload, payload_size); break;
+    case HTP_OPS_QKV_MUL_RMS_PACKED_W16A32: rc = exec_qkv_single(payload, payload_size, 0); break;
+    case HTP_OPS_QKV_MUL_RMS_PACKED_ROPE_W16A32: rc = exec_qkv_single(payload, payload_size, 1); break;
+    case HTP_OPS_QKV_MUL_RMS_PACKED_DUAL_W16A32: rc = exec_qkv_dual(payload, payload_size, 0); break;
+    case HTP_OPS_QKV_MUL_RMS_PACKED_DUAL_ROPE_W16A32: rc = exec_qkv_dual(payload, payload_size, 1); break;
     default: rc = HTP_OPS_E_UNSUPPORTED; break;
   }
   pthread_mutex_unlock(&g_exec_lock);

@@ -89,6 +89,7 @@ _SIGNATURES = {
     "hb_model_aux": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p] + [_c_int] * 9 + [ctypes.c_float,
                                                                                          _c_void_p]),
     "hb_model_aux_workspace_bytes": (_c_size_t, [_c_int] * 5),
+    "hb_qkv_post": (_c_int, [_c_void_p] * 8 + [_c_int] * 7 + [_c_void_p]),
     "hb_model_aux_ws": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p] + [_c_int] * 9 +
                         [ctypes.c_float, _c_void_p, _c_size_t, _c_void_p]),
 }
@@ -580,6 +581,54 @@ def model_aux(y_dev, x_dev, w_dev, b_dev, mode, count, width, channels=1, spatia
         check(lib().hb_model_aux_ws(y_dev.ptr, x_dev.ptr, w, b, mode, count, width, channels, spatial, groups, batch,
                                     other_count, activation, eps, workspace.ptr, workspace.nbytes, stream),
               "hb_model_aux_ws")
+
+
+OP_QKV_MUL_RMS_PACKED, OP_QKV_MUL_RMS_PACKED_DUAL, OP_QKV_MUL_RMS_PACKED_ROPE, OP_QKV_MUL_RMS_PACKED_DUAL_ROPE = \
+    8, 10, 11, 12
+_NO_BUFFER = (-1, 0)
+
+
+def qkv_params(q, k, v, act, wgt, bias, q_norm, k_norm, tokens, input_dim, n_heads, head_dim, elapsed=0):
+    """QkvMulRmsPackedParams (84 bytes, opcode 8); buffers are (fd, offset)."""
+    return _struct.pack("<16i5i", *q, *k, *v, *act, *wgt, *bias, *q_norm, *k_norm, tokens, input_dim, n_heads,
+                        head_dim, elapsed)
+
+
+def qkv_rope_params(q, k, v, act, wgt, bias, q_norm, k_norm, pe, tokens, input_dim, n_heads, head_dim,
+                    rope_offset, rope_count, elapsed=0):
+    """QkvMulRmsPackedRopeParams (100 bytes, opcode 11); bias may be (-1, 0)."""
+    return _struct.pack("<18i7i", *q, *k, *v, *act, *wgt, *bias, *q_norm, *k_norm, *pe, tokens, input_dim, n_heads,
+                        head_dim, rope_offset, rope_count, elapsed)
+
+
+def qkv_dual_params(q, k, v, image, text, image_tokens, text_tokens, input_dim, n_heads, head_dim, elapsed=0):
+    """QkvMulRmsPackedDualParams (128 bytes, opcode 10); image / text are
+    (activation, weight, bias, q_norm, k_norm) tuples of (fd, offset)."""
+    bufs = [x for b in (q, k, v, *image, *text) for x in b]
+    return _struct.pack("<26i6i", *bufs, image_tokens, text_tokens, input_dim, n_heads, head_dim, elapsed)
+
+
+def qkv_dual_rope_params(q, k, v, image, text, pe, image_tokens, text_tokens, input_dim, n_heads, head_dim,
+                         image_rope_offset, text_rope_offset, elapsed=0):
+    """QkvMulRmsPackedDualRopeParams (144 bytes, opcode 12)."""
+    bufs = [x for b in (q, k, v, *image, *text, pe) for x in b]
+    return _struct.pack("<28i8i", *bufs, image_tokens, text_tokens, input_dim, n_heads, head_dim, image_rope_offset,
+                        text_rope_offset, elapsed)
+
+
+def qkv_head_elems(token_tiles, head_dim):
+    """Halfwords of one head's region in a packed Q / K / V output."""
+    return token_tiles * (head_dim // 32) * 1024
+
+
+def qkv_post(q_dev, k_dev, v_dev, raw_dev, bias_dev, q_norm_dev, k_norm_dev, pe_dev, rope_offset, rope_count,
+             tokens, n_heads, head_dim, token_tiles, out_offset=0, stream=None):
+    """hb_qkv_post on device buffers (bias_dev / pe_dev may be None)."""
+    b = bias_dev.ptr if bias_dev else None
+    pe = pe_dev.ptr if pe_dev else None
+    check(lib().hb_qkv_post(q_dev.ptr, k_dev.ptr, v_dev.ptr, raw_dev.ptr, b, q_norm_dev.ptr, k_norm_dev.ptr, pe,
+                            rope_offset, rope_count, tokens, n_heads, head_dim, token_tiles, out_offset, stream),
+          "hb_qkv_post")
 
 
 def matmul_params(out, act, wgt, m, k, n, with_elapsed=False):

@@ -9,6 +9,8 @@
  *     opcode 19 (model auxiliary f32 ops) reference src/dsp/op_executor.cc:371-404
  *     opcodes 2/3/4 (Q4_0 / Q8_0 / IQ4_NL weights, F16 GEMM)
  *                       reference src/dsp/op_executor.cc:771-800
+ *     opcodes 8/10/11/12 (fused QKV + RMS norm (+ RoPE), packed fp16 outputs)
+ *                       reference src/dsp/op_executor.cc:542-770
  *
  * Return codes (unchanged from the reference):
  *   opcode 15: -1 payload size / shape / profile mode, -2 unmapped buffer,
@@ -20,6 +22,11 @@
  *              not a multiple of 32, misaligned buffer (128 B).
  *   opcode 19: -1 payload size / validation / unmapped buffer, -40 a norm with
  *              no whole row (the reference's empty worker pool).
+ *   opcodes 8/10/11/12: -1 payload size, unsupported shape (heads 24/30/38,
+ *              head_dim 64/128, 38 heads only with 64), input_dim not a multiple of
+ *              32, a required buffer unmapped, q/k/v/activation/weight not 128-byte
+ *              aligned, dual requests with image_tokens not a multiple of 32 or no
+ *              text tokens, negative rotary offsets or count.
  *   other opcodes: HTP_OPS_E_UNSUPPORTED (the reference silently returns 0).
  *   A GPU runtime failure while executing a valid request returns -5.
  * All argument checks happen before any GPU work is queued.

@@ -261,6 +261,22 @@ int hb_model_aux_ws(float *d_y, const float *d_x, const float *d_w, const float 
                     int channels, int spatial, int groups, int batch, int other_count, int activation, float eps,
                     void *d_workspace, size_t workspace_bytes, hb_stream s);
 
+/*
+ * Opcodes 8/10/11/12 post-processing (reference src/dsp/ops/mat_mul.c:1051-1371):
+ * d_raw is the packed-F16 GEMM output of one call (tokens x 3*n_heads*head_dim
+ * f32, fp16-exact values: hb_f16_gemm mode 0 without bias).  Per head, Q and K
+ * get bias, RMS norm with q_norm / k_norm (head_dim values each) and, with
+ * d_pe, the rotary 2x2 matrices of token rope_offset + row (head_dim/2
+ * matrices of 4 floats per token) for tokens below rope_count; V gets the
+ * bias.  The fp16 results go to the packed Q / K / V images (n_heads regions
+ * of token_tiles * head_dim * 32 halfwords) at token tiles out_offset/32 ..;
+ * rows past `tokens` in the last tile are zeros.  d_bias may be NULL (zero).
+ * head_dim 64 or 128; outputs 16-byte aligned.
+ */
+int hb_qkv_post(uint16_t *d_q, uint16_t *d_k, uint16_t *d_v, const float *d_raw, const float *d_bias,
+                const float *d_q_norm, const float *d_k_norm, const float *d_pe, int rope_offset, int rope_count,
+                int tokens, int n_heads, int head_dim, int token_tiles, int out_offset, hb_stream s);
+
 #ifdef __cplusplus
 }
 #endif

@@ -7,9 +7,12 @@
  *   W8A8 blob header / payloads reference include/op_reg.h:80-149
  *   MatMulParams (opcode 1)     reference include/op_reg.h:151-181
  *   F16EpilogueParams (op 16)   reference include/op_reg.h:477-489
+ *   QKV payloads (ops 8/10-12)  reference include/op_reg.h:183-285
+ *   NativeAuxParams (op 19)     reference include/op_reg.h:503-507
  *
- * Only opcodes 1, 15 and 16 are executed by this library; every other opcode
- * is answered with HTP_OPS_E_UNSUPPORTED instead of a silent success.
+ * Opcodes 1-4, 8, 10-12, 15, 16 and 19 are executed by this library; every
+ * other opcode is answered with HTP_OPS_E_UNSUPPORTED instead of a silent
+ * success.
  */
 #ifndef HTP_OPS_OP_REG_H
 #define HTP_OPS_OP_REG_H
@@ -185,6 +188,54 @@ struct NativeAuxParams {
 } __attribute__((packed));
 
 HTP_OPS_STATIC_ASSERT(sizeof(struct NativeAuxParams) == 76, "native auxiliary ABI");
+
+/* ---- opcodes 8/10/11/12: fused QKV projection + RMS norm (+ RoPE) ----------
+ * (reference include/op_reg.h:23-39 shape rule, :183-285 payloads)
+ * The weight is opcode 1's permuted fp16 layout with 3 * n_heads * head_dim
+ * columns (Q | K | V); bias has as many floats (fd < 0: none, except for
+ * opcode 8), q_norm / k_norm head_dim floats; outputs are fp16 packed tiles
+ * of n_heads * ceil(tokens/32) * head_dim * 32 halfwords each. */
+static inline int htp_packed_head_count_supported(int n_heads) {
+  return n_heads == 24 || n_heads == 30 || n_heads == 38;
+}
+static inline int htp_packed_head_dim_supported(int head_dim) { return head_dim == 64 || head_dim == 128; }
+static inline int htp_packed_shape_supported(int n_heads, int n_kv_heads, int head_dim, int require_equal_kv) {
+  return n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0 && htp_packed_head_count_supported(n_heads) &&
+         htp_packed_head_dim_supported(head_dim) && (n_heads != 38 || head_dim == 64) &&
+         (!require_equal_kv || (n_heads == n_kv_heads && htp_packed_head_count_supported(n_kv_heads)));
+}
+
+struct QkvMulRmsPackedParams {
+  struct RpcmemBufAddr q, k_out, v, activation, weight, bias, q_norm, k_norm;
+  int32_t tokens, input_dim, n_heads, head_dim, elapsed_us;
+} __attribute__((packed));
+
+struct QkvMulRmsPackedDualParams {
+  struct RpcmemBufAddr q, k_out, v;
+  struct RpcmemBufAddr image_activation, image_weight, image_bias, image_q_norm, image_k_norm;
+  struct RpcmemBufAddr text_activation, text_weight, text_bias, text_q_norm, text_k_norm;
+  int32_t image_tokens, text_tokens, input_dim, n_heads, head_dim, elapsed_us;
+} __attribute__((packed));
+
+/* rope_pe: rope_token_count tokens x head_dim/2 2x2 matrices (4 floats each). */
+struct QkvMulRmsPackedRopeParams {
+  struct RpcmemBufAddr q, k_out, v, activation, weight, bias, q_norm, k_norm, rope_pe;
+  int32_t tokens, input_dim, n_heads, head_dim, rope_token_offset, rope_token_count, elapsed_us;
+} __attribute__((packed));
+
+struct QkvMulRmsPackedDualRopeParams {
+  struct RpcmemBufAddr q, k_out, v;
+  struct RpcmemBufAddr image_activation, image_weight, image_bias, image_q_norm, image_k_norm;
+  struct RpcmemBufAddr text_activation, text_weight, text_bias, text_q_norm, text_k_norm;
+  struct RpcmemBufAddr rope_pe;
+  int32_t image_tokens, text_tokens, input_dim, n_heads, head_dim, image_rope_token_offset, text_rope_token_offset,
+      elapsed_us;
+} __attribute__((packed));
+
+HTP_OPS_STATIC_ASSERT(sizeof(struct QkvMulRmsPackedParams) == 84, "QKV payload ABI");
+HTP_OPS_STATIC_ASSERT(sizeof(struct QkvMulRmsPackedDualParams) == 128, "QKV dual payload ABI");
+HTP_OPS_STATIC_ASSERT(sizeof(struct QkvMulRmsPackedRopeParams) == 100, "QKV RoPE payload ABI");
+HTP_OPS_STATIC_ASSERT(sizeof(struct QkvMulRmsPackedDualRopeParams) == 144, "QKV dual RoPE payload ABI");
 HTP_OPS_STATIC_ASSERT(sizeof(struct RpcmemBufAddr) == 8, "RpcmemBufAddr ABI");
 
 #ifdef __cplusplus

@@ -655,6 +655,123 @@ void oracle_f16_gemm_epilogue(float *y, const float *x, const uint16_t *permuted
 }
 
 /* ------------------------------------------------------------------------ */
+/* Fused QKV + RMS + RoPE packing (opcodes 8/10/11/12)                      */
+/* post-processing of the F16 GEMM output: reference src/dsp/ops/mat_mul.c  */
+/* :1051-1125 (packing), :1127-1231 (sum, rsqrt, RMS with bias, rotary),    */
+/* :1233-1266 (casts), :1297-1371 (worker), :1373-1578 (driver)             */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * Halfword index of (token r of token tile tt, column c of the head) inside
+ * one head's region:
+ *   Q: row pairs interleaved per 32-column tile, wsf_to_vhf(row r+1, row r)
+ *      (qkv_pack_q_tile :1051-1072), tiles [token tile][column tile];
+ *   K: the row converted in natural column order (vdeal of wsf_to_vhf,
+ *      :1233-1247), then scattered: word w (columns 2w, 2w+1) of a 64-column
+ *      chunk of token r to byte 128*w + 4*r of the chunk's two tiles
+ *      (qkv_pack_k_tile :1078-1101);
+ *   V: row pairs interleaved per 32-column tile (vshuff of two rows,
+ *      qkv_pack_v_tile :1103-1125), tiles [column tile][token tile]
+ *      (worker :1359-1369).
+ */
+size_t oracle_qkv_index(int which, int token_tiles, int head_dim, int tt, int r, int c) {
+  const size_t pair = (size_t)(r / 2) * 64u + (size_t)(c % 32) * 2u + (size_t)(r % 2);
+  if (which == 0) return (size_t)tt * (size_t)head_dim * 32u + (size_t)(c / 32) * 1024u + pair;
+  if (which == 1)
+    return (size_t)tt * (size_t)head_dim * 32u + (size_t)(c / 64) * 2048u + (size_t)((c % 64) / 2) * 64u +
+           (size_t)r * 2u + (size_t)(c % 2);
+  return ((size_t)(c / 32) * (size_t)token_tiles + (size_t)tt) * 1024u + pair;
+}
+
+/* 1/sqrt(x): the 0x5f3759df start, then three Newton steps y*(1.5 - x/2*y*y),
+ * each operation one IEEE rounding (qkv_rsqrt_vsf :1137-1165). */
+float oracle_qkv_rsqrt(float x) {
+  const float half = x * 0.5f;
+  float y = bits_f32(0x5f3759dfu - (f32_bits(x) >> 1));
+  for (int it = 0; it < 3; ++it) {
+    const float y2 = y * y;
+    const float corr = 1.5f - half * y2;
+    y = y * corr;
+  }
+  return y;
+}
+
+/* RMS normalization of one row of a Q or K head with its bias
+ * (qkv_rms_bias :1167-1208): v = x + b; the sum of squares in the order of
+ * the 32-lane vector code (lane j adds v[64d+j]^2 then v[64d+32+j]^2 over the
+ * 64-column chunks d, then lanes are summed by the shifted adds of
+ * qkv_reduce_sum :1127-1135: lane i += lane i-s for s = 16, 8, 4, 2, 1, and
+ * lane 31 is the sum); rsqrt(sum / hd + 1e-6); y = (v * inv) * gamma. */
+static void qkv_rms_row(float *row, const float *x, const float *b, const float *gamma, int hd) {
+  float lanes[32];
+  for (int j = 0; j < 32; ++j) {
+    float acc = 0.0f;
+    for (int d = 0; d < hd / 64; ++d) {
+      const float v0 = x[64 * d + j] + (b ? b[64 * d + j] : 0.0f);
+      const float v1 = x[64 * d + 32 + j] + (b ? b[64 * d + 32 + j] : 0.0f);
+      row[64 * d + j] = v0;
+      row[64 * d + 32 + j] = v1;
+      acc = acc + v0 * v0;
+      acc = acc + v1 * v1;
+    }
+    lanes[j] = acc;
+  }
+  for (int s = 16; s >= 1; s /= 2) {
+    float next[32];
+    for (int i = 0; i < 32; ++i) next[i] = i >= s ? lanes[i] + lanes[i - s] : lanes[i];
+    memcpy(lanes, next, sizeof(lanes));
+  }
+  const float inv = oracle_qkv_rsqrt(lanes[31] / (float)hd + 1.0e-6f);
+  for (int c = 0; c < hd; ++c) row[c] = (row[c] * inv) * gamma[c];
+}
+
+void oracle_qkv_post(uint16_t *q, uint16_t *k, uint16_t *v, const float *raw, const float *bias, const float *q_norm,
+                     const float *k_norm, const float *pe, int rope_token_offset, int rope_token_count, int tokens,
+                     int n_heads, int head_dim, int output_token_tiles, int output_token_offset) {
+  const int hd = head_dim, q_cols = n_heads * hd, n = 3 * q_cols;
+  const size_t hte = (size_t)output_token_tiles * (size_t)(hd / 32) * 1024u;
+  float *row = (float *)malloc(sizeof(float) * (size_t)hd);
+  for (int t0 = 0; t0 < tokens; t0 += 32) {
+    const int rows = tokens - t0 < 32 ? tokens - t0 : 32;
+    const int tt = (output_token_offset + t0) / 32;
+    for (int col0 = 0; col0 < n; col0 += hd) {
+      const int which = col0 < q_cols ? 0 : col0 < 2 * q_cols ? 1 : 2;
+      const int head = (col0 - which * q_cols) / hd;
+      uint16_t *dst = (which == 0 ? q : which == 1 ? k : v) + (size_t)head * hte;
+      const float *b = bias ? bias + col0 : NULL;
+      for (int r = 0; r < 32; ++r) {
+        if (r >= rows) {
+          for (int c = 0; c < hd; ++c) dst[oracle_qkv_index(which, output_token_tiles, hd, tt, r, c)] = 0;
+          continue;
+        }
+        const float *x = raw + (size_t)(t0 + r) * n + col0;
+        if (which < 2) {
+          qkv_rms_row(row, x, b, which == 0 ? q_norm : k_norm, hd);
+          /* rotary (qkv_apply_rope :1210-1231): token = offset + row; rows at or
+           * past the count are left as they are */
+          const int token = rope_token_offset + t0 + r;
+          if (pe && rope_token_offset >= 0 && rope_token_count > 0 && token < rope_token_count) {
+            const float *tp = pe + (size_t)token * (size_t)(hd / 2) * 4u;
+            for (int d = 0; d < hd / 2; ++d) {
+              const float x0 = row[2 * d], x1 = row[2 * d + 1];
+              const float *m = tp + (size_t)d * 4u;
+              row[2 * d] = x0 * m[0] + x1 * m[1];
+              row[2 * d + 1] = x0 * m[2] + x1 * m[3];
+            }
+          }
+        } else {
+          /* V: bias, then the cast (qkv_bias_cast :1249-1266) */
+          for (int c = 0; c < hd; ++c) row[c] = x[c] + (b ? b[c] : 0.0f);
+        }
+        for (int c = 0; c < hd; ++c)
+          dst[oracle_qkv_index(which, output_token_tiles, hd, tt, r, c)] = oracle_f32_to_f16(row[c]);
+      }
+    }
+  }
+  free(row);
+}
+
+/* ------------------------------------------------------------------------ */
 /* Dequantizing GEMM (opcodes 2/3/4): Q4_0, Q8_0, IQ4_NL super-blocks        */
 /* block formats: reference include/dsp/quants.h:16-31 (my_block_q4_0,      */
 /* my_block_q8_0); dequantization: src/dsp/ops/mat_mul.c:330-429 (Q4_0,     */

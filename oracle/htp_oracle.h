@@ -45,6 +45,21 @@
  *                               restatement; scale-one blocks give the codes
  *                               exactly.  Parity unpinned against the sd.cpp
  *                               packer (absent) and the qf16 product rounding.
+ *   qkv_index                 pinned: a model of the HVX instructions of the
+ *                               packing steps (wsf_to_vhf interleave, vdeal,
+ *                               vshuff, vscatter byte offsets) run on a matrix
+ *                               of distinct values equals these positions.
+ *   qkv_rsqrt                 pinned: within 2 ulp of 1/sqrt in double over
+ *                               the normal range, and the magic-constant start
+ *                               (three Newton steps from 0x5f3759df, each an
+ *                               IEEE operation); parity unpinned against the
+ *                               QFloat steps of mat_mul.c:1137-1165.
+ *   qkv_post                  pinned: float64 closed forms (normalized rows
+ *                               have RMS gamma within the fp16 bound, bias
+ *                               only shifts V, identity rotary matrices keep
+ *                               Q/K, rotations keep pair norms); parity unpinned
+ *                               against the QFloat rounding of the bias add,
+ *                               sum of squares and scaling.
  */
 #ifndef HTP_ORACLE_H
 #define HTP_ORACLE_H
@@ -103,6 +118,14 @@ int oracle_qk0_dequant(uint16_t *permuted, const uint8_t *blocks, int k, int n, 
 void oracle_f16_permute(uint16_t *permuted, const uint16_t *w_kn, int k, int n);
 void oracle_f16_gemm_epilogue(float *y, const float *x, const uint16_t *permuted, const float *bias, int m, int k,
                               int n, int channels, int mode, int nthreads);
+
+/* ---- fused QKV + RMS + RoPE packing (opcodes 8/10/11/12) -------------------- */
+/* which: 0 = Q, 1 = K, 2 = V; halfword index inside one head's region. */
+size_t oracle_qkv_index(int which, int token_tiles, int head_dim, int tt, int r, int c);
+float oracle_qkv_rsqrt(float x);
+void oracle_qkv_post(uint16_t *q, uint16_t *k, uint16_t *v, const float *raw, const float *bias, const float *q_norm,
+                     const float *k_norm, const float *pe, int rope_token_offset, int rope_token_count, int tokens,
+                     int n_heads, int head_dim, int output_token_tiles, int output_token_offset);
 
 /* ---- deterministic inputs --------------------------------------------------- */
 uint64_t oracle_splitmix64(uint64_t *state);

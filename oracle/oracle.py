@@ -41,6 +41,9 @@ _SIGS = {
     "oracle_f16_permuted_index": (_S, [_I, _I, _I]),
     "oracle_f16_permute": (None, [_P, _P, _I, _I]),
     "oracle_f16_gemm_epilogue": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I]),
+    "oracle_qkv_index": (_S, [_I, _I, _I, _I, _I, _I]),
+    "oracle_qkv_rsqrt": (ctypes.c_float, [ctypes.c_float]),
+    "oracle_qkv_post": (None, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I]),
     "oracle_qk0_block_bytes": (_S, [_I]),
     "oracle_qk0_value": (ctypes.c_uint16, [_P, _I, _I]),
     "oracle_qk0_dequant": (_I, [_P, _P, _I, _I, _I]),
@@ -265,6 +268,36 @@ def f16_gemm_epilogue(x, permuted, bias, m, k, n, channels, mode, nthreads=0):
                                    _ptr(None if bias is None else np.ascontiguousarray(bias, np.float32)), m, k, n,
                                    channels, mode, nthreads)
     return y.reshape((channels, m) if mode == 3 else (m, n))
+
+
+# ---- fused QKV + RMS + RoPE packing (opcodes 8/10/11/12) -----------------------
+
+
+def qkv_index(which, token_tiles, head_dim, tt, r, c):
+    return lib().oracle_qkv_index(which, token_tiles, head_dim, tt, r, c)
+
+
+def qkv_rsqrt(x):
+    return lib().oracle_qkv_rsqrt(x)
+
+
+def qkv_head_elems(token_tiles, head_dim):
+    return token_tiles * (head_dim // 32) * 1024
+
+
+def qkv_post(raw, bias, q_norm, k_norm, pe, rope_offset, rope_count, tokens, n_heads, head_dim, token_tiles,
+             out_offset=0, out=None):
+    """Post-processing of one call's GEMM output (tokens x 3*n_heads*head_dim,
+    f32 holding fp16 values) into the packed fp16 Q/K/V images (uint16 bits of
+    n_heads * token_tiles * head_dim * 32 halfwords each); `out` (q, k, v)
+    keeps the token tiles other calls wrote."""
+    size = n_heads * qkv_head_elems(token_tiles, head_dim)
+    q, k, v = out if out is not None else (np.zeros(size, np.uint16) for _ in range(3))
+    raw = np.ascontiguousarray(raw, np.float32)
+    f = (lambda a: None if a is None else np.ascontiguousarray(a, np.float32))
+    lib().oracle_qkv_post(_ptr(q), _ptr(k), _ptr(v), _ptr(raw), _ptr(f(bias)), _ptr(f(q_norm)), _ptr(f(k_norm)),
+                          _ptr(f(pe)), rope_offset, rope_count, tokens, n_heads, head_dim, token_tiles, out_offset)
+    return q, k, v
 
 
 # ---- dequantizing GEMM (opcodes 2/3/4) ----------------------------------------

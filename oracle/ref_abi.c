@@ -33,6 +33,10 @@ size_t ref_abi_size(int which) {
     case 14: return sizeof(struct RpcmemMapRequestV2);
     case 15: return sizeof(struct W8A8CpuBatch);
     case 16: return sizeof(struct NativeAuxParams);
+    case 17: return sizeof(struct QkvMulRmsPackedParams);
+    case 18: return sizeof(struct QkvMulRmsPackedDualParams);
+    case 19: return sizeof(struct QkvMulRmsPackedRopeParams);
+    case 20: return sizeof(struct QkvMulRmsPackedDualRopeParams);
     default: return 0;
   }
 }
@@ -56,6 +60,14 @@ size_t ref_abi_offset(int which) {
     case 14: return offsetof(struct NativeAuxParams, mode);
     case 15: return offsetof(struct NativeAuxParams, eps);
     case 16: return offsetof(struct NativeAuxParams, elapsed_us);
+    case 17: return offsetof(struct QkvMulRmsPackedParams, tokens);
+    case 18: return offsetof(struct QkvMulRmsPackedParams, elapsed_us);
+    case 19: return offsetof(struct QkvMulRmsPackedDualParams, text_activation);
+    case 20: return offsetof(struct QkvMulRmsPackedDualParams, elapsed_us);
+    case 21: return offsetof(struct QkvMulRmsPackedRopeParams, rope_pe);
+    case 22: return offsetof(struct QkvMulRmsPackedRopeParams, rope_token_count);
+    case 23: return offsetof(struct QkvMulRmsPackedDualRopeParams, rope_pe);
+    case 24: return offsetof(struct QkvMulRmsPackedDualRopeParams, text_rope_token_offset);
     default: return (size_t)-1;
   }
 }
@@ -69,8 +81,17 @@ int ref_opcode(int which) {
     case 4: return REQUEST_TYPE_OP_COMPUTE;
     case 5: return REQUEST_TYPE_RPCMEM_MAP;
     case 6: return HTP_OPS_MODEL_AUX_F32;
+    case 7: return HTP_OPS_QKV_MUL_RMS_PACKED_W16A32;
+    case 8: return HTP_OPS_QKV_MUL_RMS_PACKED_DUAL_W16A32;
+    case 9: return HTP_OPS_QKV_MUL_RMS_PACKED_ROPE_W16A32;
+    case 10: return HTP_OPS_QKV_MUL_RMS_PACKED_DUAL_ROPE_W16A32;
     default: return -1;
   }
+}
+
+/* The packed QKV opcodes' head-shape rule. */
+int ref_packed_shape_supported(int n_heads, int n_kv_heads, int head_dim, int require_equal_kv) {
+  return htp_packed_shape_supported(n_heads, n_kv_heads, head_dim, require_equal_kv) ? 1 : 0;
 }
 
 int ref_message_header_validate_layout(const void *h, size_t capacity, size_t *total_size) {

@@ -43,7 +43,7 @@ def ref(orc):
 
 
 EXPECTED_SIZES = {0: 16, 1: 8, 2: 4, 3: 8, 4: 128, 5: 40, 6: 64, 7: 104, 8: 17536, 9: 48, 10: 92, 11: 56,
-                  12: 8, 13: 32, 14: 24, 15: 16, 16: 76}
+                  12: 8, 13: 32, 14: 24, 15: 16, 16: 76, 17: 84, 18: 128, 19: 100, 20: 144}
 
 
 def test_sizes_match_reference(own, ref):
@@ -52,15 +52,31 @@ def test_sizes_match_reference(own, ref):
 
 
 def test_offsets_match_reference(own, ref):
-    for which in range(17):
+    for which in range(25):
         assert own.own_abi_offset(which) == ref.ref_abi_offset(which), which
 
 
 def test_opcodes_match_reference(own, ref):
-    for which in range(7):
+    for which in range(11):
         assert own.own_opcode(which) == ref.ref_opcode(which), which
     assert own.own_opcode(1) == 15 and own.own_opcode(2) == 16 and own.own_opcode(0) == 1
     assert own.own_opcode(6) == 19
+    assert [own.own_opcode(w) for w in (7, 8, 9, 10)] == [8, 10, 11, 12]
+
+
+def test_packed_shape_rule_matches_reference(own, ref):
+    """The head-count / head-dim rule of the QKV opcodes (reference
+    include/op_reg.h:23-39) over a grid around every supported value."""
+    accepted = []
+    for n_heads in range(-1, 41):
+        for head_dim in (-64, 0, 32, 63, 64, 65, 96, 128, 129, 256):
+            for kv in (n_heads, 1, 2, 0):
+                for eq in (0, 1):
+                    a = own.own_packed_shape_supported(n_heads, kv, head_dim, eq)
+                    assert a == ref.ref_packed_shape_supported(n_heads, kv, head_dim, eq), (n_heads, kv, head_dim, eq)
+                    if a and eq:
+                        accepted.append((n_heads, head_dim))
+    assert sorted(set(accepted)) == [(24, 64), (24, 128), (30, 64), (30, 128), (38, 64)]
 
 
 def _validate(lib, fn, raw, capacity):

@@ -152,7 +152,7 @@ def test_matmul_codes(bufs):
     assert h.execute(1, h.matmul_params(*ok, 4, 64, 48))[0] == -11
 
 
-@pytest.mark.parametrize("op", [0, 5, 8, 14, 17, 18, 20, 1000])
+@pytest.mark.parametrize("op", [0, 5, 9, 14, 17, 18, 20, 1000])
 def test_unsupported_opcodes(op):
     assert h.execute(op, bytes(64))[0] == h.E_UNSUPPORTED
 
