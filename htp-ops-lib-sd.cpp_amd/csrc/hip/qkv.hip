@@ -54,70 +54,90 @@ __device__ inline int block_index(int r, int c) {
 }
 
 // One workgroup per (32-token tile, head) of one of Q / K / V (WHICH 0 / 1 / 2).
+// Every load of the tile (rows, bias, gamma, rotary matrices) is issued
+// before the arithmetic: one round of 4 row pairs per wave keeps enough
+// bytes in flight to stream from HBM.
 template <int HD, int WHICH>
 __device__ void qkv_block(uint16_t *__restrict__ dst, const float *__restrict__ raw, const float *__restrict__ bias,
                           const float *__restrict__ gamma, const float *__restrict__ pe, int rope_off, int rope_count,
                           int tokens, int ncols, int col0, int t0, int tt, int token_tiles, size_t head_base) {
   constexpr int CH = HD / 64;  // 64-column chunks; lane j holds columns 64d+j and 64d+32+j
+  constexpr int E = 2 * CH;    // values per lane and row
+  constexpr int PAIRS = 16 / (kQkvThreads / 64);
+  constexpr bool ROPE_OK = WHICH < 2;
   __shared__ __attribute__((aligned(16))) uint16_t blk[HD * 32];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int half = lane >> 5, j = lane & 31;
   const int rows = min(32, tokens - t0);
-#pragma unroll 1
-  for (int p = wave; p < 16; p += kQkvThreads / 64) {
-    const int r = 2 * p + half;
-    float v[2 * CH] = {};
-    if (r < rows) {
-      const float *x = raw + (size_t)(t0 + r) * (size_t)ncols + col0;
+  auto col = [&](int e) { return 64 * (e >> 1) + 32 * (e & 1) + j; };
+
+  float v[PAIRS][E];
 #pragma unroll
-      for (int d = 0; d < CH; ++d) {
-        v[2 * d] = __fadd_rn(x[64 * d + j], bias ? bias[col0 + 64 * d + j] : 0.0f);
-        v[2 * d + 1] = __fadd_rn(x[64 * d + 32 + j], bias ? bias[col0 + 64 * d + 32 + j] : 0.0f);
+  for (int i = 0; i < PAIRS; ++i) {
+    const int r = 2 * (wave + 4 * i) + half;
+    const float *x = raw + (size_t)(t0 + r) * (size_t)ncols + col0;
+#pragma unroll
+    for (int e = 0; e < E; ++e) v[i][e] = r < rows ? x[col(e)] : 0.0f;
+  }
+  float b[E], g[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    b[e] = bias ? bias[col0 + col(e)] : 0.0f;
+    g[e] = WHICH < 2 ? gamma[col(e)] : 0.0f;
+  }
+  // rotary matrices (x0, x1 -> m.x x0 + m.y x1, m.z x0 + m.w x1) of each row's token
+  float4 m[ROPE_OK ? PAIRS : 1][ROPE_OK ? E : 1];
+  bool rot[PAIRS];
+#pragma unroll
+  for (int i = 0; i < PAIRS; ++i) {
+    const int r = 2 * (wave + 4 * i) + half;
+    const int token = rope_off + t0 + r;
+    rot[i] = ROPE_OK && pe && r < rows && token < rope_count;
+    if (ROPE_OK) {
+#pragma unroll
+      for (int e = 0; e < E; ++e)
+        m[i][e] = rot[i] ? *(const float4 *)(pe + ((size_t)token * (HD / 2) + (size_t)(col(e) >> 1)) * 4u)
+                         : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+
+#pragma unroll
+  for (int i = 0; i < PAIRS; ++i) {
+    const int r = 2 * (wave + 4 * i) + half;
+#pragma unroll
+    for (int e = 0; e < E; ++e) v[i][e] = __fadd_rn(v[i][e], b[e]);
+    if (WHICH < 2) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int e = 0; e < E; ++e) acc = __fadd_rn(acc, __fmul_rn(v[i][e], v[i][e]));
+      // lane i += lane i - s within the 32 lanes of the row, s = 16 .. 1
+#pragma unroll
+      for (int s = 16; s >= 1; s >>= 1) {
+        const float o = __shfl(acc, (lane - s) & 63, 64);
+        if (j >= s) acc = __fadd_rn(acc, o);
       }
-      if (WHICH < 2) {
-        float acc = 0.0f;
+      const float sum = __shfl(acc, half * 32 + 31, 64);
+      const float inv = qkv_rsqrt(__fadd_rn(__fdiv_rn(sum, (float)HD), 1.0e-6f));
 #pragma unroll
-        for (int d = 0; d < CH; ++d) {
-          acc = __fadd_rn(acc, __fmul_rn(v[2 * d], v[2 * d]));
-          acc = __fadd_rn(acc, __fmul_rn(v[2 * d + 1], v[2 * d + 1]));
-        }
-        // lane i += lane i - s within the 32 lanes of the row, s = 16 .. 1
+      for (int e = 0; e < E; ++e) v[i][e] = __fmul_rn(__fmul_rn(v[i][e], inv), g[e]);
+      if (pe) {
+        // the pair of column c is c ^ 1, held by lane j ^ 1
 #pragma unroll
-        for (int s = 16; s >= 1; s >>= 1) {
-          const float o = __shfl(acc, (lane - s) & 63, 64);
-          if (j >= s) acc = __fadd_rn(acc, o);
-        }
-        const float sum = __shfl(acc, half * 32 + 31, 64);
-        const float inv = qkv_rsqrt(__fadd_rn(__fdiv_rn(sum, (float)HD), 1.0e-6f));
-#pragma unroll
-        for (int d = 0; d < CH; ++d) {
-          v[2 * d] = __fmul_rn(__fmul_rn(v[2 * d], inv), gamma[64 * d + j]);
-          v[2 * d + 1] = __fmul_rn(__fmul_rn(v[2 * d + 1], inv), gamma[64 * d + 32 + j]);
+        for (int e = 0; e < E; ++e) {
+          const float other = __shfl(v[i][e], lane ^ 1, 64);
+          if (rot[i]) {
+            const bool odd = j & 1;
+            const float x0 = odd ? other : v[i][e], x1 = odd ? v[i][e] : other;
+            const float4 mm = m[i][ROPE_OK ? e : 0];
+            v[i][e] = odd ? __fadd_rn(__fmul_rn(x0, mm.z), __fmul_rn(x1, mm.w))
+                          : __fadd_rn(__fmul_rn(x0, mm.x), __fmul_rn(x1, mm.y));
+          }
         }
       }
     }
-    // rotary: the pair of column c is c ^ 1, held by lane j ^ 1 (whole waves
-    // take part in the exchange; rows past the count are left as they are)
-    if (WHICH < 2 && pe) {
-      const int token = rope_off + t0 + r;
-      const bool rot = r < rows && token < rope_count;
 #pragma unroll
-      for (int e = 0; e < 2 * CH; ++e) {
-        const float other = __shfl(v[e], lane ^ 1, 64);
-        if (rot) {
-          const int c = 64 * (e >> 1) + 32 * (e & 1) + j;
-          const float4 m = *(const float4 *)(pe + ((size_t)token * (HD / 2) + (size_t)(c >> 1)) * 4u);
-          const float x0 = (c & 1) ? other : v[e], x1 = (c & 1) ? v[e] : other;
-          v[e] = (c & 1) ? __fadd_rn(__fmul_rn(x0, m.z), __fmul_rn(x1, m.w))
-                         : __fadd_rn(__fmul_rn(x0, m.x), __fmul_rn(x1, m.y));
-        }
-      }
-    }
-#pragma unroll
-    for (int e = 0; e < 2 * CH; ++e) {
-      const int c = 64 * (e >> 1) + 32 * (e & 1) + j;
-      blk[block_index<WHICH>(r, c)] = r < rows ? __half_as_ushort(__float2half_rn(v[e])) : (uint16_t)0;
-    }
+    for (int e = 0; e < E; ++e)
+      blk[block_index<WHICH>(r, col(e))] = r < rows ? __half_as_ushort(__float2half_rn(v[i][e])) : (uint16_t)0;
   }
   __syncthreads();
   const uint4 *src = (const uint4 *)blk;
