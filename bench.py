@@ -44,6 +44,7 @@ import htp_ops as hip  # noqa: E402
 METRIC = "W8A8 INT8 TOPS & %MFMA peak (M=4096,K=1536,N=6144); M=1 decode HBM GB/s"
 PEAK_INT8_TOPS = 5000.0   # MI355X dense INT8 MFMA
 PEAK_HBM_GBPS = 8000.0    # MI355X HBM3E
+PEAK_F16_TFLOPS = 2500.0  # MI355X dense FP16 MFMA
 HEADLINE = (4096, 1536, 6144)
 SETTLE_MS = 80.0          # untimed GPU time before each timed sequence (clock ramp)
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "w8a8_gemm_stream_4096x1536x6144_traffic.md")
@@ -603,6 +604,108 @@ def aux_cases(steps, warmup, rotate=4, with_cpu=True):
     return out
 
 
+def qkv_cases(steps, warmup, with_cpu=True):
+    """Opcode 12 (dual fused QKV + RMS norm + RoPE, packed fp16 outputs) at
+    joint-attention shapes: image 256 + text 4096 tokens, input 1536.  The
+    request runs through execute_op_simple on HBM-resident rpcmem buffers
+    (mean over `steps` requests after `warmup`); its two kernels are timed
+    alone on the text part (HIP events around `steps` launches each).
+    Post-processing bytes are algorithmic: the GEMM output read once (f32),
+    the rotary matrices of the rows read once, three packed fp16 images
+    written once."""
+    import struct
+    lib = hip.lib()
+    stream = hip.default_stream()
+    rng = np.random.default_rng(12)
+    out = {}
+    for n_heads, hd in ((24, 64), (24, 128)):
+        image, text, k = 256, 4096, 1536
+        tokens = image + text
+        cols = 3 * n_heads * hd
+        tiles = (tokens + 31) // 32
+        name = f"qkv_dual_rope_{image}+{text}x{k}_{n_heads}x{hd}"
+        act = rng.standard_normal((tokens, k), dtype=np.float32)
+        w = (rng.standard_normal((k, cols), dtype=np.float32) * 0.03).astype(np.float16)
+        perm = hip.permute_f16(w.view(np.uint16))
+        bias = rng.standard_normal(cols, dtype=np.float32) * 0.1
+        qn = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+        kn = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+        ang = rng.uniform(-3, 3, (tokens, hd // 2))
+        pe = np.stack([np.cos(ang), -np.sin(ang), np.sin(ang), np.cos(ang)], -1).astype(np.float32).ravel()
+        qkv_bytes = n_heads * tiles * (hd // 32) * 1024 * 2
+        pieces = [("act", act), ("w", perm), ("bias", bias), ("qn", qn), ("kn", kn), ("pe", pe)]
+        offs, pos = {}, 0
+        for key, arr in pieces:
+            offs[key] = pos
+            pos = (pos + arr.nbytes + 255) // 256 * 256
+        for key in ("q", "k", "v"):
+            offs[key] = pos
+            pos = (pos + qkv_bytes + 255) // 256 * 256
+        buf = hip.RpcBuffer(pos, device=True)
+        for key, arr in pieces:
+            buf.write(arr, offs[key])
+        a = {key: (buf.fd, o) for key, o in offs.items()}
+        img = (a["act"], a["w"], a["bias"], a["qn"], a["kn"])
+        txt = ((buf.fd, offs["act"] + image * k * 4), a["w"], a["bias"], a["qn"], a["kn"])
+        payload = hip.qkv_dual_rope_params(a["q"], a["k"], a["v"], img, txt, a["pe"], image, text, k, n_heads, hd,
+                                           0, image)
+        for _ in range(max(warmup // 10, 3)):
+            rc, _ = hip.execute(12, payload)
+            assert rc == 0, hip.last_error()
+        hip.sync()
+        n_req = max(steps // 10, 10)
+        elapsed = []
+        t0 = time.perf_counter()
+        for _ in range(n_req):
+            rc, after = hip.execute(12, payload)
+            elapsed.append(struct.unpack_from("<i", after, len(after) - 4)[0])
+        hip.sync()
+        wall_us = (time.perf_counter() - t0) / n_req * 1e6
+        # the two kernels alone on the text part
+        m = text
+        packed = hip.f16_prepack(hip.DeviceBuffer.from_array(perm), k, cols)
+        x = hip.DeviceBuffer.from_array(act[image:])
+        y = hip.DeviceBuffer(m * cols * 4)
+        ws = hip.DeviceBuffer(max(hip.f16_workspace_bytes(m, k, cols), 1))
+        outs = [hip.DeviceBuffer(qkv_bytes) for _ in range(3)]
+        bd, qd, kd, ped = (hip.DeviceBuffer.from_array(v) for v in (bias, qn, kn, pe))
+
+        def gemm(i):
+            hip.f16_gemm(y, x, packed, None, m, k, cols, cols, 0, stream=stream, workspace=ws)
+
+        def post(i):
+            hip.qkv_post(*outs, y, bd, qd, kd, ped, image, tokens, m, n_heads, hd, tiles, image, stream=stream)
+
+        gemm_us = _timed_graph_us(gemm, steps, warmup, stream)
+        post_us = _timed_graph_us(post, steps, warmup, stream)
+        post_bytes = m * cols * 4 + m * (hd // 2) * 16 + 3 * ((m + 31) // 32 * 32) * n_heads * hd * 2
+        flops = 2.0 * m * k * cols
+        out[name] = {
+            "op12_us_wall": round(wall_us, 1), "op12_elapsed_us_median": int(np.median(elapsed)),
+            "gemm_us": round(gemm_us, 2), "gemm_tflops": round(flops / gemm_us * 1e-6, 1),
+            "gemm_frac_fp16_mfma": round(flops / gemm_us * 1e-6 / PEAK_F16_TFLOPS, 4),
+            "post_us": round(post_us, 2), "post_gbps": round(post_bytes / post_us * 1e-3, 1),
+            "post_frac_hbm": round(post_bytes / post_us * 1e-3 / PEAK_HBM_GBPS, 4),
+            "post_algorithmic_bytes": post_bytes}
+        if with_cpu and n_heads == 24 and hd == 64:
+            # the oracle's restatement (GEMM + post-processing) of the image
+            # part, single-threaded
+            sys.path.insert(0, os.path.join(REPO, "oracle"))
+            import oracle
+            t0 = time.perf_counter()
+            raw = oracle.f16_gemm_epilogue(act[:image], perm, None, image, k, cols, cols, 0, nthreads=1)
+            oracle.qkv_post(raw, bias, qn, kn, pe, 0, tokens, image, n_heads, hd, tiles)
+            cpu_s = time.perf_counter() - t0
+            out[name]["cpu_baseline"] = {"us_per_token": round(cpu_s / image * 1e6, 1), "cores": 1, "kind": "port",
+                                         "sample": f"image part: {image} tokens (GEMM {image}x{k}x{cols} + "
+                                                   f"post-processing)",
+                                         "gpu_us_per_token": round(wall_us / tokens, 3)}
+        for b in (packed, x, y, ws, *outs, bd, qd, kd, ped):
+            b.free()
+        buf.free()
+    return out
+
+
 def f16_mlp_case(steps, warmup, m=77, k=768, n=3072, rotate=6):
     """opcode-16 F16 GEMM 77x768 -> 3072 with bias +
     QuickGELU, then 3072 -> 768 with bias (text-encoder MLP block); FP32
@@ -762,9 +865,9 @@ def main():
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--rotate", type=int, default=6)
-    ap.add_argument("--config", default="headline", choices=["headline", "all", "small", "aux", "qk0"],
-                    help="small / aux / qk0: only the C1 W8A8 and C2 F16 text-MLP cases / the opcode-19 cases / "
-                         "the opcode-2/3/4 cases (profiling aids; print those cases alone)")
+    ap.add_argument("--config", default="headline", choices=["headline", "all", "small", "aux", "qk0", "qkv"],
+                    help="small / aux / qk0 / qkv: only the C1 W8A8 and C2 F16 text-MLP cases / the opcode-19 "
+                         "cases / the opcode-2/3/4 cases / the opcode-12 fused QKV cases (print those cases alone)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true",
                     help="no HIP graph capture or replay (every timing stream-ordered); for profiler-traced runs")
@@ -802,6 +905,10 @@ def main():
         return
     if args.config == "qk0":
         print(json.dumps({"opcodes_2_3_4_qk0": qk0_cases(args.steps, args.warmup)}), flush=True)
+        return
+    if args.config == "qkv":
+        print(json.dumps({"opcodes_8_10_11_12_qkv": qkv_cases(args.steps, args.warmup, with_cpu=not args.no_cpu)}),
+              flush=True)
         return
     if args.config == "all" and args.only:
         print(json.dumps({"configs": all_configs(args.steps, args.warmup, with_cpu=not args.no_cpu,

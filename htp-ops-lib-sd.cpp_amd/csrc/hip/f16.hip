@@ -943,7 +943,12 @@ size_t a_image_bytes(int m, int k) { return hb_round_up((size_t)((m + 15) / 16 *
 // The ring path pays one extra launch (f16_pack_a); it is used from 4 GFLOP
 // of work with at least 64 rows (measured: 77x4096x14336 74 -> 29 us,
 // 2048x4096x14336 613 -> 250 us, 4096x1536x6144 212 -> 89 us).
-bool ring_worth_it(int m, int k, int n) { return m >= 64 && 2.0 * m * (double)n * k >= 4e9; }
+// The ring kernel above 128 rows at any size: against the tiled kernels it
+// measured equal or faster everywhere (256x1536x4608 30.4 -> 15.1 us,
+// 512x1536x1536 30.7 -> 14.9 us, 256x768x3072 14.4 -> 9.8 us).  From 64 to
+// 128 rows only from 4 GFLOP, below which the one-launch small kernel and the
+// split-K path keep those shapes.
+bool ring_worth_it(int m, int k, int n) { return m >= 64 && (m > 128 || 2.0 * m * (double)n * k >= 4e9); }
 
 // Ring tile shapes, cheapest (rounds of resident workgroups) x (work per
 // round per CU) / measured efficiency; 128x192 only when n allows.

@@ -413,7 +413,7 @@ static int exec_w8a8(uint8_t *payload, size_t payload_size) {
   }
   const double weight_s = built ? t_w1 - t_w0 : 0.0;
   if (!split && out.is_device) {
-    htp_registry_touch(out.fd);
+    htp_registry_touch(out.fd, out.offset, out.bytes);
     return complete(&ev, 0, 3, payload + offsetof(struct NativeW8A8Params, elapsed_us), weight_s * 1e6, 1);
   }
   if (hb_stream_sync(s) != HB_OK) {
@@ -453,7 +453,7 @@ static int exec_w8a8(uint8_t *payload, size_t payload_size) {
     if (crc) return -5;
   }
   if (stage_out(&out, s)) return -5;
-  htp_registry_touch(out.fd);
+  htp_registry_touch(out.fd, out.offset, out.bytes);
 
   const double total_us = (quant_ms + gemm_ms + out_ms) * 1e3 + weight_s * 1e6;
   p.elapsed_us = (int32_t)total_us;
@@ -542,7 +542,7 @@ static int run_f16(int kind, int qk0_type, htp_view *out, htp_view *act, htp_vie
     events_close(&ev);
     return hrc == HB_E_INVAL ? -11 : -5;
   }
-  htp_registry_touch(out->fd);
+  htp_registry_touch(out->fd, out->offset, out->bytes);
   const double extra_us = built ? (t_w1 - t_w0) * 1e6 : 0.0;
   if (complete(&ev, 0, 1, elapsed_dst, extra_us, out->is_device)) return -5;
   if (stage_out(out, s)) return -5;
@@ -767,7 +767,7 @@ static int run_qkv(htp_view out[3], qkv_part *parts, int n_parts, htp_view *pe, 
     events_close(&ev);
     return hrc == HB_E_INVAL ? -1 : -5;
   }
-  for (int i = 0; i < 3; ++i) htp_registry_touch(out[i].fd);
+  for (int i = 0; i < 3; ++i) htp_registry_touch(out[i].fd, out[i].offset, out[i].bytes);
   const int device_outputs = out[0].is_device && out[1].is_device && out[2].is_device;
   if (complete(&ev, 0, 1, elapsed_dst, extra_us, device_outputs)) return -5;
   for (int i = 0; i < 3; ++i)
@@ -999,7 +999,7 @@ static int exec_model_aux(uint8_t *payload, size_t payload_size) {
     events_close(&ev);
     return hrc == HB_E_INVAL ? -1 : -5;
   }
-  htp_registry_touch(out.fd);
+  htp_registry_touch(out.fd, out.offset, out.bytes);
   if (complete(&ev, 0, 1, payload + offsetof(struct NativeAuxParams, elapsed_us), 0.0, out.is_device)) return -5;
   return stage_out(&out, s) ? -5 : 0;
 }

@@ -32,8 +32,9 @@ int htp_registry_host_view(int fd, int64_t offset, size_t bytes, htp_view *out);
 /* Drops the device mirror and every cached prepacked weight of an fd (map "put"). */
 int htp_registry_put(int fd);
 int htp_registry_known(int fd);
-/* Monotonic counter bumped whenever the library writes into the fd. */
-void htp_registry_touch(int fd);
+/* Records a library write of [offset, offset + bytes) of fd: cached weight
+ * images built from overlapping bytes become stale. */
+void htp_registry_touch(int fd, size_t offset, size_t bytes);
 
 /* ---- prepacked weight cache (registry.c) -------------------------------- */
 

@@ -255,10 +255,21 @@ int htp_registry_known(int fd) {
   return known;
 }
 
-void htp_registry_touch(int fd) {
+/* Marks stale every cached image built from bytes of fd that overlap
+ * [offset, offset + bytes): their next lookup rebuilds them.  Images of the
+ * fd's other ranges stay valid, so one buffer may hold weights, activations
+ * and outputs (as the reference's own tests lay them out) without a rebuild
+ * per call. */
+static void stale_range_locked(int fd, size_t offset, size_t bytes) {
+  for (size_t i = 0; i < g_cache_count; ++i) {
+    cache_entry *c = &g_cache[i];
+    if (c->fd == fd && c->offset < offset + bytes && offset < c->offset + c->bytes) c->generation = 0;
+  }
+}
+
+void htp_registry_touch(int fd, size_t offset, size_t bytes) {
   pthread_mutex_lock(&g_lock);
-  reg_entry *e = find_fd_locked(fd);
-  if (e) e->generation = g_generation++;
+  stale_range_locked(fd, offset, bytes);
   pthread_mutex_unlock(&g_lock);
 }
 
@@ -306,7 +317,7 @@ int htp_ops_amd_buffer_write(int fd, size_t offset, const void *src, size_t byte
       memcpy(e->host + offset, src, bytes);
       rc = 0;
     }
-    e->generation = g_generation++;
+    stale_range_locked(fd, (size_t)offset, bytes);
   }
   pthread_mutex_unlock(&g_lock);
   return rc;
