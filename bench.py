@@ -676,8 +676,16 @@ def qkv_cases(steps, warmup, with_cpu=True):
         def post(i):
             hip.qkv_post(*outs, y, bd, qd, kd, ped, image, tokens, m, n_heads, hd, tiles, image, stream=stream)
 
+        fws = hip.DeviceBuffer(hip.qkv_gemm_workspace_bytes(m, k))
+        xt = hip.DeviceBuffer.from_array(act[image:])
+
+        def fused(i):
+            hip.qkv_gemm(*outs, xt, packed, bd, qd, kd, ped, image, tokens, m, k, n_heads, hd, tiles, image, fws,
+                         stream=stream)
+
         gemm_us = _timed_graph_us(gemm, steps, warmup, stream)
         post_us = _timed_graph_us(post, steps, warmup, stream)
+        fused_us = _timed_graph_us(fused, steps, warmup, stream)
         post_bytes = m * cols * 4 + m * (hd // 2) * 16 + 3 * ((m + 31) // 32 * 32) * n_heads * hd * 2
         flops = 2.0 * m * k * cols
         out[name] = {
@@ -686,7 +694,7 @@ def qkv_cases(steps, warmup, with_cpu=True):
             "gemm_frac_fp16_mfma": round(flops / gemm_us * 1e-6 / PEAK_F16_TFLOPS, 4),
             "post_us": round(post_us, 2), "post_gbps": round(post_bytes / post_us * 1e-3, 1),
             "post_frac_hbm": round(post_bytes / post_us * 1e-3 / PEAK_HBM_GBPS, 4),
-            "post_algorithmic_bytes": post_bytes}
+            "post_algorithmic_bytes": post_bytes, "fused_gemm_post_us": round(fused_us, 2)}
         if with_cpu and n_heads == 24 and hd == 64:
             # the oracle's restatement (GEMM + post-processing) of the image
             # part, single-threaded
@@ -700,7 +708,7 @@ def qkv_cases(steps, warmup, with_cpu=True):
                                          "sample": f"image part: {image} tokens (GEMM {image}x{k}x{cols} + "
                                                    f"post-processing)",
                                          "gpu_us_per_token": round(wall_us / tokens, 3)}
-        for b in (packed, x, y, ws, *outs, bd, qd, kd, ped):
+        for b in (packed, x, y, ws, *outs, bd, qd, kd, ped, fws, xt):
             b.free()
         buf.free()
     return out

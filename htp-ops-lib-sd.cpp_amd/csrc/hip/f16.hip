@@ -13,6 +13,7 @@
 #include <type_traits>
 
 #include "hb_internal.h"
+#include "qkv_post.h"
 
 namespace {
 
@@ -300,11 +301,14 @@ __global__ __launch_bounds__(256) void f16_pack_a(uint4 *__restrict__ img, const
   }
 }
 
+// The k loop of the ring kernels: tile (m0, n0) of the product into acc (the
+// MFMA layout: lane l holds rows 4*(l/16)..+3 and column l%16 of each 16x16
+// block of this wave's WTM x WTN sub-tile).  On return every operand stage
+// has been consumed, so the caller may reuse the LDS after a barrier.
 template <int BM, int BN, int WM, int WN, int S>
-__global__ __launch_bounds__(64 * WM *WN) void f16_gemm_ring(float *__restrict__ y, const int8_t *__restrict__ aimg,
-                                                             const int8_t *__restrict__ wpack,
-                                                             const float *__restrict__ bias, int m, int k, int n,
-                                                             int mode) {
+__device__ inline void ring_mainloop(hb_f32x4 (&acc)[BM / WM / 16][BN / WN / 16], int8_t *lds,
+                                     const int8_t *__restrict__ aimg, const int8_t *__restrict__ wpack, int m, int k,
+                                     int n, int m0, int n0, int wave, int lane) {
   constexpr int NW = WM * WN;
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int FM = WTM / 16, FN = WTN / 16;
@@ -314,14 +318,7 @@ __global__ __launch_bounds__(64 * WM *WN) void f16_gemm_ring(float *__restrict__
   constexpr int PW_LO = NB / NW;
   static_assert(PW_LO >= 1, "every wave takes part in the DMA");
   constexpr int STAGE = NB * kFragBytes;
-  __shared__ __attribute__((aligned(1024))) int8_t lds[S * STAGE];
-
-  const int tiles_m = (m + BM - 1) / BM, tiles_n = (n + BN - 1) / BN;
-  int tm, tn;
-  tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
-  const int m0 = tm * BM, n0 = tn * BN;
   const int kt_count = k / 32;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int wm = wave / WN, wn = wave % WN;
 
   const int8_t *src[PW];
@@ -340,7 +337,6 @@ __global__ __launch_bounds__(64 * WM *WN) void f16_gemm_ring(float *__restrict__
     stride[i] = kFragBytes;
   }
 
-  hb_f32x4 acc[FM][FN];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -370,6 +366,27 @@ __global__ __launch_bounds__(64 * WM *WN) void f16_gemm_ring(float *__restrict__
       for (int j = 0; j < FN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[j], acc[i][j], 0, 0, 0);
     }
   }
+}
+
+template <int BM, int BN, int WM, int WN, int S>
+__global__ __launch_bounds__(64 * WM *WN) void f16_gemm_ring(float *__restrict__ y, const int8_t *__restrict__ aimg,
+                                                             const int8_t *__restrict__ wpack,
+                                                             const float *__restrict__ bias, int m, int k, int n,
+                                                             int mode) {
+  constexpr int NW = WM * WN;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int FM = WTM / 16, FN = WTN / 16;
+  constexpr int STAGE = (BM / 16 + BN / 16) * kFragBytes;
+  __shared__ __attribute__((aligned(1024))) int8_t lds[S * STAGE];
+
+  const int tiles_m = (m + BM - 1) / BM, tiles_n = (n + BN - 1) / BN;
+  int tm, tn;
+  tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int wm = wave / WN, wn = wave % WN;
+  hb_f32x4 acc[FM][FN];
+  ring_mainloop<BM, BN, WM, WN, S>(acc, lds, aimg, wpack, m, k, n, m0, n0, wave, lane);
 
   // Epilogue: fp16 readout, bias, activation, then each 16-row chunk staged
   // in wave-private padded LDS and written as 16-byte vectors along rows.
@@ -401,6 +418,84 @@ __global__ __launch_bounds__(64 * WM *WN) void f16_gemm_ring(float *__restrict__
         const hb_f32x4 val = *(const hb_f32x4 *)(stg + r * SROW + c4 * 4);
         __builtin_nontemporal_store(val, (hb_f32x4 *)(y + (size_t)row * n + col));
       }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Opcodes 8/10/11/12 with the post-processing in the GEMM epilogue: the ring
+// kernel's 128 x BN tile (whole heads: BN = 192, three heads of 64; BN = 128,
+// one head of 128 or two of 64; all of Q, K or V, since heads * HD is a
+// multiple of BN) is read out to fp16 exactly as f16_gemm_ring reads it out
+// (mode 0, no bias), kept in LDS as fp16 (the values are fp16-exact) instead
+// of going to HBM as f32, and each (32-token tile, head) of it goes through
+// qkv_block, the standalone post-processing kernel's code.  Results are
+// identical to f16_gemm_ring followed by qkv_post.
+// ---------------------------------------------------------------------------
+
+template <int HD, int BN>
+__global__ __launch_bounds__(256) void f16_qkv_ring(uint16_t *__restrict__ q, uint16_t *__restrict__ k,
+                                                    uint16_t *__restrict__ v, const int8_t *__restrict__ aimg,
+                                                    const int8_t *__restrict__ wpack, const float *__restrict__ bias,
+                                                    const float *__restrict__ q_norm,
+                                                    const float *__restrict__ k_norm, const float *__restrict__ pe,
+                                                    int rope_off, int rope_count, int m, int kdim, int n_heads,
+                                                    int token_tiles, int out_tile0) {
+  constexpr int BM = 128, WM = 2, WN = 2, S = 4;
+  static_assert(BN % HD == 0, "whole heads per tile");
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int FM = WTM / 16, FN = WTN / 16;
+  constexpr int STAGE = (BM / 16 + BN / 16) * kFragBytes;
+  constexpr int TS = BN + 8;  // halfwords per LDS row of the tile (padded)
+  constexpr int TILE_BYTES = BM * TS * 2;
+  constexpr int POST_BYTES = TILE_BYTES + HD * 32 * 2;  // the tile, then one packed block
+  static_assert(kQkvThreads == 64 * WM * WN, "the post-processing uses the GEMM's 256 threads");
+  __shared__ __attribute__((aligned(1024))) int8_t lds[S * STAGE > POST_BYTES ? S * STAGE : POST_BYTES];
+  uint16_t *blk = (uint16_t *)(lds + TILE_BYTES);
+
+  const int q_cols = n_heads * HD, n = 3 * q_cols;
+  const int tiles_m = (m + BM - 1) / BM, tiles_n = n / BN;
+  int tm, tn;
+  tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int wm = wave / WN, wn = wave % WN;
+  hb_f32x4 acc[FM][FN];
+  ring_mainloop<BM, BN, WM, WN, S>(acc, lds, aimg, wpack, m, kdim, n, m0, n0, wave, lane);
+
+  block_barrier();  // every wave is done with the operand stages: LDS holds the tile
+  _Float16 *tile = (_Float16 *)lds;
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        tile[(wm * WTM + i * 16 + (lane >> 4) * 4 + r) * TS + wn * WTN + j * 16 + (lane & 15)] =
+            (_Float16)acc[i][j][r];
+  __syncthreads();
+
+  const int which = n0 / q_cols, head0 = (n0 % q_cols) / HD;
+  uint16_t *dst = which == 0 ? q : which == 1 ? k : v;
+  const int rows_tile = min(BM, m - m0);
+  for (int t = 0; t < BM / 32 && 32 * t < rows_tile; ++t) {
+    const int rows = min(32, rows_tile - 32 * t);
+    const int tt = out_tile0 + m0 / 32 + t;
+#pragma unroll
+    for (int h = 0; h < BN / HD; ++h) {
+      const size_t head_base = (size_t)(head0 + h) * (size_t)token_tiles * (HD / 32) * 1024;
+      const _Float16 *src = tile + 32 * t * TS + h * HD;
+      const float *b = bias ? bias + n0 + h * HD : nullptr;
+      if (which == 0)
+        qkv_block<HD, 0>(blk, dst, src, TS, b, q_norm, pe, rope_off, rope_count, rows, m0 + 32 * t, tt, token_tiles,
+                         head_base);
+      else if (which == 1)
+        qkv_block<HD, 1>(blk, dst, src, TS, b, k_norm, pe, rope_off, rope_count, rows, m0 + 32 * t, tt, token_tiles,
+                         head_base);
+      else
+        qkv_block<HD, 2>(blk, dst, src, TS, b, nullptr, nullptr, 0, 0, rows, m0 + 32 * t, tt, token_tiles,
+                         head_base);
+      __syncthreads();  // the block's LDS staging is reused by the next one
     }
   }
 }
@@ -1206,6 +1301,51 @@ int hb_f16_gemm_ws(float *d_y, const float *d_x, const uint16_t *d_packed, const
 int hb_f16_gemm(float *d_y, const float *d_x, const uint16_t *d_packed, const float *d_bias, int m, int k, int n,
                 int channels, int mode, hb_stream s) {
   return hb_f16_gemm_ws(d_y, d_x, d_packed, d_bias, m, k, n, channels, mode, nullptr, 0, s);
+}
+
+
+size_t hb_qkv_gemm_workspace_bytes(int tokens, int input_dim) {
+  if (tokens < 1 || input_dim < 32) return 0;
+  return a_image_bytes(tokens, input_dim);
+}
+
+int hb_qkv_gemm(uint16_t *d_q, uint16_t *d_k, uint16_t *d_v, const float *d_x, const uint16_t *d_packed,
+                const float *d_bias, const float *d_q_norm, const float *d_k_norm, const float *d_pe, int rope_offset,
+                int rope_count, int tokens, int input_dim, int n_heads, int head_dim, int token_tiles, int out_offset,
+                void *d_workspace, size_t workspace_bytes, hb_stream s) {
+  if (!d_q || !d_k || !d_v || !d_x || !d_packed || !d_q_norm || !d_k_norm || !d_workspace)
+    return hb_invalid("hb_qkv_gemm null pointer");
+  if (tokens <= 0 || input_dim < 32 || input_dim % 32 || n_heads <= 0 || (head_dim != 64 && head_dim != 128) ||
+      (n_heads * head_dim) % 128 || out_offset < 0 || out_offset % 32 ||
+      out_offset / 32 + (tokens + 31) / 32 > token_tiles)
+    return hb_invalid("hb_qkv_gemm shape");
+  if (workspace_bytes < a_image_bytes(tokens, input_dim)) return hb_invalid("hb_qkv_gemm workspace too small");
+  if (!aligned(d_q, 16) || !aligned(d_k, 16) || !aligned(d_v, 16) || !aligned(d_x, 16) || !aligned(d_packed, 16) ||
+      !aligned(d_workspace, 256) || (d_bias && !aligned(d_bias, 4)) || (d_pe && !aligned(d_pe, 16)))
+    return hb_invalid("hb_qkv_gemm alignment");
+  if (d_pe && (rope_offset < 0 || rope_count <= 0)) d_pe = nullptr;  // the reference skips the rotation
+  hipStream_t st = hb_resolve_stream(s);
+  const int m = tokens, k = input_dim, n = 3 * n_heads * head_dim;
+  const int mp = (m + 15) / 16 * 16;
+  const size_t slots = (size_t)mp * k / 8u;
+  const int pg = (int)((slots + 255) / 256 < 65536 ? (slots + 255) / 256 : 65536);
+  hipLaunchKernelGGL(f16_pack_a, dim3(pg), dim3(256), 0, st, (uint4 *)d_workspace, d_x, m, k, mp);
+  int rc = hb_check_launch("f16_pack_a");
+  if (rc) return rc;
+  // 128 x 192 tiles (three heads of 64) where the heads allow, else 128 x 128
+  const int bn = head_dim == 64 && (n_heads * head_dim) % 192 == 0 ? 192 : 128;
+  const int grid = ((m + 127) / 128) * (n / bn);
+  const int8_t *a = (const int8_t *)d_workspace, *w = (const int8_t *)d_packed;
+  if (bn == 192)
+    hipLaunchKernelGGL((f16_qkv_ring<64, 192>), dim3(grid), dim3(256), 0, st, d_q, d_k, d_v, a, w, d_bias, d_q_norm,
+                       d_k_norm, d_pe, rope_offset, rope_count, m, k, n_heads, token_tiles, out_offset / 32);
+  else if (head_dim == 64)
+    hipLaunchKernelGGL((f16_qkv_ring<64, 128>), dim3(grid), dim3(256), 0, st, d_q, d_k, d_v, a, w, d_bias, d_q_norm,
+                       d_k_norm, d_pe, rope_offset, rope_count, m, k, n_heads, token_tiles, out_offset / 32);
+  else
+    hipLaunchKernelGGL((f16_qkv_ring<128, 128>), dim3(grid), dim3(256), 0, st, d_q, d_k, d_v, a, w, d_bias,
+                       d_q_norm, d_k_norm, d_pe, rope_offset, rope_count, m, k, n_heads, token_tiles, out_offset / 32);
+  return hb_check_launch("f16_qkv_ring");
 }
 
 }  // extern "C"

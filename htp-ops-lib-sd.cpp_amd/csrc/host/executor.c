@@ -713,18 +713,27 @@ static int run_qkv(htp_view out[3], qkv_part *parts, int n_parts, htp_view *pe, 
     if (rc) return rc;
     if (built) extra_us += (now_seconds() - t0) * 1e6;
   }
-  int max_tokens = 0;
-  for (int i = 0; i < n_parts; ++i) max_tokens = parts[i].tokens > max_tokens ? parts[i].tokens : max_tokens;
-  float *raw = (float *)htp_executor_scratch(1, (size_t)max_tokens * (size_t)ncols * sizeof(float));
+
+  /* A part of 512 tokens or more runs the GEMM with the post-processing in
+   * its epilogue (hb_qkv_gemm: its tiles then fill the CUs); a smaller one
+   * the GEMM into scratch, then hb_qkv_post (same results either way). */
+  int fused[2] = {0, 0};
   size_t ws_max = 0;
   for (int i = 0; i < n_parts; ++i) {
-    const size_t b = hb_f16_workspace_bytes(parts[i].tokens, input_dim, ncols);
+    fused[i] = parts[i].tokens >= 512 && (ncols / 3) % 128 == 0;
+    const size_t b = fused[i] ? hb_qkv_gemm_workspace_bytes(parts[i].tokens, input_dim)
+                              : hb_f16_workspace_bytes(parts[i].tokens, input_dim, ncols);
     ws_max = b > ws_max ? b : ws_max;
   }
+  int raw_tokens = 0;
+  for (int i = 0; i < n_parts; ++i)
+    if (!fused[i] && parts[i].tokens > raw_tokens) raw_tokens = parts[i].tokens;
+  float *raw = raw_tokens ? (float *)htp_executor_scratch(1, (size_t)raw_tokens * (size_t)ncols * sizeof(float))
+                          : NULL;
   void *ws = ws_max ? htp_executor_scratch(4, ws_max) : NULL;
   uint16_t *dst[3];
   for (int i = 0; i < 3; ++i) dst[i] = (uint16_t *)qkv_output(&out[i], 8 + i);
-  if (!raw || (ws_max && !ws) || !dst[0] || !dst[1] || !dst[2]) return -5;
+  if ((raw_tokens && !raw) || (ws_max && !ws) || !dst[0] || !dst[1] || !dst[2]) return -5;
   const float *d_pe = NULL;
   if (pe) {
     if (stage_in(pe, s)) return -5;
@@ -753,10 +762,14 @@ static int run_qkv(htp_view out[3], qkv_part *parts, int n_parts, htp_view *pe, 
       break;
     }
     if (i == 0) hrc = hb_event_record(ev.e[0], s);
-    if (!hrc)
+    if (!hrc && fused[i])
+      hrc = hb_qkv_gemm(dst[0], dst[1], dst[2], x, (const uint16_t *)packed[i], b, qn, kn, d_pe, p->rope_offset,
+                        rope_count, p->tokens, input_dim, n_heads, head_dim, token_tiles, p->out_offset, ws, ws_max,
+                        s);
+    if (!hrc && !fused[i])
       hrc = hb_f16_gemm_ws(raw, x, (const uint16_t *)packed[i], NULL, p->tokens, input_dim, ncols, ncols, 0, ws,
                            ws_max, s);
-    if (!hrc)
+    if (!hrc && !fused[i])
       hrc = hb_qkv_post(dst[0], dst[1], dst[2], raw, b, qn, kn, d_pe, p->rope_offset, rope_count, p->tokens, n_heads,
                         head_dim, token_tiles, p->out_offset, s);
   }

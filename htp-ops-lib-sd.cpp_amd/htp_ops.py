@@ -90,6 +90,8 @@ _SIGNATURES = {
                                                                                          _c_void_p]),
     "hb_model_aux_workspace_bytes": (_c_size_t, [_c_int] * 5),
     "hb_qkv_post": (_c_int, [_c_void_p] * 8 + [_c_int] * 7 + [_c_void_p]),
+    "hb_qkv_gemm_workspace_bytes": (_c_size_t, [_c_int, _c_int]),
+    "hb_qkv_gemm": (_c_int, [_c_void_p] * 9 + [_c_int] * 8 + [_c_void_p, _c_size_t, _c_void_p]),
     "hb_model_aux_ws": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p] + [_c_int] * 9 +
                         [ctypes.c_float, _c_void_p, _c_size_t, _c_void_p]),
 }
@@ -629,6 +631,20 @@ def qkv_post(q_dev, k_dev, v_dev, raw_dev, bias_dev, q_norm_dev, k_norm_dev, pe_
     check(lib().hb_qkv_post(q_dev.ptr, k_dev.ptr, v_dev.ptr, raw_dev.ptr, b, q_norm_dev.ptr, k_norm_dev.ptr, pe,
                             rope_offset, rope_count, tokens, n_heads, head_dim, token_tiles, out_offset, stream),
           "hb_qkv_post")
+
+
+def qkv_gemm_workspace_bytes(tokens, input_dim):
+    return lib().hb_qkv_gemm_workspace_bytes(tokens, input_dim)
+
+
+def qkv_gemm(q_dev, k_dev, v_dev, x_dev, packed, bias_dev, q_norm_dev, k_norm_dev, pe_dev, rope_offset, rope_count,
+             tokens, input_dim, n_heads, head_dim, token_tiles, out_offset, workspace, stream=None):
+    """hb_qkv_gemm: the GEMM with the post-processing in its epilogue."""
+    b = bias_dev.ptr if bias_dev else None
+    pe = pe_dev.ptr if pe_dev else None
+    check(lib().hb_qkv_gemm(q_dev.ptr, k_dev.ptr, v_dev.ptr, x_dev.ptr, packed.ptr, b, q_norm_dev.ptr,
+                            k_norm_dev.ptr, pe, rope_offset, rope_count, tokens, input_dim, n_heads, head_dim,
+                            token_tiles, out_offset, workspace.ptr, workspace.nbytes, stream), "hb_qkv_gemm")
 
 
 def matmul_params(out, act, wgt, m, k, n, with_elapsed=False):

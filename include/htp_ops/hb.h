@@ -277,6 +277,23 @@ int hb_qkv_post(uint16_t *d_q, uint16_t *d_k, uint16_t *d_v, const float *d_raw,
                 const float *d_q_norm, const float *d_k_norm, const float *d_pe, int rope_offset, int rope_count,
                 int tokens, int n_heads, int head_dim, int token_tiles, int out_offset, hb_stream s);
 
+/*
+ * The same opcodes in one GEMM (reference src/dsp/ops/mat_mul.c:1373-1502,
+ * the chunked HMX product with the post-processing of each output chunk):
+ * d_x (tokens x input_dim f32) times the hb_f16_prepack image of the
+ * input_dim x 3*n_heads*head_dim weight, with the post-processing of
+ * hb_qkv_post applied to each 128 x 128 output tile in LDS, so the f32
+ * product never reaches HBM.  Results are identical to hb_f16_gemm_ws (mode
+ * 0, no bias) followed by hb_qkv_post.  n_heads * head_dim must be a
+ * multiple of 128; d_workspace (256-byte aligned) holds
+ * hb_qkv_gemm_workspace_bytes(tokens, input_dim) bytes, no state.
+ */
+size_t hb_qkv_gemm_workspace_bytes(int tokens, int input_dim);
+int hb_qkv_gemm(uint16_t *d_q, uint16_t *d_k, uint16_t *d_v, const float *d_x, const uint16_t *d_packed,
+                const float *d_bias, const float *d_q_norm, const float *d_k_norm, const float *d_pe, int rope_offset,
+                int rope_count, int tokens, int input_dim, int n_heads, int head_dim, int token_tiles, int out_offset,
+                void *d_workspace, size_t workspace_bytes, hb_stream s);
+
 #ifdef __cplusplus
 }
 #endif

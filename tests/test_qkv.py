@@ -635,10 +635,15 @@ def test_qkv_opcodes_end_to_end(hip, orc, op, bias_kind, device):
 
 
 @pytest.mark.gpu
-def test_qkv_ragged_dual_and_rotary_window(hip, orc):
-    """Dual request with a ragged text part (image 64 + text 45 tokens, 30
-    heads x 64, input 256) and rotary offsets 3 / 70, against the oracle."""
-    n_heads, hd, k, image, text = 30, 64, 256, 64, 45
+@pytest.mark.parametrize("n_heads,hd,image,text", [
+    (30, 64, 64, 45),     # both parts: GEMM, then the post-processing kernel
+    (24, 64, 256, 1100),  # text part: the GEMM with the post-processing in its epilogue
+    (24, 128, 96, 600),   # the same with heads of 128
+])
+def test_qkv_ragged_dual_and_rotary_window(hip, orc, n_heads, hd, image, text):
+    """Dual request with a ragged text part (input 256) and rotary offsets
+    3 / 70, against the oracle post-processing of the library's GEMM."""
+    k = 256
     tokens = image + text
     tiles = (tokens + 31) // 32
     rng = np.random.default_rng(11)
@@ -679,3 +684,52 @@ def test_qkv_ragged_dual_and_rotary_window(hip, orc):
     ref = orc.qkv_post(raws[1], None, qn, kn, pe, 70, tokens, text, n_heads, hd, tiles, out_offset=image, out=ref)
     for which in range(3):
         assert np.array_equal(got[which], ref[which]), which
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("tokens,n_heads,hd,rope,bias,offset,count,out_tile", [
+    (1100, 24, 64, True, True, 0, 1100, 0),   # ragged last row tile (1100 = 8 * 128 + 76)
+    (520, 24, 128, True, False, 7, 300, 1),   # rotary window, no bias, later output tiles
+    (300, 30, 64, False, True, 0, 0, 0),
+    (160, 38, 64, True, True, 0, 160, 2),
+])
+def test_hb_qkv_gemm_bit_exact(hip, orc, tokens, n_heads, hd, rope, bias, offset, count, out_tile):
+    """The GEMM with the post-processing in its epilogue equals the oracle's
+    post-processing of the library's GEMM output (hb_f16_gemm_ws)."""
+    k = 256
+    rng = np.random.default_rng(tokens + n_heads)
+    cols = 3 * n_heads * hd
+    act = rng.normal(0, 1, (tokens, k)).astype(np.float32)
+    w = rng.normal(0, 0.05, (k, cols)).astype(np.float16)
+    perm = h.permute_f16(w.view(np.uint16))
+    _, b, qn, kn, pe = post_inputs(tokens, n_heads, hd, tokens, rope_tokens=offset + tokens + 3 if rope else 0)
+    b = b if bias else None
+    raw = library_raw(dict(tokens=tokens, k=k, n_heads=n_heads, hd=hd, permuted=perm, act=act))
+    tiles = out_tile + (tokens + 31) // 32
+    size = n_heads * orc.qkv_head_elems(tiles, hd)
+    ref = orc.qkv_post(raw, b, qn, kn, pe, offset, count, tokens, n_heads, hd, tiles, out_offset=32 * out_tile,
+                       out=tuple(np.full(size, 0x1234, np.uint16) for _ in range(3)))
+    outs = [dev(np.full(size, 0x1234, np.uint16)) for _ in range(3)]
+    packed = h.f16_prepack(dev(perm), k, cols)
+    ws = h.DeviceBuffer(h.qkv_gemm_workspace_bytes(tokens, k))
+    h.qkv_gemm(*outs, dev(act), packed, dev(b) if bias else None, dev(qn), dev(kn), dev(pe) if rope else None, offset,
+               count, tokens, k, n_heads, hd, tiles, 32 * out_tile, ws)
+    h.sync()
+    for which, (o, r) in enumerate(zip(outs, ref)):
+        got = o.read(np.uint16, size)
+        assert np.array_equal(got, r), (which, int((got != r).sum()))
+
+
+@pytest.mark.gpu
+def test_hb_qkv_gemm_rejects_bad_arguments(hip):
+    x = h.DeviceBuffer(1 << 20)
+    ws = h.DeviceBuffer(1 << 20)
+    args = (x, x, x, x, x, None, x, x, None, 0, 0)
+    with pytest.raises(h.HtpOpsError):
+        h.qkv_gemm(*args, 64, 256, 1, 64, 2, 0, ws)        # heads * head_dim not a multiple of 128
+    with pytest.raises(h.HtpOpsError):
+        h.qkv_gemm(*args, 64, 250, 2, 64, 2, 0, ws)        # input_dim not a multiple of 32
+    with pytest.raises(h.HtpOpsError):
+        h.qkv_gemm(*args, 4096, 4096, 2, 64, 128, 0, ws)   # workspace too small
+    with pytest.raises(h.HtpOpsError):
+        h.qkv_gemm(*args, 64, 256, 2, 64, 2, 32, ws)       # tokens past the output tiles
