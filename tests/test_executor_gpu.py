@@ -229,6 +229,42 @@ def test_opcode1_and_direct_rpc(hip, orc):
     assert lib.htp_ops_close(handle) == 0
 
 
+def test_weight_cache_in_a_shared_buffer(hip, orc):
+    """One HBM buffer holds a weight, activations and outputs.  Outputs written
+    elsewhere in it keep the cached weight image (results unchanged); an
+    output written over the weight's own bytes makes the next call use the
+    new bytes."""
+    m, k, n = 32, 64, 64
+    rng = np.random.default_rng(41)
+    x = rng.integers(-2, 3, (m, k)).astype(np.float32)
+    w1 = rng.integers(-2, 3, (k, n)).astype(np.float16)
+    w3 = rng.integers(-2, 3, (k, n)).astype(np.float16)
+    p1, p3 = h.permute_f16(w1.view(np.uint16)), h.permute_f16(w3.view(np.uint16))
+    ow, ow3, ox, oy = 0, 8192, 16384, 24576  # the weight's k*n*2 bytes = the m*n*4 output bytes
+    buf = rpc(32768, True)
+    buf.write(p1, ow)
+    buf.write(p3, ow3)
+    buf.write(x, ox)
+
+    def matmul(out, wgt):
+        rc, _ = h.execute(1, h.matmul_params((buf.fd, out), (buf.fd, ox), (buf.fd, wgt), m, k, n))
+        assert rc == 0, h.last_error()
+
+    matmul(oy, ow)
+    y1 = buf.read(np.float32, m * n, oy)
+    assert np.array_equal(y1.reshape(m, n), x @ w1.astype(np.float32))  # small integers: exact
+    matmul(oy, ow)  # the output lands beside the weight: same result
+    assert np.array_equal(buf.read(np.float32, m * n, oy), y1)
+    matmul(ow, ow3)  # the output overwrites the first weight's bytes
+    w2_perm = buf.read(np.uint16, k * n, ow)
+    assert not np.array_equal(w2_perm, p1)
+    matmul(oy, ow)  # must read the new bytes, not the cached image of the old ones
+    ref = orc.f16_gemm_epilogue(x, w2_perm, None, m, k, n, n, 0)
+    got = buf.read(np.float32, m * n, oy).reshape(m, n)
+    assert np.all(np.abs(got - ref) <= 2e-3 * np.abs(ref) + 1e-6)
+    assert not np.allclose(got, y1.reshape(m, n))
+
+
 def post(chan_view, requests, capacity, timeout=60.0):
     msg, offs = h.build_message(requests, capacity)
     chan_view[8:len(msg)] = np.frombuffer(bytes(msg[8:]), np.uint8)
