@@ -548,11 +548,15 @@ def test_hb_qkv_post_rejects_bad_arguments(hip):
         h.qkv_post(*base, 0, 0, 32, 1, 64, 2, 16)      # offset not a tile
 
 
-def gpu_case(orc, op, bias_kind, device):
+def gpu_case(orc, op, bias_kind, device, shape=None):
     """The reference test's request for op (24 heads; 8: head_dim 64,
-    32 tokens; 10/11/12: head_dim 128, 64 tokens), laid out in one buffer."""
+    32 tokens; 10/11/12: head_dim 128, 64 tokens; `shape` = (heads, head_dim)
+    overrides, as the test's HTP_QKV_ROPE_HEADS / _HEAD_DIM do), laid out in
+    one buffer."""
     rope = op in (11, 12)
     n_heads, hd, k, tokens = (24, 64, 1536, 32) if op == 8 else (24, 128, 1536, 64)
+    if shape is not None:
+        n_heads, hd = shape
     act, w, bias, qn, kn, pe = reference_case(n_heads, hd, k, tokens, bias_kind, rope)
     tiles = (tokens + 31) // 32
     qkv_bytes = n_heads * orc.qkv_head_elems(tiles, hd) * 2
@@ -601,14 +605,17 @@ def library_raw(c):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("op,bias_kind,device", [
-    (8, "mul", False), (8, "mul", True),
-    (10, "rope", True), (10, "none", False),
-    (11, "rope", False), (11, "none", True),
-    (12, "rope", True), (12, "none", False),
+@pytest.mark.parametrize("op,bias_kind,device,shape", [
+    (8, "mul", False, None), (8, "mul", True, None),
+    (10, "rope", True, None), (10, "none", False, None),
+    (11, "rope", False, None), (11, "none", True, None),
+    (12, "rope", True, None), (12, "none", False, None),
+    # every supported head shape (op_reg.h:23-39): 24 / 30 heads of 64 or 128, 38 heads of 64
+    (11, "rope", True, (30, 128)), (12, "rope", True, (30, 64)), (11, "rope", True, (38, 64)),
+    (12, "none", True, (24, 64)), (8, "mul", True, (38, 64)), (10, "rope", True, (30, 128)),
 ])
-def test_qkv_opcodes_end_to_end(hip, orc, op, bias_kind, device):
-    c = gpu_case(orc, op, bias_kind, device)
+def test_qkv_opcodes_end_to_end(hip, orc, op, bias_kind, device, shape):
+    c = gpu_case(orc, op, bias_kind, device, shape)
     rc, after = h.execute(op, c["payload"])
     assert rc == 0, h.last_error()
     elapsed = struct.unpack_from("<i", after, len(after) - 4)[0]
