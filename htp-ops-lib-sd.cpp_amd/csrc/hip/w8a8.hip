@@ -1800,8 +1800,16 @@ int hb_w8a8_quantize(int8_t *d_q, float *d_scales, const float *d_x, const float
       whole_tiles ? launch_quant_block<4, 16>(d_q, d_scales, d_x, d_inv, m, k, kp, st)
                   : launch_quant_block<4, 8>(d_q, d_scales, d_x, d_inv, m, k, kp, st);
     } else if (k <= 256 * 6) {
-      whole_tiles ? launch_quant_block<6, 16>(d_q, d_scales, d_x, d_inv, m, k, kp, st)
-                  : launch_quant_block<6, 8>(d_q, d_scales, d_x, d_inv, m, k, kp, st);
+      // from 2048 rows: 16-row blocks when they put exactly one on each CU
+      // (4096 rows: 7.30 us against 7.84 for the form below), otherwise
+      // 8-row blocks with the smoothing vector in LDS, two or more per CU
+      // (2048 rows 6.08 -> 5.12 us, 8192 rows 14.27 -> 12.75 us at k=1536)
+      if (whole_tiles && (m + 15) / 16 == compute_units())
+        launch_quant_block<6, 16>(d_q, d_scales, d_x, d_inv, m, k, kp, st);
+      else if (whole_tiles)
+        launch_quant_block<6, 8, 4, true>(d_q, d_scales, d_x, d_inv, m, k, kp, st);
+      else
+        launch_quant_block<6, 8>(d_q, d_scales, d_x, d_inv, m, k, kp, st);
     } else if (k <= 256 * 8) {
       launch_quant_block<8, 8>(d_q, d_scales, d_x, d_inv, m, k, kp, st);
     } else if (k <= 256 * 12) {

@@ -45,7 +45,10 @@ def upload_blob(hip, blob):
                                           # 16-row and 8-row blocks (m > 64, k <= 6144), ragged m and k % 64 == 32
                                           (100, 480, "uniform"), (97, 1024, "ones"), (72, 2048, "uniform"),
                                           (81, 3040, "uniform"), (90, 4096, "uniform"), (75, 6144, "uniform"),
-                                          (129, 5152, "uniform")])
+                                          (129, 5152, "uniform"),
+                                          # from 2048 rows: 16-row blocks at one per CU (4096 x 1536 in the
+                                          # baseline tests), else 8-row blocks with the smoothing vector in LDS
+                                          (2100, 1536, "uniform"), (2048, 1248, "ones")])
 def test_quantize_bit_exact(hip, orc, m, k, inv_kind):
     x, _, blob = make_w8a8(orc, m, k, 64, seed=m + k, inv_kind=inv_kind)
     x[0, :] = 0.0  # zero row: s = 1e-12, u = 128
