@@ -448,7 +448,8 @@ __global__ __launch_bounds__(256) void f16_qkv_ring(uint16_t *__restrict__ q, ui
   constexpr int STAGE = (BM / 16 + BN / 16) * kFragBytes;
   constexpr int TS = BN + 8;  // halfwords per LDS row of the tile (padded)
   constexpr int TILE_BYTES = BM * TS * 2;
-  constexpr int POST_BYTES = TILE_BYTES + HD * 32 * 2;  // the tile, then one packed block
+  constexpr int NH = BN / HD;                          // heads per tile, post-processed together
+  constexpr int POST_BYTES = TILE_BYTES + NH * HD * 32 * 2;  // the tile, then its packed blocks
   static_assert(kQkvThreads == 64 * WM * WN, "the post-processing uses the GEMM's 256 threads");
   __shared__ __attribute__((aligned(1024))) int8_t lds[S * STAGE > POST_BYTES ? S * STAGE : POST_BYTES];
   uint16_t *blk = (uint16_t *)(lds + TILE_BYTES);
@@ -478,25 +479,23 @@ __global__ __launch_bounds__(256) void f16_qkv_ring(uint16_t *__restrict__ q, ui
   const int which = n0 / q_cols, head0 = (n0 % q_cols) / HD;
   uint16_t *dst = which == 0 ? q : which == 1 ? k : v;
   const int rows_tile = min(BM, m - m0);
+  const size_t head_stride = (size_t)token_tiles * (HD / 32) * 1024;
   for (int t = 0; t < BM / 32 && 32 * t < rows_tile; ++t) {
     const int rows = min(32, rows_tile - 32 * t);
     const int tt = out_tile0 + m0 / 32 + t;
-#pragma unroll
-    for (int h = 0; h < BN / HD; ++h) {
-      const size_t head_base = (size_t)(head0 + h) * (size_t)token_tiles * (HD / 32) * 1024;
-      const _Float16 *src = tile + 32 * t * TS + h * HD;
-      const float *b = bias ? bias + n0 + h * HD : nullptr;
-      if (which == 0)
-        qkv_block<HD, 0>(blk, dst, src, TS, b, q_norm, pe, rope_off, rope_count, rows, m0 + 32 * t, tt, token_tiles,
-                         head_base);
-      else if (which == 1)
-        qkv_block<HD, 1>(blk, dst, src, TS, b, k_norm, pe, rope_off, rope_count, rows, m0 + 32 * t, tt, token_tiles,
-                         head_base);
-      else
-        qkv_block<HD, 2>(blk, dst, src, TS, b, nullptr, nullptr, 0, 0, rows, m0 + 32 * t, tt, token_tiles,
-                         head_base);
-      __syncthreads();  // the block's LDS staging is reused by the next one
-    }
+    const size_t head_base = (size_t)head0 * head_stride;
+    const _Float16 *src = tile + 32 * t * TS;
+    const float *b = bias ? bias + n0 : nullptr;
+    if (which == 0)
+      qkv_blocks<HD, 0, NH>(blk, dst, src, TS, b, q_norm, pe, rope_off, rope_count, rows, m0 + 32 * t, tt,
+                            token_tiles, head_base, head_stride);
+    else if (which == 1)
+      qkv_blocks<HD, 1, NH>(blk, dst, src, TS, b, k_norm, pe, rope_off, rope_count, rows, m0 + 32 * t, tt,
+                            token_tiles, head_base, head_stride);
+    else
+      qkv_blocks<HD, 2, NH>(blk, dst, src, TS, b, nullptr, nullptr, 0, 0, rows, m0 + 32 * t, tt, token_tiles,
+                            head_base, head_stride);
+    __syncthreads();  // the packed blocks' LDS staging is reused by the next token tile
   }
 }
 

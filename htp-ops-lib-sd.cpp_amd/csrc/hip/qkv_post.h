@@ -58,17 +58,21 @@ __device__ inline int block_index(int r, int c) {
 // Every load of the tile (rows, bias, gamma, rotary matrices) is issued
 // before the arithmetic: one round of 4 row pairs per wave keeps enough
 // bytes in flight to stream from HBM.
-// src: row 0, column 0 of the block's input (f32, or fp16 holding the same
+// NH blocks side by side: heads h = 0 .. NH-1 of one 32-token tile, whose
+// inputs are HD columns apart in src (and in bias); the NH heads' arithmetic
+// is interleaved (independent chains), the rotary matrices are shared (they
+// depend on the token and the column pair only).
+// src: row 0, column 0 of head 0's input (f32, or fp16 holding the same
 // fp16-exact values; rows src_stride elements apart);
-// bias: the block's first column (NULL: none); rows: valid rows (1..32);
+// bias: head 0's first column (NULL: none); rows: valid rows (1..32);
 // token0: the call's token index of row 0 (for the rotary matrices);
-// blk: HD * 32 halfwords of LDS, 16-byte aligned, for the packed block.
-template <int HD, int WHICH, typename T>
-__device__ void qkv_block(uint16_t *__restrict__ blk, uint16_t *__restrict__ dst, const T *__restrict__ src,
-                          int src_stride,
-                          const float *__restrict__ bias, const float *__restrict__ gamma,
-                          const float *__restrict__ pe, int rope_off, int rope_count, int rows, int token0, int tt,
-                          int token_tiles, size_t head_base) {
+// blk: NH * HD * 32 halfwords of LDS, 16-byte aligned, for the packed blocks;
+// head h's block goes to dst + head_base + h * head_stride.
+template <int HD, int WHICH, int NH, typename T>
+__device__ void qkv_blocks(uint16_t *__restrict__ blk, uint16_t *__restrict__ dst, const T *__restrict__ src,
+                           int src_stride, const float *__restrict__ bias, const float *__restrict__ gamma,
+                           const float *__restrict__ pe, int rope_off, int rope_count, int rows, int token0, int tt,
+                           int token_tiles, size_t head_base, size_t head_stride) {
   constexpr int CH = HD / 64;  // 64-column chunks; lane j holds columns 64d+j and 64d+32+j
   constexpr int E = 2 * CH;    // values per lane and row
   constexpr int PAIRS = 16 / (kQkvThreads / 64);
@@ -77,18 +81,21 @@ __device__ void qkv_block(uint16_t *__restrict__ blk, uint16_t *__restrict__ dst
   const int half = lane >> 5, j = lane & 31;
   auto col = [&](int e) { return 64 * (e >> 1) + 32 * (e & 1) + j; };
 
-  float v[PAIRS][E];
+  float v[NH][PAIRS][E];
 #pragma unroll
   for (int i = 0; i < PAIRS; ++i) {
     const int r = 2 * (wave + 4 * i) + half;
     const T *x = src + (size_t)r * (size_t)src_stride;
 #pragma unroll
-    for (int e = 0; e < E; ++e) v[i][e] = r < rows ? (float)x[col(e)] : 0.0f;
+    for (int h = 0; h < NH; ++h)
+#pragma unroll
+      for (int e = 0; e < E; ++e) v[h][i][e] = r < rows ? (float)x[h * HD + col(e)] : 0.0f;
   }
-  float b[E], g[E];
+  float b[NH][E], g[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) {
-    b[e] = bias ? bias[col(e)] : 0.0f;
+#pragma unroll
+    for (int h = 0; h < NH; ++h) b[h][e] = bias ? bias[h * HD + col(e)] : 0.0f;
     g[e] = WHICH < 2 ? gamma[col(e)] : 0.0f;
   }
   // rotary matrices (x0, x1 -> m.x x0 + m.y x1, m.z x0 + m.w x1) of each row's token
@@ -111,52 +118,70 @@ __device__ void qkv_block(uint16_t *__restrict__ blk, uint16_t *__restrict__ dst
   for (int i = 0; i < PAIRS; ++i) {
     const int r = 2 * (wave + 4 * i) + half;
 #pragma unroll
-    for (int e = 0; e < E; ++e) v[i][e] = __fadd_rn(v[i][e], b[e]);
-    if (WHICH < 2) {
-      float acc = 0.0f;
+    for (int h = 0; h < NH; ++h) {
 #pragma unroll
-      for (int e = 0; e < E; ++e) acc = __fadd_rn(acc, __fmul_rn(v[i][e], v[i][e]));
-      // lane i += lane i - s within the 32 lanes of the row, s = 16 .. 1
+      for (int e = 0; e < E; ++e) v[h][i][e] = __fadd_rn(v[h][i][e], b[h][e]);
+      if (WHICH < 2) {
+        float acc = 0.0f;
 #pragma unroll
-      for (int s = 16; s >= 1; s >>= 1) {
-        const float o = __shfl(acc, (lane - s) & 63, 64);
-        if (j >= s) acc = __fadd_rn(acc, o);
-      }
-      const float sum = __shfl(acc, half * 32 + 31, 64);
-      const float inv = qkv_rsqrt(__fadd_rn(__fdiv_rn(sum, (float)HD), 1.0e-6f));
+        for (int e = 0; e < E; ++e) acc = __fadd_rn(acc, __fmul_rn(v[h][i][e], v[h][i][e]));
+        // lane i += lane i - s within the 32 lanes of the row, s = 16 .. 1
 #pragma unroll
-      for (int e = 0; e < E; ++e) v[i][e] = __fmul_rn(__fmul_rn(v[i][e], inv), g[e]);
-      if (pe) {
-        // the pair of column c is c ^ 1, held by lane j ^ 1
+        for (int s = 16; s >= 1; s >>= 1) {
+          const float o = __shfl(acc, (lane - s) & 63, 64);
+          if (j >= s) acc = __fadd_rn(acc, o);
+        }
+        const float sum = __shfl(acc, half * 32 + 31, 64);
+        const float inv = qkv_rsqrt(__fadd_rn(__fdiv_rn(sum, (float)HD), 1.0e-6f));
 #pragma unroll
-        for (int e = 0; e < E; ++e) {
-          const float other = __shfl(v[i][e], lane ^ 1, 64);
-          if (rot[i]) {
-            const bool odd = j & 1;
-            const float x0 = odd ? other : v[i][e], x1 = odd ? v[i][e] : other;
-            const float4 mm = m[i][ROPE_OK ? e : 0];
-            v[i][e] = odd ? __fadd_rn(__fmul_rn(x0, mm.z), __fmul_rn(x1, mm.w))
-                          : __fadd_rn(__fmul_rn(x0, mm.x), __fmul_rn(x1, mm.y));
+        for (int e = 0; e < E; ++e) v[h][i][e] = __fmul_rn(__fmul_rn(v[h][i][e], inv), g[e]);
+        if (pe) {
+          // the pair of column c is c ^ 1, held by lane j ^ 1
+#pragma unroll
+          for (int e = 0; e < E; ++e) {
+            const float other = __shfl(v[h][i][e], lane ^ 1, 64);
+            if (rot[i]) {
+              const bool odd = j & 1;
+              const float x0 = odd ? other : v[h][i][e], x1 = odd ? v[h][i][e] : other;
+              const float4 mm = m[i][ROPE_OK ? e : 0];
+              v[h][i][e] = odd ? __fadd_rn(__fmul_rn(x0, mm.z), __fmul_rn(x1, mm.w))
+                               : __fadd_rn(__fmul_rn(x0, mm.x), __fmul_rn(x1, mm.y));
+            }
           }
         }
       }
-    }
 #pragma unroll
-    for (int e = 0; e < E; ++e)
-      blk[block_index<WHICH>(r, col(e))] = r < rows ? __half_as_ushort(__float2half_rn(v[i][e])) : (uint16_t)0;
+      for (int e = 0; e < E; ++e)
+        blk[h * HD * 32 + block_index<WHICH>(r, col(e))] =
+            r < rows ? __half_as_ushort(__float2half_rn(v[h][i][e])) : (uint16_t)0;
+    }
   }
   __syncthreads();
-  const uint4 *packed = (const uint4 *)blk;
-  if (WHICH < 2) {
-    uint4 *out = (uint4 *)(dst + head_base + (size_t)tt * HD * 32);
-    for (int i = threadIdx.x; i < HD * 32 / 8; i += kQkvThreads) out[i] = packed[i];
-  } else {
-    for (int i = threadIdx.x; i < HD * 32 / 8; i += kQkvThreads) {
-      const int ct = i / 128;  // 1024 halfwords = 128 uint4 per column tile
-      uint4 *out = (uint4 *)(dst + head_base + ((size_t)ct * token_tiles + tt) * 1024);
-      out[i % 128] = packed[i];
+#pragma unroll
+  for (int h = 0; h < NH; ++h) {
+    const uint4 *packed = (const uint4 *)(blk + h * HD * 32);
+    uint16_t *hdst = dst + head_base + (size_t)h * head_stride;
+    if (WHICH < 2) {
+      uint4 *out = (uint4 *)(hdst + (size_t)tt * HD * 32);
+      for (int i = threadIdx.x; i < HD * 32 / 8; i += kQkvThreads) out[i] = packed[i];
+    } else {
+      for (int i = threadIdx.x; i < HD * 32 / 8; i += kQkvThreads) {
+        const int ct = i / 128;  // 1024 halfwords = 128 uint4 per column tile
+        uint4 *out = (uint4 *)(hdst + ((size_t)ct * token_tiles + tt) * 1024);
+        out[i % 128] = packed[i];
+      }
     }
   }
+}
+
+// One block (NH = 1).
+template <int HD, int WHICH, typename T>
+__device__ void qkv_block(uint16_t *__restrict__ blk, uint16_t *__restrict__ dst, const T *__restrict__ src,
+                          int src_stride, const float *__restrict__ bias, const float *__restrict__ gamma,
+                          const float *__restrict__ pe, int rope_off, int rope_count, int rows, int token0, int tt,
+                          int token_tiles, size_t head_base) {
+  qkv_blocks<HD, WHICH, 1, T>(blk, dst, src, src_stride, bias, gamma, pe, rope_off, rope_count, rows, token0, tt,
+                              token_tiles, head_base, 0);
 }
 
 }  // namespace
