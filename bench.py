@@ -49,13 +49,18 @@ HEADLINE = (4096, 1536, 6144)
 SETTLE_MS = 80.0          # untimed GPU time before each timed sequence (clock ramp)
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "w8a8_gemm_stream_4096x1536x6144_traffic.md")
 COPY_PROBE_BYTES = 256 << 20
-CHUNKS = 20               # timed steps are split into this many event-bracketed chunks (median reported)
+CHUNKS = 20               # chunks of the separate median pass (run only when every chunk has >= 10 steps)
 USE_GRAPHS = True         # --no-graph: no graph capture or replay anywhere (for traced runs)
 
 
 def progress(msg):
     """One progress line on stderr per finished case, so a failing run names its case."""
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def _us(ms, digits=3):
+    """ms -> us rounded, None stays None."""
+    return None if ms is None else round(ms * 1e3, digits)
 
 
 def w8a8_bytes(m, k, n):
@@ -135,20 +140,46 @@ def run_w8a8(m, k, n, steps, warmup, rotate, outliers=0.0, scale=(1e-4, 1e-3), s
         hip.sync()
 
     def timed_stream(fn, count):
-        """Total ms of `count` stream-ordered launches, and the median over
-        CHUNKS event-bracketed chunks of the per-launch ms."""
-        chunks = max(1, min(CHUNKS, count))
-        bounds = [count * c // chunks for c in range(chunks + 1)]
-        events = [hip.Event() for _ in range(chunks + 1)]
+        """ms of `count` stream-ordered launches between ONE pair of HIP events
+        (no event inside the timed region: each record costs GPU time), and
+        the host's enqueue ms per launch.  `count` untimed launches (at least
+        200) are queued first without a sync, so the GPU is still busy with
+        them while the host enqueues the timed ones: the timed launches never
+        wait for the host as long as one enqueue is shorter than one launch's
+        GPU time (the host figure says whether it was)."""
+        a, b = hip.Event(), hip.Event()
         synced()
+        lead = max(count, 200)
+        for i in range(lead):
+            fn(sets[i % rotate])
+        t0 = time.perf_counter()
+        a.record(stream)
+        for i in range(count):
+            fn(sets[i % rotate])
+        b.record(stream)
+        host_ms = (time.perf_counter() - t0) * 1e3 / count
+        synced()
+        return a.elapsed_ms(b), host_ms
+
+    def chunk_median(fn, count):
+        """Median over CHUNKS event-bracketed chunks of the per-launch ms, in a
+        pass of its own (the chunk events cost GPU time, so they never share
+        a run with the mean); None unless every chunk has at least 10 launches."""
+        if count < 10 * CHUNKS:
+            return None
+        bounds = [count * c // CHUNKS for c in range(CHUNKS + 1)]
+        events = [hip.Event() for _ in range(CHUNKS + 1)]
+        synced()
+        for i in range(max(count, 200)):
+            fn(sets[i % rotate])
         events[0].record(stream)
-        for c in range(chunks):
+        for c in range(CHUNKS):
             for i in range(bounds[c], bounds[c + 1]):
                 fn(sets[i % rotate])
             events[c + 1].record(stream)
         synced()
-        per = [events[c].elapsed_ms(events[c + 1]) / max(1, bounds[c + 1] - bounds[c]) for c in range(chunks)]
-        return events[0].elapsed_ms(events[-1]), statistics.median(per)
+        return statistics.median(events[c].elapsed_ms(events[c + 1]) / (bounds[c + 1] - bounds[c])
+                                 for c in range(CHUNKS))
 
     def timed_graph(graph):
         a, b = hip.Event(), hip.Event()
@@ -178,11 +209,11 @@ def run_w8a8(m, k, n, steps, warmup, rotate, outliers=0.0, scale=(1e-4, 1e-3), s
         step(st)
     synced()
     settle(warmup)
-    wall0 = time.perf_counter()
-    total_ms, step_median = timed_stream(step, steps)
-    wall = time.perf_counter() - wall0
-    gemm_total, gemm_median = timed_stream(gemm, steps)
-    quant_total, quant_median = timed_stream(quant, steps)
+    total_ms, host_ms = timed_stream(step, steps)
+    gemm_total, _ = timed_stream(gemm, steps)
+    quant_total, _ = timed_stream(quant, steps)
+    step_median = chunk_median(step, steps)
+    gemm_median = chunk_median(gemm, steps)
     graph_ms = {"step": None, "gemm": None, "quant": None}
     if USE_GRAPHS:
         for name, fn in (("step", step), ("gemm", gemm), ("quant", quant)):
@@ -190,9 +221,9 @@ def run_w8a8(m, k, n, steps, warmup, rotate, outliers=0.0, scale=(1e-4, 1e-3), s
             settle(0)
             graph_ms[name] = timed_graph(g) / steps
             g.destroy()
-    return {"ms_per_step": total_ms / steps, "ms_per_step_median": step_median, "wall_ms_per_step": wall * 1e3 / steps,
+    return {"ms_per_step": total_ms / steps, "ms_per_step_median": step_median, "host_enqueue_ms": host_ms,
             "gemm_ms_mean": gemm_total / steps, "gemm_ms_median": gemm_median, "quant_ms_mean": quant_total / steps,
-            "quant_ms_median": quant_median, "graph_ms_per_step": graph_ms["step"],
+            "graph_ms_per_step": graph_ms["step"],
             "graph_gemm_ms_mean": graph_ms["gemm"], "graph_quant_ms_mean": graph_ms["quant"], "sets": sets}
 
 
@@ -339,14 +370,32 @@ def e2e_mailbox(cases, reps=20):
     return out
 
 
+KERNEL_SOURCE = os.path.join(REPO, "htp-ops-lib-sd.cpp_amd", "csrc", "hip", "w8a8.hip")
+
+
+def kernel_source_sha16():
+    """First 16 hex digits of the SHA-256 of the W8A8 kernel source: the
+    provenance key of the committed counter summary."""
+    import hashlib
+    with open(KERNEL_SOURCE, "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()[:16]
+
+
 def read_traffic():
-    """HBM bytes per headline GEMM launch from the committed PMC summary."""
+    """HBM bytes per headline GEMM launch from the committed PMC summary, and
+    whether that summary is stale: it records the kernel source hash it was
+    measured on (`kernel_source_sha16:`), and a different hash now (or none)
+    means the kernel changed since, so the figure is reported as stale
+    instead of silently reused."""
     try:
         with open(TRAFFIC_FILE) as f:
-            match = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", f.read(), re.M)
+            text = f.read()
     except OSError:
-        return None
-    return int(match.group(1)) if match else None
+        return None, None
+    match = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", text, re.M)
+    src = re.search(r"^kernel_source_sha16:\s*([0-9a-f]{16})", text, re.M)
+    stale = src is None or src.group(1) != kernel_source_sha16()
+    return (int(match.group(1)) if match else None), stale
 
 
 def decode_case(m, k, n, steps, warmup, rotate):
@@ -359,7 +408,8 @@ def decode_case(m, k, n, steps, warmup, rotate):
             "gemm_us": round(r["gemm_ms_mean"] * 1e3, 3),
             "gemm_gbps": round(gemm_bytes(m, k, n) / (r["gemm_ms_mean"] * 1e-3) / 1e9, 1),
             "quant_us": round(r["quant_ms_mean"] * 1e3, 3), "rotated_sets": rotate,
-            "us_per_call_median": round(r["ms_per_step_median"] * 1e3, 3),
+            "us_per_call_median": _us(r["ms_per_step_median"]),
+            "host_enqueue_us": _us(r["host_enqueue_ms"]),
             "graph_us_per_call": None if r["graph_ms_per_step"] is None else round(r["graph_ms_per_step"] * 1e3, 3)}
 
 
@@ -381,7 +431,7 @@ def all_configs(steps, warmup, with_cpu=False, only=None):
         progress(f"start {name}")
         r = run_w8a8(m, k, n, steps, warmup, 4, outliers=outl, scale=sc,
                      epilogue=hip.EPI_SCALE_GELU if "gelu" in name else None)
-        out[name] = {"us": round(r["ms_per_step"] * 1e3, 2), "us_median": round(r["ms_per_step_median"] * 1e3, 2),
+        out[name] = {"us": round(r["ms_per_step"] * 1e3, 2), "us_median": _us(r["ms_per_step_median"]),
                      "tops": round(2 * m * n * k / (r["ms_per_step"] * 1e-3) / 1e12, 1),
                      "gemm_us": round(r["gemm_ms_mean"] * 1e3, 2)}
         del r
@@ -923,6 +973,7 @@ def main():
                                                  only=set(args.only.split(",")))}), flush=True)
         return
     m, k, n = HEADLINE
+    traffic, traffic_stale = read_traffic()
     r = run_w8a8(m, k, n, args.steps, args.warmup, args.rotate, outliers=0.01)
     ops = 2.0 * m * n * k
     tops = ops / (r["ms_per_step"] * 1e-3) / 1e12
@@ -946,20 +997,26 @@ def main():
         "mfma_frac_full_op": round(tops / PEAK_INT8_TOPS, 4),
         "hbm_gbps_full_op": round(w8a8_bytes(m, k, n) / (r["ms_per_step"] * 1e-3) / 1e9, 1),
         "quant_us": round(r["quant_ms_mean"] * 1e3, 3),
-        "us_per_step_median": round(r["ms_per_step_median"] * 1e3, 3),
-        "timing": f"{args.steps} stream-ordered launches between HIP events on the library stream (value: their "
-                  f"mean; median over {CHUNKS} event-bracketed chunks beside it)" +
+        "us_per_step_median": _us(r["ms_per_step_median"]),
+        "host_enqueue_us": _us(r["host_enqueue_ms"]),
+        "timing": f"{args.steps} stream-ordered launches between one pair of HIP events on the library stream, "
+                  f"queued behind {max(args.steps, 200)} untimed launches (value: their mean" +
+                  (f"; median over {CHUNKS} event-bracketed chunks in a separate pass beside it)"
+                   if r["ms_per_step_median"] is not None else ")") +
                   ("" if r["graph_ms_per_step"] is None else
                    f"; graph replay of the same steps: {r['graph_ms_per_step'] * 1e3:.3f} us/step, "
                    f"GEMM {r['graph_gemm_ms_mean'] * 1e3:.3f} us"),
         "roofline": {"kernel": hip.w8a8_gemm_kernel(m, k, n), "bound": "mfma", "achieved": round(gemm_tops, 2),
                      "peak": PEAK_INT8_TOPS, "unit": "TOPS", "frac": round(gemm_tops / PEAK_INT8_TOPS, 4),
-                     "traffic": read_traffic(), "gemm_us": round(r["gemm_ms_mean"] * 1e3, 3),
+                     "traffic": traffic, "traffic_stale": traffic_stale,
+                     "gemm_us": round(r["gemm_ms_mean"] * 1e3, 3),
                      "gemm_gbps": round(gemm_bytes(m, k, n) / (r["gemm_ms_mean"] * 1e-3) / 1e9, 1),
                      "algorithmic_ops_per_launch": ops,
                      "algorithmic_bytes_per_launch": gemm_bytes(m, k, n)},
     }
-    line["roofline"]["gemm_us_median"] = round(r["gemm_ms_median"] * 1e3, 3)
+    line["roofline"]["gemm_us_median"] = _us(r["gemm_ms_median"])
+    if r["graph_gemm_ms_mean"] is not None:
+        line["roofline"]["gemm_us_graph"] = _us(r["graph_gemm_ms_mean"])
     del r
     progress(f"headline {line['ms_per_step'] * 1e3:.2f} us/step")
     line["decode_m1"] = decode_case(1, 4096, 14336, args.steps, args.warmup, 6)

@@ -1452,7 +1452,6 @@ int compute_units() {
 // double buffer).
 bool stream_applies(int kp) { return kp / kKStep >= kStreamStages - 1; }
 bool stream_wide_applies(int n, int kp) { return n % kStreamWideBN == 0 && kp / kKStep >= kStreamWideStages - 1; }
-
 int stream_mode() {
   static const int mode = getenv("HTP_OPS_AMD_W8A8_STREAM") ? atoi(getenv("HTP_OPS_AMD_W8A8_STREAM")) : -1;
   return mode;
@@ -1859,6 +1858,22 @@ int hb_w8a8_gemm_choice(int m, int k, int n) {
   const int rtiles = (m + 15) / 16;
   if (rtiles <= 5 && 4LL * ((m + 63) / 64) * (n / 64) <= compute_units()) return HB_W8A8_CHOICE_DECODE_TILES;
   return pick_tile_shape(m, n, (int)kp_of(k));
+}
+
+int hb_w8a8_gemm_tile(int m, int k, int n, int *bm, int *bn) {
+  const int choice = hb_w8a8_gemm_choice(m, k, n);
+  if (choice == HB_E_INVAL || !bm || !bn) return HB_E_INVAL;
+  if (choice == HB_W8A8_CHOICE_DECODE || choice == HB_W8A8_CHOICE_DECODE_TILES) {
+    *bm = 16;  // one 16-row tile (m <= 16: all rows) per 16-column block
+    *bn = 16;
+  } else if (choice == kStreamShape || choice == kStreamWideShape) {
+    *bm = kStreamBM;
+    *bn = choice == kStreamWideShape ? kStreamWideBN : kStreamBN;
+  } else {
+    *bm = kTileShapes[choice].bm;
+    *bn = kTileShapes[choice].bn;
+  }
+  return choice;
 }
 
 int hb_w8a8_linear(float *d_y, const float *d_x, const void *d_packed, int m, int k, int n, int epilogue,

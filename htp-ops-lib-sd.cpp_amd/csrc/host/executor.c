@@ -469,10 +469,12 @@ static int exec_w8a8(uint8_t *payload, size_t payload_size) {
       profile.mac_ticks = profile.hmx_ticks;
       profile.readout_ticks = 0;
     } else if (profile.mode == 3) {
-      /* reserved: low 16 bits = rows per workgroup tile, high 16 = columns;
-       * mac/readout = weight loads / bytes during this call. */
-      const uint32_t bm = m <= 16 ? 16u : 0u, bn = 16u;
-      profile.reserved = bm | (bn << 16);
+      /* reserved: low 16 bits = rows per workgroup tile, high 16 = columns,
+       * of the GEMM kernel that ran (the choice hb_w8a8_gemm makes for this
+       * shape); mac/readout = weight loads / bytes during this call. */
+      int bm = 0, bn = 0;
+      if (hb_w8a8_gemm_tile(m, k, n, &bm, &bn) == HB_E_INVAL) bm = bn = 0;
+      profile.reserved = (uint32_t)bm | ((uint32_t)bn << 16);
       profile.mac_ticks = built ? 1u : 0u;
       profile.readout_ticks = built ? (uint64_t)k * n : 0u;
     }

@@ -73,6 +73,7 @@ _SIGNATURES = {
     "hb_w8a8_linear_noalloc": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_void_p]),
     "hb_w8a8_force_tile": (_c_int, [_c_int]),
     "hb_w8a8_gemm_choice": (_c_int, [_c_int, _c_int, _c_int]),
+    "hb_w8a8_gemm_tile": (_c_int, [_c_int, _c_int, _c_int, ctypes.POINTER(_c_int), ctypes.POINTER(_c_int)]),
     # F16
     "hb_f16_packed_bytes": (_c_size_t, [_c_int, _c_int]),
     "hb_qk0_block_bytes": (_c_size_t, [_c_int]),

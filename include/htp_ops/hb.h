@@ -142,6 +142,11 @@ int hb_w8a8_force_tile(int index);
 #define HB_W8A8_CHOICE_DECODE_TILES (-2)
 int hb_w8a8_gemm_choice(int m, int k, int n);
 
+/* The output tile of that choice for the scale epilogue: *bm rows by *bn
+ * columns per workgroup tile (16 x 16 for the decode kernels).  Returns the
+ * choice, or HB_E_INVAL.  Fills opcode 15's profile mode 3. */
+int hb_w8a8_gemm_tile(int m, int k, int n, int *bm, int *bn);
+
 /* Full opcode-15 computation: quantize + GEMM + epilogue (workspace from hb_w8a8_workspace_bytes).
  * With the SCALE or SCALE_GELU epilogue, 16-byte aligned x and y and K a
  * multiple of 32, small problems run as one launch that quantizes its own

@@ -75,7 +75,35 @@ def test_opcode15_profile_modes(hip, orc):
         assert prof["hmx_ticks"] > 0 and prof["activation_ticks"] > 0
         if mode == 2:
             assert prof["mac_ticks"] == prof["hmx_ticks"]
+        if mode == 3:
+            assert prof["reserved"] == gemm_tile(m, k, n)
         assert np.array_equal(out.read(np.float32, m * n).reshape(m, n), ref)
+
+
+def gemm_tile(m, k, n):
+    """rows | columns << 16 of the tile hb_w8a8_gemm runs for this shape."""
+    bm, bn = ctypes.c_int(0), ctypes.c_int(0)
+    assert h.lib().hb_w8a8_gemm_tile(m, k, n, ctypes.byref(bm), ctypes.byref(bn)) >= -2
+    return bm.value | (bn.value << 16)
+
+
+def test_opcode15_profile_mode3_reports_the_tile_that_ran(hip, orc):
+    """Mode 3's reserved field holds the GEMM's tile rows | columns << 16:
+    256 x 192 streaming tiles at the headline shape, 16-row tiles for few rows."""
+    assert gemm_tile(4096, 1536, 6144) == 256 | (192 << 16)
+    assert gemm_tile(4, 4096, 14336) == 16 | (16 << 16)
+    for m, k, n in ((4096, 1536, 6144), (4, 4096, 4096)):
+        x, blob = w8a8_inputs(orc, m, k, n, seed=5)
+        out, act, cst = rpc(m * n * 4, True), rpc(m * k * 4, True), rpc(blob.nbytes, True)
+        act.write(x)
+        cst.write(blob)
+        payload = h.w8a8_params((out.fd, 0), (act.fd, 0), (cst.fd, 0), m, k, n) + h.w8a8_profile(3)
+        rc, after = h.execute(15, payload)
+        assert rc == 0
+        prof = h.unpack_w8a8_profile(after[40:])
+        assert prof["mode"] == 3 and prof["reserved"] == gemm_tile(m, k, n)
+        for b in (out, act, cst):
+            b.free()
 
 
 def test_opcode15_cpu_control_variant(hip, orc):

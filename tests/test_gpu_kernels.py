@@ -451,7 +451,10 @@ def test_f16_gemm_epilogue(hip, orc, m, k, n, mode, channels, bias, split_k):
     else:
         got = got.reshape(m, n)
         bias_cols = np.abs(b)[None, :] if b is not None else 0.0
-    assert_f16_close(got, ref, v_ref, bias_cols, absdot, k)
+    rel = assert_f16_close(got, ref, v_ref, bias_cols, absdot, k)
+    # the north star's figure: the largest relative error where nothing cancels
+    print(f"f16 {m}x{k}x{n} mode {mode} split_k {split_k}: max relative error {rel:.3g}")
+    assert rel <= 2e-3
 
 
 @pytest.mark.parametrize("m,k,n,mode,bias,check_oracle", [
