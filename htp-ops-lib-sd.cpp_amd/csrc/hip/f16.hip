@@ -381,7 +381,7 @@ __global__ __launch_bounds__(64 * WM *WN) void f16_gemm_ring(float *__restrict__
 
   const int tiles_m = (m + BM - 1) / BM, tiles_n = (n + BN - 1) / BN;
   int tm, tn;
-  tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  tile_coords_2d<BM, BN>(blockIdx.x, tiles_m, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int wm = wave / WN, wn = wave % WN;
@@ -457,7 +457,7 @@ __global__ __launch_bounds__(256) void f16_qkv_ring(uint16_t *__restrict__ q, ui
   const int q_cols = n_heads * HD, n = 3 * q_cols;
   const int tiles_m = (m + BM - 1) / BM, tiles_n = n / BN;
   int tm, tn;
-  tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  tile_coords_2d<BM, BN>(blockIdx.x, tiles_m, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int wm = wave / WN, wn = wave % WN;

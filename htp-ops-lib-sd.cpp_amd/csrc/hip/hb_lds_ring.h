@@ -50,6 +50,40 @@ __device__ inline void tile_coords(int bid, int tiles_m, int tiles_n, int &tm, i
   tn = in_group / gsize;
 }
 
+// Tile of workgroup bid for kernels of one tile per workgroup, XCD-aware in
+// two dimensions: each of the 8 XCDs (bid % 8) owns one of pm x (8 / pm)
+// equal rectangles of the tile grid, pm chosen to minimise the operand bytes
+// a rectangle touches (rows * BM + columns * BN, both operands being of one
+// element size), walked in groups of 4 row blocks column by column.  An
+// XCD then reads only its rectangle's row and column blocks, where the
+// 1-D chunks of tile_coords make every XCD read most of the wider operand.
+// Falls back to tile_coords when no split divides the grid evenly.
+template <int BM, int BN>
+__device__ inline void tile_coords_2d(int bid, int tiles_m, int tiles_n, int &tm, int &tn) {
+  int pm = 0, best = -1;
+#pragma unroll
+  for (int p = 1; p <= 8; p *= 2) {
+    if (tiles_m % p != 0 || tiles_n % (8 / p) != 0) continue;
+    const int cost = (tiles_m / p) * BM + (tiles_n / (8 / p)) * BN;
+    if (best < 0 || cost < best) {
+      best = cost;
+      pm = p;
+    }
+  }
+  if (pm == 0) {
+    tile_coords(bid, tiles_m, tiles_n, tm, tn);
+    return;
+  }
+  const int pn = 8 / pm, rows = tiles_m / pm, cols = tiles_n / pn;
+  const int xcd = bid % 8, p = bid / 8;  // p < rows * cols: the grid is rows * cols * 8 tiles
+  constexpr int G = 4;
+  const int first = (p / (G * cols)) * G;
+  const int gsize = min(rows - first, G);
+  const int in_group = p % (G * cols);
+  tm = (xcd / pn) * rows + first + in_group % gsize;
+  tn = (xcd % pn) * cols + in_group / gsize;
+}
+
 // Issues one stage's DMA: instruction i of this wave fills block i*NW + wave
 // of the NB blocks of a stage (waves below NB % NW issue one more than the
 // others when the blocks do not split evenly).
