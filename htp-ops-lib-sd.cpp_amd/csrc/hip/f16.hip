@@ -862,6 +862,14 @@ __global__ __launch_bounds__(64 * W) void f16_small(float *__restrict__ y, const
   using Raw = typename std::conditional<TYPE == 0, hb_f16x8, Qk0Raw<TYPE == 0 ? HB_GGML_Q4_0 : TYPE>>::type;
   Raw b[KPW][CF];
   float4 alo[KPW], ahi[KPW];
+  // the bias of the fragment this wave finishes (waves below CF), requested
+  // with the operands
+  const int col = (g * CF + (wave < CF ? wave : 0)) * 16 + 4 * (lane >> 4);
+  float bv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (wave < CF && bias) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) bv[r] = col + r < channels ? bias[col + r] : 0.0f;
+  }
 #pragma unroll
   for (int t = 0; t < KPW; ++t) {
     const int kb = min(kb0 + t, kblocks - 1);  // blocks past k are loaded, then zeroed
@@ -905,12 +913,11 @@ __global__ __launch_bounds__(64 * W) void f16_small(float *__restrict__ y, const
   hb_f32x4 tot = red[0][j][lane];
 #pragma unroll
   for (int w = 1; w < W; ++w) tot += red[w][j][lane];
-  const int col = (g * CF + j) * 16 + 4 * (lane >> 4);
   hb_f32x4 out;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const float v = (float)(_Float16)tot[r];
-    out[r] = bias && col + r < channels ? __fadd_rn(v, bias[col + r]) : v;
+    out[r] = bias && col + r < channels ? __fadd_rn(v, bv[r]) : v;
   }
   if (mode == 3) {
 #pragma unroll
