@@ -7,6 +7,7 @@
  *   F16 permute: reference src/host/test.c:551-556.
  */
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "host_internal.h"
@@ -94,6 +95,50 @@ int htp_ops_w8a8_quantize_weights(int8_t *q, float *sw, const float *w, const fl
     }
   }
   return 0;
+}
+
+/* IEEE binary16 bits -> float (every half value is exactly representable). */
+static float half_to_float(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h >> 15) << 31, e = (h >> 10) & 0x1f, m = h & 0x3ff;
+  uint32_t bits;
+  if (e == 0x1f) {
+    bits = sign | 0x7f800000u | (m << 13); /* inf / nan (payload kept) */
+  } else if (e != 0) {
+    bits = sign | ((e + 112u) << 23) | (m << 13); /* normal: rebias 15 -> 127 */
+  } else if (m == 0) {
+    bits = sign; /* signed zero */
+  } else {
+    /* subnormal half: m * 2^-24, normalized as a float */
+    uint32_t shift = 0, mm = m;
+    while (!(mm & 0x400)) {
+      mm <<= 1;
+      ++shift;
+    }
+    bits = sign | ((113u - shift) << 23) | ((mm & 0x3ff) << 13);
+  }
+  float f;
+  memcpy(&f, &bits, sizeof(f));
+  return f;
+}
+
+int htp_ops_w8a8_pack_f16(uint8_t *blob, size_t blob_bytes, const uint16_t *w_f16, const float *inv, int k, int n) {
+  if (!blob || !w_f16 || k < 32 || k % 32 || n < 64 || n % 64) return -1;
+  if (blob_bytes < htp_ops_w8a8_constants_bytes(k, n)) return -1;
+  const size_t kn = (size_t)k * (size_t)n;
+  float *w = (float *)malloc(kn * sizeof(float));
+  int8_t *q = (int8_t *)malloc(kn);
+  float *sw = (float *)malloc((size_t)n * sizeof(float));
+  int rc = (w && q && sw) ? 0 : -1;
+  if (!rc) {
+    for (size_t i = 0; i < kn; ++i) w[i] = half_to_float(w_f16[i]);
+    rc = htp_ops_w8a8_quantize_weights(q, sw, w, inv, k, n);
+  }
+  if (!rc)
+    rc = htp_ops_w8a8_pack_constants(blob, blob_bytes, q, sw, NULL, inv, k, n, htp_fnv1a64(w_f16, kn * 2u));
+  free(w);
+  free(q);
+  free(sw);
+  return rc;
 }
 
 int htp_ops_f16_permute_weights(uint16_t *permuted, const uint16_t *w_kn, int k, int n) {

@@ -168,6 +168,7 @@ _HOST_SIGNATURES = {
     "htp_ops_w8a8_pack_constants": (_c_int, [_c_void_p, _c_size_t, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                              _c_int, _c_int, ctypes.c_uint64]),
     "htp_ops_w8a8_quantize_weights": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int]),
+    "htp_ops_w8a8_pack_f16": (_c_int, [_c_void_p, _c_size_t, _c_void_p, _c_void_p, _c_int, _c_int]),
     "htp_ops_fnv1a64": (ctypes.c_uint64, [_c_void_p, _c_size_t]),
     "htp_ops_f16_permute_weights": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_int]),
 }
@@ -509,6 +510,20 @@ def quantize_weights(w_nk_f32, inv=None):
     if rc != 0:
         raise HtpOpsError("htp_ops_w8a8_quantize_weights failed")
     return q, sw
+
+
+def pack_f16(w_nk_f16, inv=None):
+    """fp16 weights [n][k] (float16 array or uint16 bits) -> W8A8 constants blob
+    (quantized per output channel, original_f16_signature = FNV-1a 64 of the fp16 bytes)."""
+    w = np.ascontiguousarray(w_nk_f16).view(np.uint16)
+    n, k = w.shape
+    nbytes = lib().htp_ops_w8a8_constants_bytes(k, n)
+    blob = np.zeros(nbytes, np.uint8)
+    inv = None if inv is None else np.ascontiguousarray(inv, np.float32)
+    rc = lib().htp_ops_w8a8_pack_f16(blob.ctypes.data, blob.nbytes, w.ctypes.data, _arr_ptr(inv), k, n)
+    if rc != 0:
+        raise HtpOpsError("htp_ops_w8a8_pack_f16 failed")
+    return blob
 
 
 def permute_f16(w_kn_bits):

@@ -42,6 +42,20 @@ int htp_ops_w8a8_pack_constants(uint8_t *blob, size_t blob_bytes, const int8_t *
  */
 int htp_ops_w8a8_quantize_weights(int8_t *q, float *sw, const float *w, const float *inv, int k, int n);
 
+/*
+ * FP16 source weights -> W8A8 constants blob in one call (the sd.cpp-side
+ * producer the reference's blob header is designed for: op_reg.h:80-85 keeps
+ * an original_f16_signature of the weights the blob was made from).
+ * w_f16: fp16 bits [n][k] (row n = output channel), converted to f32 exactly;
+ * inv: f32[k] smoothing vector or NULL (then 1.0, stored as such).  The
+ * weights are quantized by htp_ops_w8a8_quantize_weights (w / inv, per
+ * output channel), sums are sum_k q, and original_f16_signature is
+ * htp_ops_fnv1a64 of the k*n*2 fp16 bytes.  Same shape and size rules as
+ * htp_ops_w8a8_pack_constants.  Returns 0, or -1 on a bad argument or when
+ * scratch memory cannot be allocated.
+ */
+int htp_ops_w8a8_pack_f16(uint8_t *blob, size_t blob_bytes, const uint16_t *w_f16, const float *inv, int k, int n);
+
 /* FNV-1a 64 of a byte range (the value stored as original_f16_signature by callers that want one). */
 uint64_t htp_ops_fnv1a64(const void *data, size_t bytes);
 
