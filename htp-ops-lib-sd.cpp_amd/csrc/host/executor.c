@@ -106,8 +106,9 @@ static uint64_t content_hash(const uint8_t *p, size_t n) {
  * "put" (or call htp_ops_amd_invalidate_weights) after writing: it hashes
  * the first 128 bytes (the W8A8 header), the last `tail` bytes in full (the
  * W8A8 scale, sum and smoothing sections) and 64 spaced 64-byte samples of
- * the rest.  HBM-resident weights change only through this library, which
- * bumps the fd generation instead. */
+ * the rest.  HBM-resident weights change only through this library: a
+ * library write marks the cached images whose byte range it overlaps stale,
+ * and images of other ranges of the same fd stay valid. */
 static uint64_t weight_signature(const htp_view *v, size_t tail) {
   if (v->is_device || !v->host) return 0;
   static int sampled = -1;
@@ -327,9 +328,9 @@ static int exec_w8a8(uint8_t *payload, size_t payload_size) {
 
   /* Header acceptance, reference src/dsp/op_executor.cc:331-335.  A device
    * blob whose prepacked image is cached passed this check when the image was
-   * built and has not been written since (the cache key holds the buffer's
-   * write generation), so only a miss reads the header back (a blocking
-   * copy). */
+   * built and has not been written since (a library write that overlaps the
+   * blob's bytes marks its image stale), so only a miss reads the header back
+   * (a blocking copy). */
   const uint64_t cst_sig = weight_signature(&cst, (size_t)n * 8u + (size_t)k * 4u);
   if (!(cst.is_device && htp_weight_cache_peek(HTP_WEIGHT_W8A8, &cst, k, n, cst_sig))) {
     struct W8A8Header h;
