@@ -1367,6 +1367,35 @@ __global__ __launch_bounds__(1024) void w8a8_small(void *__restrict__ y, const f
 }
 
 // ---------------------------------------------------------------------------
+// The GEMM epilogue as its own pass (profile mode 2): raw = sum_k u*W (the
+// HB_W8A8_EPI_RAW output), c = raw - wsum128 + delta = raw - 128*sums
+// (wrapping, the bits the fused kernels start their accumulators from), then
+// epilogue_bits, so the values equal the fused epilogue's.  Four columns per
+// thread, grid-stride over the m x n/4 quads.
+// ---------------------------------------------------------------------------
+
+template <int EPI>
+__global__ __launch_bounds__(256) void w8a8_readout(float *__restrict__ y, int ldy, const int32_t *__restrict__ raw,
+                                                    const float *__restrict__ scales, const float *__restrict__ sw,
+                                                    const int32_t *__restrict__ delta,
+                                                    const int32_t *__restrict__ wsum, int m, int n) {
+  const int nq = n / 4;
+  const size_t quads = (size_t)m * (size_t)nq;
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < quads; i += (size_t)gridDim.x * 256) {
+    const int row = (int)(i / nq), c0 = (int)(i % nq) * 4;
+    const hb_i32x4 a = *(const hb_i32x4 *)(raw + (size_t)row * n + c0);
+    const hb_i32x4 d = *(const hb_i32x4 *)(delta + c0), w = *(const hb_i32x4 *)(wsum + c0);
+    const hb_f32x4 sc = *(const hb_f32x4 *)(sw + c0);
+    const float s = scales[row];
+    hb_u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      o[e] = epilogue_bits<EPI>((int32_t)((uint32_t)a[e] - (uint32_t)w[e]), d[e], sc[e], s);
+    __builtin_nontemporal_store(o, (hb_u32x4 *)(y + (size_t)row * ldy + c0));
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Raw accumulator -> byte-plane export of the CPU-control variant.
 // One thread per output byte position (row, 32-column half, byte in 128).
 // ---------------------------------------------------------------------------
@@ -2007,6 +2036,29 @@ int hb_w8a8_force_tile(int index) {
   if (index < -1 || index > kStreamWideShape) return hb_invalid("hb_w8a8_force_tile index");
   forced_tile_shape();  // settle the environment default first
   return g_forced_tile.exchange(index);
+}
+
+int hb_w8a8_readout(float *d_y, int ldy, const int32_t *d_raw, const float *d_scales, const void *d_packed, int m,
+                    int k, int n, int epilogue, hb_stream s) {
+  if (!d_y || !d_raw || !d_scales || !d_packed) return hb_invalid("hb_w8a8_readout null pointer");
+  if (m < 1 || k < 32 || k % 32 || n < 16 || n % 16 || ldy < n || ldy % 4) return hb_invalid("hb_w8a8_readout shape");
+  if ((uintptr_t)d_y % 16 || (uintptr_t)d_raw % 16) return hb_invalid("hb_w8a8_readout alignment");
+  const uint8_t *base = (const uint8_t *)d_packed;
+  const float *sw = (const float *)(base + hb_w8a8_packed_offset(k, n, HB_W8A8_SW));
+  const int32_t *delta = (const int32_t *)(base + hb_w8a8_packed_offset(k, n, HB_W8A8_DELTA));
+  const int32_t *wsum = (const int32_t *)(base + hb_w8a8_packed_offset(k, n, HB_W8A8_WSUM128));
+  const size_t quads = (size_t)m * (size_t)(n / 4);
+  const int grid = (int)std::min<size_t>((quads + 255) / 256, 65536);
+  hipStream_t st = hb_resolve_stream(s);
+  if (epilogue == HB_W8A8_EPI_SCALE)
+    hipLaunchKernelGGL((w8a8_readout<HB_W8A8_EPI_SCALE>), dim3(grid), dim3(256), 0, st, d_y, ldy, d_raw, d_scales, sw,
+                       delta, wsum, m, n);
+  else if (epilogue == HB_W8A8_EPI_SCALE_GELU)
+    hipLaunchKernelGGL((w8a8_readout<HB_W8A8_EPI_SCALE_GELU>), dim3(grid), dim3(256), 0, st, d_y, ldy, d_raw,
+                       d_scales, sw, delta, wsum, m, n);
+  else
+    return hb_invalid("hb_w8a8_readout epilogue");
+  return hb_check_launch("w8a8_readout");
 }
 
 int hb_w8a8_planes_from_raw(uint8_t *d_out, const int32_t *d_raw, int m, int n, hb_stream s) {

@@ -379,8 +379,11 @@ static int exec_w8a8(uint8_t *payload, size_t payload_size) {
   const float *inv = (const float *)((const uint8_t *)packed + hb_w8a8_packed_offset(k, n, HB_W8A8_INV));
   /* The GEMM writes 16-byte vectors: a misaligned output is produced in scratch and copied. */
   float *y = ((uintptr_t)out.dev % 16u) == 0 ? (float *)out.dev : (float *)htp_executor_scratch(3, out.bytes);
-  void *raw = cpu_output ? htp_executor_scratch(1, (size_t)m * n * 4u) : NULL;
-  if (!y || (cpu_output && !raw)) return -5;
+  /* profile mode 2 runs the GEMM's epilogue as its own launch, so the MAC
+   * and readout phases are timed apart (reference linear_w8a8.c:488-500) */
+  const int split_readout = profiled && profile.mode == 2 && !cpu_output;
+  void *raw = cpu_output || split_readout ? htp_executor_scratch(1, (size_t)m * n * 4u) : NULL;
+  if (!y || ((cpu_output || split_readout) && !raw)) return -5;
 
   event_set ev;
   if (events_open(&ev, 4)) {
@@ -401,11 +404,13 @@ static int exec_w8a8(uint8_t *payload, size_t payload_size) {
   if (!hrc && split) hrc = hb_event_record(ev.e[1], s);
   if (!hrc) {
     if (!split) hrc = hb_w8a8_linear(y, x, packed, m, k, n, HB_W8A8_EPI_SCALE, ws, ws_bytes, s);
-    else if (cpu_output) hrc = hb_w8a8_gemm(raw, n, q, scales, packed, m, k, n, HB_W8A8_EPI_RAW, s);
+    else if (cpu_output || split_readout) hrc = hb_w8a8_gemm(raw, n, q, scales, packed, m, k, n, HB_W8A8_EPI_RAW, s);
     else hrc = hb_w8a8_gemm(y, n, q, scales, packed, m, k, n, HB_W8A8_EPI_SCALE, s);
   }
   if (!hrc && split) hrc = hb_event_record(ev.e[2], s);
   if (!hrc && cpu_output) hrc = hb_w8a8_planes_from_raw((uint8_t *)y, (const int32_t *)raw, m, n, s);
+  if (!hrc && split_readout)
+    hrc = hb_w8a8_readout(y, n, (const int32_t *)raw, scales, packed, m, k, n, HB_W8A8_EPI_SCALE, s);
   if (!hrc) hrc = hb_event_record(ev.e[3], s);
   if (!hrc && (void *)y != (void *)out.dev) hrc = hb_memcpy_d2d(out.dev, y, out.bytes, s);
   if (hrc) {
@@ -466,9 +471,14 @@ static int exec_w8a8(uint8_t *payload, size_t payload_size) {
     profile.hmx_ticks = (uint64_t)(gemm_ms * 1e-3 * QTIMER_HZ);
     profile.output_ticks = (uint64_t)(out_ms * 1e-3 * QTIMER_HZ);
     if (profile.mode == 2) {
-      /* The epilogue is fused into the GEMM: all GEMM time counts as MAC time. */
+      /* the accumulating GEMM (int32 sums out) is the MAC phase; the launch
+       * after it (the scale epilogue, or the byte planes of the CPU-control
+       * variant) reads the sums out.  Both are HMX-phase time, as on the
+       * reference, and no output phase remains. */
       profile.mac_ticks = profile.hmx_ticks;
-      profile.readout_ticks = 0;
+      profile.readout_ticks = profile.output_ticks;
+      profile.hmx_ticks += profile.output_ticks;
+      profile.output_ticks = 0;
     } else if (profile.mode == 3) {
       /* reserved: low 16 bits = rows per workgroup tile, high 16 = columns,
        * of the GEMM kernel that ran (the choice hb_w8a8_gemm makes for this

@@ -69,6 +69,8 @@ _SIGNATURES = {
     "hb_w8a8_linear": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_void_p,
                                 _c_size_t, _c_void_p]),
     "hb_w8a8_planes_from_raw": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
+    "hb_w8a8_readout": (_c_int, [_c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int,
+                                 _c_void_p]),
     "hb_w8a8_static_setup": (_c_int, [_c_int]),
     "hb_w8a8_linear_noalloc": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_void_p]),
     "hb_w8a8_force_tile": (_c_int, [_c_int]),
@@ -314,6 +316,12 @@ def w8a8_quantize(x_dev, inv_ptr, m, k):
 def w8a8_gemm(y_dev, q_dev, s_dev, packed, m, k, n, epilogue=EPI_SCALE, ldy=None, stream=None):
     check(lib().hb_w8a8_gemm(y_dev.ptr, n if ldy is None else ldy, q_dev.ptr, s_dev.ptr if s_dev else None,
                              packed.ptr, m, k, n, epilogue, stream), "hb_w8a8_gemm")
+
+
+def w8a8_readout(y_dev, raw_dev, s_dev, packed, m, k, n, epilogue=EPI_SCALE, ldy=None, stream=None):
+    """The GEMM epilogue as its own launch: raw int32 sums (EPI_RAW output) -> f32 values."""
+    check(lib().hb_w8a8_readout(y_dev.ptr, n if ldy is None else ldy, raw_dev.ptr, s_dev.ptr, packed.ptr, m, k, n,
+                                epilogue, stream), "hb_w8a8_readout")
 
 
 def w8a8_linear(y_dev, x_dev, packed, m, k, n, workspace, epilogue=EPI_SCALE, stream=None):

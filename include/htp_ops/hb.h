@@ -177,6 +177,15 @@ int hb_w8a8_linear_noalloc(float *d_y, const float *d_x, const void *d_packed, i
  * format (reference linear_w8a8.c:209-227) written over the f32 output tensor. */
 int hb_w8a8_planes_from_raw(uint8_t *d_out, const int32_t *d_raw, int m, int n, hb_stream s);
 
+/* The epilogue of hb_w8a8_gemm as its own launch, for the opcode-15 profile
+ * mode 2 split of MAC from readout (reference linear_w8a8.c:488-500): raw
+ * holds hb_w8a8_gemm's HB_W8A8_EPI_RAW output (sum_k u*W per element,
+ * row stride n), y gets the HB_W8A8_EPI_SCALE / _SCALE_GELU values of the
+ * same request, bit for bit (row stride ldy >= n).  n % 16 == 0; y and raw
+ * 16-byte aligned, ldy % 4 == 0. */
+int hb_w8a8_readout(float *d_y, int ldy, const int32_t *d_raw, const float *d_scales, const void *d_packed, int m,
+                    int k, int n, int epilogue, hb_stream s);
+
 /* ---- packed-F16 GEMM (opcodes 1 and 16) ------------------------------------ */
 
 /* Permuted fp16 weight (reference layout) -> 16(n) x 32(k) MFMA tiles:

@@ -74,7 +74,10 @@ def test_opcode15_profile_modes(hip, orc):
         assert prof["mode"] == mode
         assert prof["hmx_ticks"] > 0 and prof["activation_ticks"] > 0
         if mode == 2:
-            assert prof["mac_ticks"] == prof["hmx_ticks"]
+            # MAC (the accumulating GEMM) and readout (the separate epilogue launch) timed apart
+            assert prof["mac_ticks"] > 0 and prof["readout_ticks"] > 0
+            assert prof["mac_ticks"] + prof["readout_ticks"] == prof["hmx_ticks"]
+            assert prof["output_ticks"] == 0
         if mode == 3:
             assert prof["reserved"] == gemm_tile(m, k, n)
         assert np.array_equal(out.read(np.float32, m * n).reshape(m, n), ref)

@@ -385,6 +385,27 @@ def test_w8a8_gelu_epilogue(hip, orc, m, k, n):
     np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-30)
 
 
+@pytest.mark.parametrize("m,k,n,epi", [(300, 1536, 576, "scale"), (77, 768, 3072, "gelu"), (1, 4096, 1024, "scale")])
+def test_w8a8_readout_equals_fused_epilogue(hip, orc, m, k, n, epi):
+    """hb_w8a8_readout over the EPI_RAW sums gives the fused epilogue's bits
+    (the profile-mode-2 split of MAC from readout)."""
+    x, _, blob = make_w8a8(orc, m, k, n, seed=m + 3, inv_kind="uniform", sums_kind="random",
+                           scale_lo=1e-3 if epi == "gelu" else 1e-4, scale_hi=1e-2 if epi == "gelu" else 1e-3)
+    packed = hip.w8a8_prepack(upload_blob(hip, blob), k, n)
+    xd = hip.DeviceBuffer.from_array(x)
+    q, s = hip.w8a8_quantize(xd, packed.ptr + hip.w8a8_packed_offset(k, n, hip.SECTION_INV), m, k)
+    epilogue = hip.EPI_SCALE if epi == "scale" else hip.EPI_SCALE_GELU
+    raw, fused, split = hip.DeviceBuffer(m * n * 4), hip.DeviceBuffer(m * n * 4), hip.DeviceBuffer(m * n * 4)
+    hip.w8a8_gemm(raw, q, s, packed, m, k, n, hip.EPI_RAW)
+    hip.w8a8_gemm(fused, q, s, packed, m, k, n, epilogue)
+    hip.w8a8_readout(split, raw, s, packed, m, k, n, epilogue)
+    hip.sync()
+    got = split.read(np.uint32, m * n)
+    np.testing.assert_array_equal(got, fused.read(np.uint32, m * n))
+    if epi == "scale":
+        np.testing.assert_array_equal(got.reshape(m, n), orc.linear(x, blob, k, n).view(np.uint32))
+
+
 def test_w8a8_planes_export(hip, orc):
     m, k, n = 77, 64, 128
     x, _, blob = make_w8a8(orc, m, k, n, seed=5)
