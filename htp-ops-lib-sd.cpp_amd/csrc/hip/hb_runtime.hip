@@ -116,6 +116,13 @@ int hb_memcpy_d2h(void *h_dst, const void *d_src, size_t bytes, hb_stream s) {
   return copy(h_dst, d_src, bytes, hipMemcpyDeviceToHost, s, "hb_memcpy_d2h");
 }
 
+int hb_memcpy_d2h_async(void *h_dst, const void *d_src, size_t bytes, hb_stream s) {
+  if (bytes == 0) return HB_OK;
+  if (h_dst == nullptr || d_src == nullptr) return hb_invalid("hb_memcpy_d2h_async");
+  hipError_t err = hipMemcpyAsync(h_dst, d_src, bytes, hipMemcpyDeviceToHost, hb_resolve_stream(s));
+  return err == hipSuccess ? HB_OK : hb_fail(err, "hb_memcpy_d2h_async");
+}
+
 int hb_memcpy_d2d(void *d_dst, const void *d_src, size_t bytes, hb_stream s) {
   if (bytes == 0) return HB_OK;
   if (d_dst == nullptr || d_src == nullptr) return hb_invalid("hb_memcpy_d2d");

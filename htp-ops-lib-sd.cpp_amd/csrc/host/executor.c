@@ -301,6 +301,55 @@ int htp_executor_message_end(void) {
 
 /* ---- opcode 15 --------------------------------------------------------------- */
 
+/* Rows per batch of the CPU-control variant, planned as the reference plans
+ * its M chunks for its 8 MB VTCM (reference src/dsp/ops/linear_w8a8.c:338-390),
+ * so a caller sees the same batch boundaries: with W8A8_CONTROL_WEIGHT_FIRST
+ * and every weight resident beside one 64-row activation slab, the caller's
+ * resident_batch_rows in 64-row slabs (at least one, at most what the VTCM
+ * holds beside the weights); otherwise as many 64-row slabs as min(2 MB, the
+ * VTCM left beside one weight slab) holds, at most 64.  Also returns the
+ * resident weight columns (in 64s) the reference reports. */
+static int cpu_batch_rows(int m, int k, int n, uint32_t flags, uint32_t resident_rows, uint32_t *weight_columns) {
+  const size_t vtcm = (size_t)8 << 20, planes = (size_t)1 << 20, meta = 1024u + 4096u * 4u;
+  const size_t slab = (size_t)k * 64u; /* one 64-column weight slab = one 64-row activation slab */
+  const size_t all_weights = (size_t)k * (size_t)n;
+  const long slabs_m = (m + 63) / 64;
+  long slabs;
+  size_t weight_area;
+  if ((flags & W8A8_CONTROL_WEIGHT_FIRST) && all_weights + planes + meta + slab <= vtcm) {
+    const long room = (long)((vtcm - planes - meta - all_weights) / slab);
+    slabs = (long)(resident_rows / 64u);
+    if (slabs > room) slabs = room;
+    if (slabs > slabs_m) slabs = slabs_m;
+    if (slabs < 1) slabs = 1;
+    weight_area = all_weights;
+  } else {
+    size_t budget = vtcm > planes + meta + slab ? vtcm - planes - meta - slab : 0;
+    if (budget > ((size_t)2 << 20)) budget = (size_t)2 << 20;
+    slabs = (long)(budget / slab);
+    if (slabs > 64) slabs = 64;
+    if (slabs > slabs_m) slabs = slabs_m;
+    if (slabs < 1) slabs = 1;
+    const size_t used = (size_t)slabs * slab + planes + meta;
+    weight_area = vtcm > used ? (vtcm - used) / slab * slab : slab;
+  }
+  *weight_columns = (uint32_t)(weight_area / slab);
+  return (int)(slabs * 64);
+}
+
+/* Events that mark each CPU-control batch done (created once, reused under
+ * the executor lock). */
+static hb_event g_batch_events[W8A8_CPU_MAX_BATCHES];
+static int g_batch_events_n = 0;
+
+static int batch_events(int count) {
+  while (g_batch_events_n < count) {
+    if (hb_event_create(&g_batch_events[g_batch_events_n]) != HB_OK) return -5;
+    ++g_batch_events_n;
+  }
+  return 0;
+}
+
 static int exec_w8a8(uint8_t *payload, size_t payload_size) {
   /* reference src/dsp/op_executor.cc:314-353 */
   if (payload_size != sizeof(struct NativeW8A8Params) && payload_size != sizeof(struct NativeW8A8ProfileParams) &&
@@ -385,9 +434,41 @@ static int exec_w8a8(uint8_t *payload, size_t payload_size) {
   void *raw = cpu_output || split_readout ? htp_executor_scratch(1, (size_t)m * n * 4u) : NULL;
   if (!y || ((cpu_output || split_readout) && !raw)) return -5;
 
+  /* CPU-control variant: the control block as the caller left it (flags,
+   * requested batch rows), the batch plan, and the block's diagnostics; a
+   * host-resident block is updated in place, so the caller may poll
+   * `produced` while the batches complete. */
+  struct W8A8CpuControl *hc = NULL;
+  int batch_rows = m, nbatch = 1;
+  if (cpu_output) {
+    if (ctl.is_device) {
+      hc = (struct W8A8CpuControl *)malloc(sizeof(*hc));
+      if (!hc || hb_memcpy_d2h(hc, ctl.dev, sizeof(*hc), s) != HB_OK) {
+        free(hc);
+        return -5;
+      }
+    } else {
+      hc = (struct W8A8CpuControl *)ctl.host;
+    }
+    uint32_t weight_columns = 0;
+    batch_rows = cpu_batch_rows(m, k, n, hc->flags, hc->resident_batch_rows, &weight_columns);
+    nbatch = (m + batch_rows - 1) / batch_rows;
+    if (batch_events(nbatch)) {
+      if (ctl.is_device) free(hc);
+      return -5;
+    }
+    __atomic_store_n(&hc->produced, 0u, __ATOMIC_RELEASE);
+    hc->vtcm_bytes = 8u << 20; /* the budget the batches are planned for */
+    hc->activation_rows = (uint32_t)batch_rows;
+    hc->weight_columns = weight_columns;
+    hc->weight_loads = built ? 1u : 0u;
+    hc->weight_loaded_bytes = built ? (uint64_t)k * n : 0u;
+  }
+
   event_set ev;
   if (events_open(&ev, 4)) {
     events_close(&ev);
+    if (cpu_output && ctl.is_device) free(hc);
     return -5;
   }
   int hrc = hb_event_record(ev.e[0], s);
@@ -402,19 +483,53 @@ static int exec_w8a8(uint8_t *payload, size_t payload_size) {
   /* the phase events only where phases are reported (each record is a host
    * call and a GPU packet: about 2 us per request at M=1) */
   if (!hrc && split) hrc = hb_event_record(ev.e[1], s);
-  if (!hrc) {
+  /* the row scales reach a host-resident control block with the first batch */
+  if (!hrc && cpu_output && !ctl.is_device) hrc = hb_memcpy_d2h_async(hc->scales, scales, (size_t)m * 4u, s);
+  if (!hrc && cpu_output) {
+    /* batch b: its rows' accumulators, their byte planes in the output, and
+     * (host-resident output) their copy to the host, then its event */
+    const size_t kp = (size_t)(k + 63) / 64 * 64, row_bytes = (size_t)n * 4u;
+    for (int b = 0; !hrc && b < nbatch; ++b) {
+      const int m0 = b * batch_rows, rows = m - m0 < batch_rows ? m - m0 : batch_rows;
+      int32_t *rb = (int32_t *)raw + (size_t)m0 * n;
+      uint8_t *yb = (uint8_t *)y + (size_t)m0 * row_bytes, *ob = (uint8_t *)out.dev + (size_t)m0 * row_bytes;
+      hrc = hb_w8a8_gemm(rb, n, q + (size_t)m0 * kp, scales + m0, packed, rows, k, n, HB_W8A8_EPI_RAW, s);
+      if (!hrc) hrc = hb_w8a8_planes_from_raw(yb, rb, rows, n, s);
+      if (!hrc && (void *)y != (void *)out.dev) hrc = hb_memcpy_d2d(ob, yb, (size_t)rows * row_bytes, s);
+      if (!hrc && !out.is_device)
+        hrc = hb_memcpy_d2h_async((uint8_t *)out.host + (size_t)m0 * row_bytes, ob, (size_t)rows * row_bytes, s);
+      if (!hrc) hrc = hb_event_record(g_batch_events[b], s);
+    }
+  } else if (!hrc) {
     if (!split) hrc = hb_w8a8_linear(y, x, packed, m, k, n, HB_W8A8_EPI_SCALE, ws, ws_bytes, s);
-    else if (cpu_output || split_readout) hrc = hb_w8a8_gemm(raw, n, q, scales, packed, m, k, n, HB_W8A8_EPI_RAW, s);
+    else if (split_readout) hrc = hb_w8a8_gemm(raw, n, q, scales, packed, m, k, n, HB_W8A8_EPI_RAW, s);
     else hrc = hb_w8a8_gemm(y, n, q, scales, packed, m, k, n, HB_W8A8_EPI_SCALE, s);
   }
   if (!hrc && split) hrc = hb_event_record(ev.e[2], s);
-  if (!hrc && cpu_output) hrc = hb_w8a8_planes_from_raw((uint8_t *)y, (const int32_t *)raw, m, n, s);
   if (!hrc && split_readout)
     hrc = hb_w8a8_readout(y, n, (const int32_t *)raw, scales, packed, m, k, n, HB_W8A8_EPI_SCALE, s);
   if (!hrc) hrc = hb_event_record(ev.e[3], s);
-  if (!hrc && (void *)y != (void *)out.dev) hrc = hb_memcpy_d2d(out.dev, y, out.bytes, s);
+  if (!hrc && !cpu_output && (void *)y != (void *)out.dev) hrc = hb_memcpy_d2d(out.dev, y, out.bytes, s);
+  if (!hrc && cpu_output && !ctl.is_device) {
+    /* publish each batch as soon as it is done (reference
+     * src/dsp/ops/linear_w8a8.c:512-526): the caller's CPU epilogue of
+     * batch b overlaps the GPU's work on the batches after it */
+    for (int b = 0; !hrc && b < nbatch; ++b) {
+      if (hb_event_sync(g_batch_events[b]) != HB_OK) {
+        hrc = -5;
+        break;
+      }
+      const int m0 = b * batch_rows, rows = m - m0 < batch_rows ? m - m0 : batch_rows;
+      hc->batches[b].m0 = m0;
+      hc->batches[b].rows = rows;
+      hc->batches[b].n0 = 0;
+      hc->batches[b].columns = n / 64;
+      __atomic_store_n(&hc->produced, (uint32_t)(b + 1), __ATOMIC_RELEASE);
+    }
+  }
   if (hrc) {
     events_close(&ev);
+    if (cpu_output && ctl.is_device) free(hc);
     return hrc == HB_E_INVAL ? -10 : -5;
   }
   const double weight_s = built ? t_w1 - t_w0 : 0.0;
@@ -424,41 +539,34 @@ static int exec_w8a8(uint8_t *payload, size_t payload_size) {
   }
   if (hb_stream_sync(s) != HB_OK) {
     events_close(&ev);
+    if (cpu_output && ctl.is_device) free(hc);
     return -5;
   }
-  /* a plain request recorded only the bracketing events: all its time is GEMM time */
+  /* a plain request recorded only the bracketing events: all its time is GEMM
+   * time; a CPU-control request's batches (GEMM, planes and copies) all count
+   * as GEMM time */
   const double quant_ms = split ? event_ms(&ev, 0, 1) : 0.0;
   const double gemm_ms = split ? event_ms(&ev, 1, 2) : event_ms(&ev, 0, 3);
   const double out_ms = split ? event_ms(&ev, 2, 3) : 0.0;
   events_close(&ev);
 
-  if (cpu_output) {
-    /* Publish row scales and one batch covering every row
-     * (reference src/dsp/ops/linear_w8a8.c:413-438, :512-526). */
-    struct W8A8CpuControl *c = (struct W8A8CpuControl *)malloc(sizeof(*c));
-    if (!c) return -5;
-    int crc = 0;
-    if (ctl.is_device) crc = hb_memcpy_d2h(c, ctl.dev, sizeof(*c), s) != HB_OK;
-    else memcpy(c, ctl.host, sizeof(*c));
-    if (!crc) crc = hb_memcpy_d2h(c->scales, scales, (size_t)m * 4u, s) != HB_OK;
-    if (!crc) {
-      c->vtcm_bytes = 0;
-      c->activation_rows = (uint32_t)((m + 63) / 64 * 64);
-      c->weight_columns = (uint32_t)(n / 64);
-      c->weight_loads = built ? 1u : 0u;
-      c->weight_loaded_bytes = built ? (uint64_t)k * n : 0u;
-      c->batches[0].m0 = 0;
-      c->batches[0].rows = m;
-      c->batches[0].n0 = 0;
-      c->batches[0].columns = n / 64;
-      c->produced = 1;
-      if (ctl.is_device) crc = hb_memcpy_h2d(ctl.dev, c, sizeof(*c), s) != HB_OK;
-      else memcpy(ctl.host, c, sizeof(*c));
+  if (cpu_output && ctl.is_device) {
+    /* an HBM-resident control block is written once, after every batch */
+    int crc = hb_memcpy_d2h(hc->scales, scales, (size_t)m * 4u, s) != HB_OK;
+    for (int b = 0; b < nbatch; ++b) {
+      const int m0 = b * batch_rows;
+      hc->batches[b].m0 = m0;
+      hc->batches[b].rows = m - m0 < batch_rows ? m - m0 : batch_rows;
+      hc->batches[b].n0 = 0;
+      hc->batches[b].columns = n / 64;
     }
-    free(c);
+    hc->produced = (uint32_t)nbatch;
+    if (!crc) crc = hb_memcpy_h2d(ctl.dev, hc, sizeof(*hc), s) != HB_OK;
+    free(hc);
     if (crc) return -5;
   }
-  if (stage_out(&out, s)) return -5;
+  /* (a CPU-control request copied its host-resident output batch by batch) */
+  if (!cpu_output && stage_out(&out, s)) return -5;
   htp_registry_touch(out.fd, out.offset, out.bytes);
 
   const double total_us = (quant_ms + gemm_ms + out_ms) * 1e3 + weight_s * 1e6;

@@ -43,6 +43,7 @@ _SIGNATURES = {
     "hb_host_free": (_c_int, [_c_void_p]),
     "hb_memcpy_h2d": (_c_int, [_c_void_p, _c_void_p, _c_size_t, _c_void_p]),
     "hb_memcpy_d2h": (_c_int, [_c_void_p, _c_void_p, _c_size_t, _c_void_p]),
+    "hb_memcpy_d2h_async": (_c_int, [_c_void_p, _c_void_p, _c_size_t, _c_void_p]),
     "hb_memcpy_d2d": (_c_int, [_c_void_p, _c_void_p, _c_size_t, _c_void_p]),
     "hb_memset": (_c_int, [_c_void_p, _c_int, _c_size_t, _c_void_p]),
     "hb_stream_create": (_c_int, [ctypes.POINTER(_c_void_p)]),

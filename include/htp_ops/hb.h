@@ -55,6 +55,10 @@ int hb_host_free(void *h_ptr);
 int hb_memcpy_h2d(void *d_dst, const void *h_src, size_t bytes, hb_stream s);
 int hb_memcpy_d2h(void *h_dst, const void *d_src, size_t bytes, hb_stream s);
 int hb_memcpy_d2d(void *d_dst, const void *d_src, size_t bytes, hb_stream s);
+/* Device -> host copy queued on s without waiting (h_dst pinned, e.g. a
+ * host rpcmem buffer); complete once later work on s, or an event recorded
+ * after it, has completed. */
+int hb_memcpy_d2h_async(void *h_dst, const void *d_src, size_t bytes, hb_stream s);
 int hb_memset(void *d_dst, int value, size_t bytes, hb_stream s);
 int hb_stream_create(hb_stream *s);
 int hb_stream_destroy(hb_stream s);

@@ -131,6 +131,42 @@ def test_opcode15_cpu_control_variant(hip, orc):
     assert struct.unpack_from("<4i", c, 16512) == (0, m, 0, n // 64)
 
 
+@pytest.mark.parametrize("m,k,n,flags,resident,rows,wcols,out_dev,ctl_dev", [
+    # activation-first plan: min(2 MB, VTCM beside one slab) / (64 k) = 5 slabs of 64 rows at k = 6144;
+    # 13 resident weight slabs beside them (reference linear_w8a8.c:380-388)
+    (700, 6144, 256, 0, 0, 320, 13, False, False),
+    # weight-first (all 512 columns resident): the caller's 200 rows -> 3 slabs (linear_w8a8.c:373-379)
+    (700, 256, 512, 1, 200, 192, 8, True, False),
+    # HBM-resident output and control block
+    (700, 6144, 256, 0, 0, 320, 13, True, True),
+])
+def test_opcode15_cpu_control_batches(hip, orc, m, k, n, flags, resident, rows, wcols, out_dev, ctl_dev):
+    """The CPU-control variant publishes one batch per M chunk of the
+    reference's plan; planes, scales and batch records of every chunk."""
+    x, blob = w8a8_inputs(orc, m, k, n, seed=m + k)
+    out, act, cst, ctl = (rpc(m * n * 4, out_dev), rpc(m * k * 4, False), rpc(blob.nbytes, False),
+                          rpc(17536, ctl_dev))
+    act.write(x)
+    cst.write(blob)
+    c0 = np.zeros(17536, np.uint8)
+    struct.pack_into("<I", c0, 4, flags)
+    struct.pack_into("<I", c0, 32, resident)
+    struct.pack_into("<I", c0, 0, 99)  # stale progress from an earlier call
+    ctl.write(c0)
+    payload = h.w8a8_params((out.fd, 0), (act.fd, 0), (cst.fd, 0), m, k, n) + struct.pack("<ii", ctl.fd, 0)
+    rc, _ = h.execute(15, payload)
+    assert rc == 0
+    u, s = orc.quantize(x, np.ones(k, np.float32))
+    assert np.array_equal(out.read(np.uint8, m * n * 4), orc.planes(orc.accumulate(u, blob, k, n)))
+    c = ctl.read(np.uint8, 17536)
+    nb = (m + rows - 1) // rows
+    assert struct.unpack_from("<I", c, 0)[0] == nb                      # produced
+    assert struct.unpack_from("<III", c, 8) == (8 << 20, rows, wcols)    # vtcm_bytes, activation_rows, weight_columns
+    assert np.array_equal(np.frombuffer(c[128:128 + 4 * m].tobytes(), np.float32), s)
+    for b in range(nb):
+        assert struct.unpack_from("<4i", c, 16512 + 16 * b) == (b * rows, min(rows, m - b * rows), 0, n // 64)
+
+
 def test_opcode15_weight_cache_follows_rewrites(hip, orc):
     m, k, n = 16, 256, 256
     x, blob1 = w8a8_inputs(orc, m, k, n, seed=21)
