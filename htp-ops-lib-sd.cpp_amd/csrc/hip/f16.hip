@@ -10,6 +10,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <cstdlib>
 #include <type_traits>
 
 #include "hb_internal.h"
@@ -634,7 +635,9 @@ __device__ inline void qk0_load(Qk0Raw<TYPE> &r, const uint8_t *__restrict__ blo
 // IQ4_NL code book + 128, as bytes (ggml's kvalues_iq4nl).
 constexpr uint32_t kIq4Biased[4] = {0x3F2D1801u, 0x766A5D4Fu, 0xA6998D81u, 0xF1D9C5B5u};
 
-// Four nibbles (one per byte) -> their biased IQ4_NL codes.
+// Four nibbles (one per byte) -> their biased IQ4_NL codes: two byte
+// permutes look up the low and high halves of the code book, bit 3 of each
+// nibble picks one (v_bfi).
 __device__ inline uint32_t iq4_lookup(uint32_t nib) {
   const uint32_t sel = nib & 0x07070707u;
   const uint32_t lo = __builtin_amdgcn_perm(kIq4Biased[1], kIq4Biased[0], sel);
@@ -643,41 +646,58 @@ __device__ inline uint32_t iq4_lookup(uint32_t nib) {
   return (hi & m) | (lo & ~m);
 }
 
+// The 8 fp16 weights a lane holds of one fragment.  Pair p's two codes go
+// into the low bytes of an fp16 pair whose high bytes are 0x64 (the value
+// 1024 + code, exact), one packed subtract of the bias leaves the exact
+// code, one packed multiply by the pair's scale rounds code * scale once.
+// The byte moves are single permutes where the codes are whole bytes and an
+// and-or where they are nibbles (Q4_0); the scale of pair p (low or high
+// half of scale word p) is broadcast to both halves by one permute.
 template <int TYPE>
 __device__ inline hb_f16x8 qk0_fragment(const Qk0Raw<TYPE> &r, int odd) {
-  uint32_t u[4];  // pair p: two biased codes in the low byte of each half
+  constexpr uint32_t kExp = 0x64646464u;  // permute source of the 0x64 high bytes (selector 4)
+  uint32_t u[4];  // pair p: 0x64 | code0, 0x64 | code1
   float bias;
   if constexpr (TYPE == HB_GGML_Q8_0) {
+    // int8 codes: +128 by flipping bit 7 (the 0x64 bytes are untouched)
 #pragma unroll
-    for (int p = 0; p < 4; ++p) u[p] = ((r.q[p] & 0xFFu) | ((r.q[p] & 0xFF00u) << 8)) ^ 0x00800080u;
+    for (int p = 0; p < 4; ++p) u[p] = __builtin_amdgcn_perm(kExp, r.q[p], 0x04010400u) ^ 0x00800080u;
+    bias = 1152.0f;
+  } else if constexpr (TYPE == HB_GGML_IQ4_NL) {
+    // pair p takes bytes (0,2), (1,3) of the low nibbles' codes for p = 0, 1, of the high for p = 2, 3
+    const uint32_t lo = iq4_lookup(r.q[0] & 0x0F0F0F0Fu), hi = iq4_lookup((r.q[0] >> 4) & 0x0F0F0F0Fu);
+    u[0] = __builtin_amdgcn_perm(kExp, lo, 0x04020400u);
+    u[1] = __builtin_amdgcn_perm(kExp, lo, 0x04030401u);
+    u[2] = __builtin_amdgcn_perm(kExp, hi, 0x04020400u);
+    u[3] = __builtin_amdgcn_perm(kExp, hi, 0x04030401u);
     bias = 1152.0f;
   } else {
-    uint32_t lo = r.q[0] & 0x0F0F0F0Fu, hi = (r.q[0] >> 4) & 0x0F0F0F0Fu;
-    if constexpr (TYPE == HB_GGML_IQ4_NL) {
-      lo = iq4_lookup(lo);
-      hi = iq4_lookup(hi);
-      bias = 1152.0f;
-    } else {
-      bias = 1032.0f;
-    }
-    u[0] = lo & 0x00FF00FFu;
-    u[1] = (lo >> 8) & 0x00FF00FFu;
-    u[2] = hi & 0x00FF00FFu;
-    u[3] = (hi >> 8) & 0x00FF00FFu;
+    // Q4_0: pair p takes the low nibbles of bytes (0,2), (1,3) for p = 0, 1,
+    // the high nibbles for p = 2, 3
+    // (one v_and_or_b32 each; gfx9 VOP3 takes no literal, so the mask comes
+    // from an SGPR and the exponent bytes from a VGPR)
+    const uint32_t w = r.q[0];
+    const uint32_t nib = __builtin_amdgcn_readfirstlane(0x000F000Fu);
+    uint32_t e = 0x64006400u;
+    asm("" : "+v"(e));  // keep the exponent bytes in a VGPR
+    const uint32_t src[4] = {w, w >> 8, w >> 4, w >> 12};
+#pragma unroll
+    for (int p = 0; p < 4; ++p) asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(u[p]) : "v"(src[p]), "s"(nib), "v"(e));
+    bias = 1032.0f;
   }
   const hb_f16x2 b2 = {(_Float16)bias, (_Float16)bias};
-  hb_f16x8 out;
+  const uint32_t ssel = odd ? 0x03020302u : 0x01000100u;
+  hb_u32x4 out;
 #pragma unroll
   for (int p = 0; p < 4; ++p) {
-    const uint32_t sw = r.s[p];
-    const uint32_t sb = odd ? (sw >> 16) : (sw & 0xFFFFu);
-    const hb_f16x2 sc = __builtin_bit_cast(hb_f16x2, sb | (sb << 16));
-    const hb_f16x2 v = __builtin_bit_cast(hb_f16x2, u[p] | 0x64006400u) - b2;  // exact codes
-    const hb_f16x2 d = v * sc;  // one fp16 rounding of code * scale
-    out[2 * p] = d[0];
-    out[2 * p + 1] = d[1];
+    // the scale of pair p, broadcast to both halves by one permute (a vector
+    // shuffle of the extracted word here was compiled to the multiply's
+    // operand selection on scale word 0 for every p: wrong results)
+    const hb_f16x2 sc = __builtin_bit_cast(hb_f16x2, __builtin_amdgcn_perm(r.s[p], r.s[p], ssel));
+    const hb_f16x2 v = __builtin_bit_cast(hb_f16x2, u[p]) - b2;  // exact codes
+    out[p] = __builtin_bit_cast(uint32_t, v * sc);                 // one fp16 rounding of code * scale
   }
-  return out;
+  return __builtin_bit_cast(hb_f16x8, out);
 }
 
 // One row (m == 1) on quantized weights: one workgroup per 32-column tile,
@@ -744,6 +764,148 @@ __global__ __launch_bounds__(64 * WAVES) void qk0_decode(float *__restrict__ y, 
         const hb_f16x8 w = live ? qk0_fragment<TYPE>(raw[t][j], j) : hb_f16x8{};
         acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, a, acc[j], 0, 0, 0);
       }
+    }
+  }
+  // row 0 of the product: element r of lanes 0, 16, 32, 48 holds column 4*(lane/16) + r
+  if (has_row) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[wave][16 * j + 4 * (lane >> 4) + r] = acc[j][r];
+  }
+  __syncthreads();
+  if (threadIdx.x >= 32) return;
+  float sum = red[0][threadIdx.x];
+#pragma unroll
+  for (int w = 1; w < WAVES; ++w) sum += red[w][threadIdx.x];
+  y[tile * 32 + threadIdx.x] = (float)(_Float16)sum;
+}
+
+// One row (m == 1) on quantized weights, the weights streamed through LDS:
+// the same plan as qk0_decode (a workgroup per 32-column tile; wave w owns
+// k-blocks [w*KB, w*KB + KB), whose 4 super-blocks each lie back to back,
+// so a wave's weights are one contiguous run of KB * 4 * block bytes), but
+// the run arrives in whole 1 KB pieces (buffer_load ... lds, 16 bytes per
+// lane) into a 4 KB ring per wave instead of 2- to 16-byte register loads
+// per lane, which moved up to four times the run's bytes through the CU's
+// memory pipeline (every lane of a super-block fetched its 16 scale bytes).
+// A piece is re-used for the ring once every fragment that reads it has
+// been multiplied; the fragments are dequantized from LDS exactly as from
+// registers (qk0_fragment), so the arithmetic is qk0_decode's.
+template <int TYPE, int WAVES, int KB>
+__global__ __launch_bounds__(64 * WAVES) void qk0_decode_ring(float *__restrict__ y, const float *__restrict__ x,
+                                                             const uint8_t *__restrict__ blocks, int k, int n) {
+  constexpr int BB = qk0_block_bytes<TYPE>(), BLK = 4 * BB;  // bytes of one 32-k block of a tile
+  constexpr int RUN = KB * BLK, NCH = (RUN + 1023) / 1024, RS = 4;
+  constexpr int XV = (WAVES * KB * 8) / (64 * WAVES);  // float4 of the row per thread
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[WAVES][RS * 1024];
+  __shared__ __attribute__((aligned(16))) _Float16 xs[WAVES * KB * 32];
+  __shared__ float red[WAVES][32];
+  const int tile = blockIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int kblocks = k / 32;
+  const int kb0 = wave * KB;
+  // the row first (its registers are needed before any weight arrives)
+  float4 xv[XV];
+#pragma unroll
+  for (int i = 0; i < XV; ++i) xv[i] = *(const float4 *)(x + 4 * min((int)threadIdx.x + 64 * WAVES * i, k / 4 - 1));
+  // this wave's run, piece by piece (global_load_lds: the compiler then tracks
+  // which LDS bytes each piece writes, so reading a landed piece does not wait
+  // for the later ones).  Addresses past the weights are clamped to their
+  // last 16 bytes; those bytes, like other tiles' blocks read past a short K,
+  // are never multiplied.
+  const size_t total = (size_t)(n / 32) * (size_t)kblocks * (size_t)BLK;
+  const size_t run0 = ((size_t)tile * (size_t)kblocks + (size_t)kb0) * (size_t)BLK;
+  uint8_t *const mine = ring[wave];
+  const uint32_t ring_lds = (uint32_t)(uintptr_t)HB_LDS_PTR(mine);  // LDS address of this wave's ring
+  auto piece = [&](int c) {
+    const size_t off = min(run0 + (size_t)c * 1024u + (size_t)lane * 16u, total - 16u);
+    __builtin_amdgcn_global_load_lds(blocks + off, HB_LDS_PTR(mine + (c % RS) * 1024), 16, 0, 0);
+  };
+  // The row goes to LDS before any weight piece is requested: pieces
+  // requested first (by every workgroup at once) queue ahead of the rows in
+  // the memory system and held a workgroup's row back for about 3 us
+  // (phase stamps), with its ring full and nothing to multiply.
+#pragma unroll
+  for (int i = 0; i < XV; ++i) {
+    const int v = threadIdx.x + 64 * WAVES * i;
+    xs[4 * v] = (_Float16)xv[i].x;
+    xs[4 * v + 1] = (_Float16)xv[i].y;
+    xs[4 * v + 2] = (_Float16)xv[i].z;
+    xs[4 * v + 3] = (_Float16)xv[i].w;
+    if (4 * v >= k) *(uint2 *)(xs + 4 * v) = make_uint2(0u, 0u);  // zeros past k
+  }
+#pragma unroll
+  for (int c = 0; c < RS && c < NCH; ++c) piece(c);
+  // the row in LDS for every wave (a bare barrier: __syncthreads would also
+  // wait for the pieces in flight)
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  block_barrier();
+  const bool has_row = (lane & 15) == 0;
+  const int q = lane >> 4, c16 = lane & 15;
+  hb_f32x4 acc[2] = {hb_f32x4{0.0f, 0.0f, 0.0f, 0.0f}, hb_f32x4{0.0f, 0.0f, 0.0f, 0.0f}};
+  int issued = RS < NCH ? RS : NCH;
+#pragma unroll
+  for (int t = 0; t < KB; ++t) {
+    // every piece of k-block t has landed: at most (issued - 1 - last) younger pieces outstanding
+    const int last = (t * BLK + BLK - 1) / 1024;
+    switch (issued - 1 - last) {
+      case 0: wait_vmcnt<0>(); break;
+      case 1: wait_vmcnt<1>(); break;
+      case 2: wait_vmcnt<2>(); break;
+      default: wait_vmcnt<3>(); break;
+    }
+    const int kb = kb0 + t;
+    const bool live = kb < kblocks;
+    // every lane reads row 0's values: the other lanes' A values reach only
+    // rows 1-15 of the product, which are never read
+    const hb_f16x8 a = *(const hb_f16x8 *)(xs + kb * 32 + 8 * (lane >> 4));
+    // this lane's super-block in the ring.  The reads are written as LDS
+    // instructions the compiler does not track: it cannot tell them from the
+    // pieces still in flight into the ring, and would wait for every one of
+    // them (vmcnt(0)) before each read; the wait above covers the bytes read.
+    const int sb = (t * BLK + q * BB) % (RS * 1024);
+    Qk0Raw<TYPE> raw[2];
+    hb_u32x4 scales;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(scales) : "v"(ring_lds + (uint32_t)sb));
+    uint32_t codes[2][TYPE == HB_GGML_Q8_0 ? 4 : 1];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int c = j * 16 + c16;
+      if constexpr (TYPE == HB_GGML_Q8_0) {
+#pragma unroll
+        for (int p = 0; p < 4; ++p)
+          asm volatile("ds_read_u16 %0, %1"
+                       : "=v"(codes[j][p])
+                       : "v"(ring_lds + (uint32_t)((sb + 16 + 64 * p + 2 * c) % (RS * 1024))));
+      } else {
+        asm volatile("ds_read_b32 %0, %1" : "=v"(codes[j][0]) : "v"(ring_lds + (uint32_t)((sb + 16 + 4 * c) % (RS * 1024))));
+      }
+    }
+    // the values are used only after this wait (they pass through it)
+    if constexpr (TYPE == HB_GGML_Q8_0)
+      asm volatile("s_waitcnt lgkmcnt(0)"
+                   : "+v"(scales), "+v"(codes[0][0]), "+v"(codes[0][1]), "+v"(codes[0][2]), "+v"(codes[0][3]),
+                     "+v"(codes[1][0]), "+v"(codes[1][1]), "+v"(codes[1][2]), "+v"(codes[1][3]));
+    else
+      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(scales), "+v"(codes[0][0]), "+v"(codes[1][0]));
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      raw[j].s = scales;
+#pragma unroll
+      for (int p = 0; p < (TYPE == HB_GGML_Q8_0 ? 4 : 1); ++p) raw[j].q[p] = codes[j][p];
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const hb_f16x8 w = live ? qk0_fragment<TYPE>(raw[j], j) : hb_f16x8{};
+      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, a, acc[j], 0, 0, 0);
+    }
+    // pieces before k-block t + 1's first are free once these reads are done
+    const int next_first = t + 1 < KB ? ((t + 1) * BLK) / 1024 : NCH;
+    if (issued < NCH && issued < next_first + RS) {
+      __builtin_amdgcn_sched_barrier(0);  // (the reads of the freed pieces completed at the wait above)
+      while (issued < NCH && issued < next_first + RS) piece(issued++);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
   // row 0 of the product: element r of lanes 0, 16, 32, 48 holds column 4*(lane/16) + r
@@ -1203,6 +1365,21 @@ int hb_qk0_gemm_ws(float *d_y, const float *d_x, const uint8_t *d_blocks, int m,
   // One row: the whole-K kernel (measured at k=4096, n=14336, m=1: Q4_0 11.0
   // against 14.1 us split-K; Q8_0 25.3 either way, 16 waves keep its
   // registers at one round).
+  // One row through the LDS ring (k <= 4096).  HTP_OPS_AMD_QK0_RING=0 keeps
+  // the register-load kernel below (comparisons only).
+  static const int ring_on = getenv("HTP_OPS_AMD_QK0_RING") ? atoi(getenv("HTP_OPS_AMD_QK0_RING")) : 1;
+  if (ring_on && m == 1 && k <= 16 * 8 * 32) {
+    if (type == HB_GGML_Q4_0)
+      hipLaunchKernelGGL((qk0_decode_ring<HB_GGML_Q4_0, 16, 8>), dim3(n / 32), dim3(1024), 0, st, d_y, d_x, d_blocks,
+                         k, n);
+    else if (type == HB_GGML_IQ4_NL)
+      hipLaunchKernelGGL((qk0_decode_ring<HB_GGML_IQ4_NL, 16, 8>), dim3(n / 32), dim3(1024), 0, st, d_y, d_x,
+                         d_blocks, k, n);
+    else
+      hipLaunchKernelGGL((qk0_decode_ring<HB_GGML_Q8_0, 16, 8>), dim3(n / 32), dim3(1024), 0, st, d_y, d_x,
+                         d_blocks, k, n);
+    return hb_check_launch("qk0_decode_ring");
+  }
   if (m == 1 && k <= 8 * 16 * 32) {
     if (type == HB_GGML_Q4_0)
       hipLaunchKernelGGL((qk0_decode<HB_GGML_Q4_0, 8, 16, 2>), dim3(n / 32), dim3(512), 0, st, d_y, d_x, d_blocks, k,
