@@ -9,6 +9,8 @@
 // The fp32->fp16 activation conversion is fused into the A-tile staging.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <atomic>
 #include <cstdint>
 #include <cstdlib>
 #include <type_traits>
@@ -421,6 +423,242 @@ __global__ __launch_bounds__(64 * WM *WN) void f16_gemm_ring(float *__restrict__
       }
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// Streaming F16 GEMM (persistent): the plan of the int8 streaming GEMM with
+// fp16 operands.  One workgroup per CU walks its share of BM x BN tiles with
+// one continuous operand ring, so the next tile's first k-steps are in flight
+// while a tile finishes.
+//  - ND DMA waves issue every operand DMA (buffer loads into LDS, 1 KB
+//    lane-ordered blocks of the f16_pack_a image and of the packed weights)
+//    and the tile's bias, wait for their own DMA only and publish each stage
+//    with the workgroup barrier.  A wave's loads and stores complete in issue
+//    order for its s_waitcnt count, so only waves that never store can wait
+//    for one stage while output stores are still draining.
+//  - WM x WN compute waves never load from global memory: each step they read
+//    the next step's fragments from LDS while the current step's MFMAs run.
+//    The weights are the MFMA's first operand, so a lane holds 4 consecutive
+//    columns of one output row; every output element sees the k-steps in the
+//    order f16_gemm_ring uses, so the bits are the same.  At a tile's end they
+//    read out in registers (fp16 readout, bias, activation), trade halves of
+//    each 16-lane row by DPP so that every store fills whole 128-byte lines,
+//    and store without waiting: the stores drain during the next tile.
+//  - The bias of a tile arrives in LDS with the tile's first stage, double
+//    buffered by tile parity.
+//  - The XCD that runs a workgroup (blockIdx % 8) owns a contiguous chunk of
+//    the tiles in 4-row-block groups, so the blocks its workgroups share stay
+//    in its L2.  Workgroups of odd slot start `stagger` ticks of the 100 MHz
+//    real-time counter late, so that the two halves' tile ends, and the store
+//    bursts after them, alternate.
+// Requires gridDim.x % 8 == 0, k / 32 >= S - 1 (a tile's bias buffer is
+// rewritten only after the tile two before it has finished), n % 32 == 0,
+// and both operand images below 4 GB (32-bit buffer offsets).
+// ---------------------------------------------------------------------------
+
+// TAG (the kernel's activation mode) gives each kernel instantiation its own
+// type: hipcc's host pass drops the launch stub of a kernel that shares this
+// device-only type with another instantiation.
+template <int BM, int BN, int ND, int TAG>
+struct F16StreamDma {
+  static constexpr int ABLK = BM / 16, NB = ABLK + BN / 16, PW = NB / ND;
+  static_assert(NB % ND == 0 && ABLK % ND == 0 && BN * 4 <= kFragBytes, "DMA split");
+  uint32_t soff[PW];    // byte offset of each block's k-step 0 in its operand image (uniform)
+  const float *pbias;   // this lane's 16 bytes of the tile's bias (null: no bias)
+  int tile, kt, slot;
+
+  __device__ void point(int tm, int tn, const float *bias, int m, int n, int ktc, int d, int lane) {
+    const int mblocks = (m + 15) / 16, nblocks = n / 16;
+#pragma unroll
+    for (int i = 0; i < PW; ++i) {
+      const int b = i * ND + d;
+      const int blk = i < ABLK / ND ? min(tm * ABLK + b, mblocks - 1) : min(tn * (BN / 16) + (b - ABLK), nblocks - 1);
+      soff[i] = (uint32_t)blk * (uint32_t)ktc * (uint32_t)kFragBytes;
+    }
+    pbias = bias ? bias + min(tn * BN + 4 * min(lane, BN / 4 - 1), n - 4) : nullptr;
+  }
+
+  __device__ void issue(int8_t *lds, int stage_bytes, int8_t *params, int ktc, int S, int d, __amdgpu_buffer_rsrc_t ra,
+                        __amdgpu_buffer_rsrc_t rb, uint32_t l16) {
+    int8_t *dst = lds + slot * stage_bytes;
+#pragma unroll
+    for (int i = 0; i < PW; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(i < ABLK / ND ? ra : rb, HB_LDS_PTR(dst + (i * ND + d) * kFragBytes), 16,
+                                               l16, soff[i] + (uint32_t)kt * (uint32_t)kFragBytes, 0, 0);
+    if (kt == 0 && d == 0 && pbias)
+      __builtin_amdgcn_global_load_lds(pbias, HB_LDS_PTR(params + (tile & 1) * kFragBytes), 16, 0, 0);
+    if (++kt == ktc) kt = 0;
+    if (++slot == S) slot = 0;
+  }
+};
+
+// One output element: fp16 readout of the fp32 sum, bias, activation.
+template <int MODE>
+__device__ inline uint32_t f16_out_bits(float acc, float b, bool has_bias) {
+  const float v = (float)(_Float16)acc;
+  const float z = has_bias ? __fadd_rn(v, b) : v;
+  return __float_as_uint(apply_mode(z, MODE));
+}
+
+// DPP row shifts (within 16-lane rows): lane i takes lane i - 8 / lane i + 8.
+constexpr int kDppRowShr8 = 0x118, kDppRowShl8 = 0x108;
+
+template <int BM, int BN, int WM, int WN, int ND, int S, int MODE>
+__global__ __launch_bounds__(64 * (WM * WN + ND), 1) void f16_gemm_stream(float *__restrict__ y,
+                                                                         const int8_t *__restrict__ aimg,
+                                                                         const int8_t *__restrict__ wpack,
+                                                                         const float *__restrict__ bias, int m, int k,
+                                                                         int n, int tiles_m, int tiles_n, int stagger) {
+  constexpr int NW = WM * WN;  // compute waves 0..NW-1; DMA waves NW..NW+ND-1
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int FM = WTM / 16, FN = WTN / 16;
+  constexpr int ABLK = BM / 16;
+  constexpr int STAGE = (ABLK + BN / 16) * kFragBytes;
+  constexpr int SPLIT = FM < 2 ? FM : 2;  // row blocks of a step multiplied before the step's barrier
+  static_assert(FN % 2 == 0, "column blocks in pairs (32 columns, one 128-byte line)");
+  using Dma = F16StreamDma<BM, BN, ND, MODE>;
+  __shared__ __attribute__((aligned(1024))) int8_t lds[S * STAGE + 2 * kFragBytes];
+  int8_t *params = lds + S * STAGE;
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int ktc = k / 32;
+
+  // This workgroup's tiles: chunk [c0, c1) of the grouped order belongs to its XCD.
+  const int total = tiles_m * tiles_n;
+  const int xcd = blockIdx.x % 8, slot = blockIdx.x / 8, nslots = gridDim.x / 8;
+  const int per = (total + 7) / 8;
+  const int c0 = min(total, xcd * per), c1 = min(total, c0 + per);
+  const int ntile = c0 + slot < c1 ? (c1 - c0 - slot + nslots - 1) / nslots : 0;
+  if (ntile == 0) return;
+  const int steps = ntile * ktc;
+  if (stagger > 0 && (slot & 1)) {
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    while (__builtin_amdgcn_s_memrealtime() - t0 < (uint64_t)stagger) __builtin_amdgcn_s_sleep(8);
+  }
+
+  if (wave >= NW) {
+    // --------------------------------- DMA wave ---------------------------------
+    // Stage g + 1 has landed once at most (S - 3) * PW of this wave's DMA
+    // instructions are outstanding while the S - 3 stages after it have been
+    // issued (a tile's first stage may carry the bias load besides, which only
+    // makes the wait longer).  With fewer stages left: vmcnt(0).
+    const int d = wave - NW;
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)aimg, 0, (uint32_t)((m + 15) / 16) * (uint32_t)k * 32u, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rb =
+        __builtin_amdgcn_make_buffer_rsrc((void *)wpack, 0, (uint32_t)n * (uint32_t)k * 2u, 0x00020000);
+    Dma dma;
+    dma.tile = -1;
+    dma.kt = 0;
+    dma.slot = 0;
+    auto next = [&]() {
+      if (dma.kt == 0) {
+        int tm, tn;
+        group_tile(c0 + slot + (++dma.tile) * nslots, tiles_m, tiles_n, tm, tn);
+        dma.point(tm, tn, bias, m, n, ktc, d, lane);
+      }
+      dma.issue(lds, STAGE, params, ktc, S, d, ra, rb, (uint32_t)lane * 16u);
+    };
+    static_assert(S >= 4, "at least one stage in flight behind the awaited one");
+    for (int st = 0; st < S - 1 && st < steps; ++st) next();
+    if (S - 1 <= steps) wait_vmcnt<(S - 2) * Dma::PW>(); else wait_vmcnt<0>();
+    block_barrier();  // stage 0 published
+    for (int g = 0; g < steps; ++g) {
+      if (g + S - 2 < steps) wait_vmcnt<(S - 3) * Dma::PW>();
+      else if (g + 1 < steps) wait_vmcnt<0>();
+      block_barrier();  // stage g + 1 published; every compute wave is done with stage g - 1
+      if (g + S - 1 < steps) next();  // into the slot stage g - 1 held
+    }
+    return;
+  }
+
+  // ------------------------------- compute wave -------------------------------
+  const int wm = wave / WN, wn = wave % WN;
+  hb_f32x4 acc[FM][FN];
+  hb_f16x8 fa[2][FM], fb[2][FN];
+  const int aoff = (wm * FM) * kFragBytes + lane * 16, boff = (ABLK + wn * FN) * kFragBytes + lane * 16;
+  const int lcol = wn * WTN + 4 * (lane >> 4);                // tile column of this lane in block 0
+  const int scol = 16 * ((lane >> 3) & 1) + 4 * (lane >> 4);  // column in a 32-column pair after the DPP trade
+  const bool has_bias = bias != nullptr;
+  block_barrier();  // stage 0 published
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = hb_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int i = 0; i < FM; ++i) fa[0][i] = *(const hb_f16x8 *)(lds + aoff + i * kFragBytes);
+#pragma unroll
+  for (int j = 0; j < FN; ++j) fb[0][j] = *(const hb_f16x8 *)(lds + boff + j * kFragBytes);
+  int r = 0, kt = 0, rd_slot = 1 % S;  // tile and k-step of the step; slot of the next fragments
+
+#define F16_STREAM_MFMA(P, I0, I1)                                                                          \
+  _Pragma("unroll") for (int i = (I0); i < (I1); ++i) _Pragma("unroll") for (int j = 0; j < FN; ++j) acc[i][j] = \
+      __builtin_amdgcn_mfma_f32_16x16x32_f16(fb[P][j], fa[P][i], acc[i][j], 0, 0, 0);
+#define F16_STREAM_STEP(P)                                                                                  \
+  {                                                                                                         \
+    F16_STREAM_MFMA(P, 0, SPLIT)                                                                            \
+    __builtin_amdgcn_sched_barrier(0);                                                                      \
+    block_barrier();                                                                                        \
+    __builtin_amdgcn_sched_barrier(0);                                                                      \
+    {                                                                                                       \
+      /* unconditional (after the last step it reads a stale slot, unused): a branch here */                \
+      /* would make the compiler wait for these reads before the MFMAs below */                             \
+      const int8_t *base = lds + rd_slot * STAGE;                                                           \
+      if (++rd_slot == S) rd_slot = 0;                                                                      \
+      _Pragma("unroll") for (int i = 0; i < FM; ++i) fa[1 - (P)][i] =                                       \
+          *(const hb_f16x8 *)(base + aoff + i * kFragBytes);                                                \
+      _Pragma("unroll") for (int j = 0; j < FN; ++j) fb[1 - (P)][j] =                                       \
+          *(const hb_f16x8 *)(base + boff + j * kFragBytes);                                                \
+    }                                                                                                       \
+    __builtin_amdgcn_sched_barrier(0);                                                                      \
+    F16_STREAM_MFMA(P, SPLIT, FM)                                                                           \
+    __builtin_amdgcn_sched_barrier(0);                                                                      \
+    if (++kt == ktc) {                                                                                      \
+      /* readout of tile r: each 16-row x 32-column piece leaves in two stores of 8 whole */                \
+      /* 128-byte lines: the upper 8 lanes of every 16-lane row trade their block-0 values */               \
+      /* for block 1 of the lanes 8 below (DPP), so a lane then holds row lane%8 (+8 in the */              \
+      /* second store) of the piece, columns 16*(lane/8%2) + 4*(lane/16)..+3 of the pair */                 \
+      int tm, tn;                                                                                           \
+      group_tile(c0 + slot + r * nslots, tiles_m, tiles_n, tm, tn);                                         \
+      const float *par = (const float *)(params + (r & 1) * kFragBytes);                                    \
+      const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(                                \
+          y + (size_t)tm * BM * n, 0, (uint32_t)min(BM, m - tm * BM) * (uint32_t)n * 4u, 0x00020000);       \
+      const uint32_t vcol = ((uint32_t)(lane & 7) * (uint32_t)n + (uint32_t)(tn * BN + wn * WTN + scol)) * 4u; \
+      _Pragma("unroll") for (int jp = 0; jp < FN / 2; ++jp) {                                               \
+        const hb_f32x4 b0 = has_bias ? *(const hb_f32x4 *)(par + lcol + jp * 32) : hb_f32x4{0, 0, 0, 0};    \
+        const hb_f32x4 b1 = has_bias ? *(const hb_f32x4 *)(par + lcol + jp * 32 + 16) : hb_f32x4{0, 0, 0, 0}; \
+        /* n % 32 == 0: a 32-column pair lies wholly inside or wholly past n */                            \
+        if (tn * BN + wn * WTN + jp * 32 >= n) continue;                                                    \
+        _Pragma("unroll") for (int i = 0; i < FM; ++i) {                                                    \
+          hb_u32x4 o0, o1, lo, hi;                                                                          \
+          _Pragma("unroll") for (int e = 0; e < 4; ++e) {                                                   \
+            o0[e] = f16_out_bits<MODE>(acc[i][2 * jp][e], b0[e], has_bias);                                 \
+            o1[e] = f16_out_bits<MODE>(acc[i][2 * jp + 1][e], b1[e], has_bias);                             \
+          }                                                                                                 \
+          _Pragma("unroll") for (int e = 0; e < 4; ++e) {                                                   \
+            lo[e] = (uint32_t)__builtin_amdgcn_update_dpp((int)o0[e], (int)o1[e], kDppRowShr8, 0xf, 0xc, false); \
+            hi[e] = (uint32_t)__builtin_amdgcn_update_dpp((int)o1[e], (int)o0[e], kDppRowShl8, 0xf, 0x3, false); \
+          }                                                                                                 \
+          /* the whole offset in the vector operand: the range check that drops rows past m */              \
+          /* does not cover the scalar offset */                                                             \
+          const uint32_t srow = (uint32_t)(wm * WTM + i * 16) * (uint32_t)n * 4u;                            \
+          __builtin_amdgcn_raw_buffer_store_b128(lo, rsrc, vcol + srow + (uint32_t)jp * 128u, 0, 2);        \
+          __builtin_amdgcn_raw_buffer_store_b128(hi, rsrc, vcol + srow + (uint32_t)n * 32u + (uint32_t)jp * 128u, 0, 2); \
+        }                                                                                                   \
+      }                                                                                                     \
+      _Pragma("unroll") for (int i = 0; i < FM; ++i) _Pragma("unroll") for (int j = 0; j < FN; ++j)          \
+          acc[i][j] = hb_f32x4{0.0f, 0.0f, 0.0f, 0.0f};                                                     \
+      kt = 0;                                                                                               \
+      ++r;                                                                                                  \
+    }                                                                                                       \
+  }
+
+  for (int g = 0; g < steps; g += 2) {
+    F16_STREAM_STEP(0)
+    if (g + 1 < steps) F16_STREAM_STEP(1)
+  }
+#undef F16_STREAM_STEP
+#undef F16_STREAM_MFMA
 }
 
 // ---------------------------------------------------------------------------
@@ -1220,7 +1458,7 @@ struct RingShape {
 };
 constexpr RingShape kRingShapes[] = {{128, 192, 2, 100}, {128, 128, 2, 92}, {64, 64, 4, 60}};
 
-int pick_ring_shape(int m, int n) {
+int pick_ring_shape(int m, int n, long long *cost_out = nullptr) {
   const int cus = compute_units();
   int best = -1;
   long long best_cost = -1;
@@ -1235,7 +1473,83 @@ int pick_ring_shape(int m, int n) {
       best = i;
     }
   }
+  if (cost_out) *cost_out = best_cost;
   return best;
+}
+
+// The streaming kernel (f16_gemm_stream, one persistent workgroup per CU,
+// 256 x 128 tiles, 6 stages of 24 KB) where its tiles occupy at least half of
+// the CUs and its cost in the ring shapes' model (rounds of tiles x work per
+// tile per CU) is strictly lower than the best ring shape's.  Measured, us,
+// streaming / ring kernel (one box): chosen at 2048x4096x14336 253 / 264,
+// 4096x6144x1536 99.6 / 114, 1024x4096x4096 51.4 / 59.6; not chosen at
+// 4096x1536x6144 88.0 / 90.3 (equal cost), 4096x1536x4608 80.9 / 75.6 (equal
+// cost), 2048x4096x6144 111 / 106, 2048x1536x6144 50.9 / 49.0 (one whole
+// round of 128 x 192 ring tiles against one and a half of streaming tiles),
+// 512x14336x4096 222 / 125 (64 tiles).  One barrier per two k-steps instead
+// of one per k-step measured within 3 %; the 256 x 192 form needs more
+// registers than three waves per SIMD hold and spilled (3x slower).
+// HTP_OPS_AMD_F16_STREAM gives the initial setting of hb_f16_force_stream;
+// HTP_OPS_AMD_F16_STAGGER=ticks sets the odd slots' start delay.
+constexpr int kF16StreamBM = 256, kF16StreamBN = 128, kF16StreamStages = 6;
+
+bool f16_stream_setting_ok(int v) { return v >= -1 && v <= 1; }
+
+// -1: automatic, 0: off, 1: on wherever it applies.
+std::atomic<int> g_f16_stream{-2};
+
+int f16_stream_mode() {
+  int mode = g_f16_stream.load(std::memory_order_relaxed);
+  if (mode == -2) {
+    const char *v = getenv("HTP_OPS_AMD_F16_STREAM");
+    mode = (v && *v && f16_stream_setting_ok(atoi(v))) ? atoi(v) : -1;
+    int expected = -2;
+    if (!g_f16_stream.compare_exchange_strong(expected, mode)) mode = expected;
+  }
+  return mode;
+}
+
+int f16_stream_stagger(int tiles, int grid) {
+  const char *env = getenv("HTP_OPS_AMD_F16_STAGGER");
+  if (env && *env && atoi(env) >= 0) return atoi(env);
+  const int rounds = tiles % grid == 0 ? tiles / grid : 0;
+  return rounds >= 2 ? 500 : 0;
+}
+
+bool f16_stream_applies(int m, int k, int n) {
+  const int smode = f16_stream_mode();
+  if (smode == 0 || k / 32 < kF16StreamStages - 1) return false;
+  const int mp = (m + 15) / 16 * 16;
+  if ((size_t)mp * (size_t)k * 2u >= ((size_t)1 << 32) || (size_t)n * (size_t)k * 2u >= ((size_t)1 << 32) ||
+      (size_t)kF16StreamBM * (size_t)n * 4u >= ((size_t)1 << 32))
+    return false;
+  if (smode == 1) return true;
+  const long long cus = compute_units();
+  const long long tiles =
+      (long long)((m + kF16StreamBM - 1) / kF16StreamBM) * ((n + kF16StreamBN - 1) / kF16StreamBN);
+  long long ring_cost = 0;
+  pick_ring_shape(m, n, &ring_cost);
+  return 2 * tiles >= cus && (tiles + cus - 1) / cus * kF16StreamBM * kF16StreamBN < ring_cost;
+}
+
+int launch_f16_stream(float *y, const int8_t *a, const int8_t *w, const float *bias, int m, int k, int n, int mode,
+                      hipStream_t st) {
+  constexpr int BM = kF16StreamBM, BN = kF16StreamBN, S = kF16StreamStages;
+  const int tiles_m = (m + BM - 1) / BM, tiles_n = (n + BN - 1) / BN;
+  const int tiles = tiles_m * tiles_n;
+  const int grid = std::min(compute_units(), (tiles + 7) / 8 * 8) / 8 * 8;
+  if (grid < 8) return hb_invalid("f16_gemm_stream grid");
+  const int stagger = f16_stream_stagger(tiles, grid);
+  if (mode == 1)
+    hipLaunchKernelGGL((f16_gemm_stream<BM, BN, 4, 2, 4, S, 1>), dim3(grid), dim3(768), 0, st, y, a, w, bias, m, k, n,
+                       tiles_m, tiles_n, stagger);
+  else if (mode == 2)
+    hipLaunchKernelGGL((f16_gemm_stream<BM, BN, 4, 2, 4, S, 2>), dim3(grid), dim3(768), 0, st, y, a, w, bias, m, k, n,
+                       tiles_m, tiles_n, stagger);
+  else
+    hipLaunchKernelGGL((f16_gemm_stream<BM, BN, 4, 2, 4, S, 0>), dim3(grid), dim3(768), 0, st, y, a, w, bias, m, k, n,
+                       tiles_m, tiles_n, stagger);
+  return hb_check_launch("f16_gemm_stream");
 }
 
 int launch_ring(float *y, const float *x, const uint16_t *packed, const float *bias, int m, int k, int n, int mode,
@@ -1246,6 +1560,8 @@ int launch_ring(float *y, const float *x, const uint16_t *packed, const float *b
   hipLaunchKernelGGL(f16_pack_a, dim3(pg), dim3(256), 0, st, (uint4 *)ws, x, m, k, mp);
   int rc = hb_check_launch("f16_pack_a");
   if (rc) return rc;
+  if (f16_stream_applies(m, k, n))
+    return launch_f16_stream(y, (const int8_t *)ws, (const int8_t *)packed, bias, m, k, n, mode, st);
   const int shape = pick_ring_shape(m, n);
   const RingShape t = kRingShapes[shape];
   const int grid = ((m + t.bm - 1) / t.bm) * ((n + t.bn - 1) / t.bn);
@@ -1479,6 +1795,13 @@ int hb_f16_gemm_ws(float *d_y, const float *d_x, const uint16_t *d_packed, const
                        m, k, n, channels, mode);
   }
   return hb_check_launch("f16_gemm_tiles");
+}
+
+int hb_f16_force_stream(int setting) {
+  if (!f16_stream_setting_ok(setting)) return hb_invalid("hb_f16_force_stream setting");
+  const int prev = f16_stream_mode();
+  g_f16_stream.store(setting, std::memory_order_relaxed);
+  return prev;
 }
 
 int hb_f16_gemm(float *d_y, const float *d_x, const uint16_t *d_packed, const float *d_bias, int m, int k, int n,

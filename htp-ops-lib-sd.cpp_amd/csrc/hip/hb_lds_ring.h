@@ -36,18 +36,23 @@ __device__ inline void wait_stage(int ahead) {
   }
 }
 
+// Tile p of the grid walked in groups of 4 row blocks, column by column.
+__device__ inline void group_tile(int p, int tiles_m, int tiles_n, int &tm, int &tn) {
+  constexpr int G = 4;
+  const int first_m = (p / (G * tiles_n)) * G;
+  const int gsize = min(tiles_m - first_m, G);
+  const int in_group = p % (G * tiles_n);
+  tm = first_m + in_group % gsize;
+  tn = in_group / gsize;
+}
+
 // Workgroups are dispatched round-robin over the 8 XCDs: tile ids are first
 // made contiguous per XCD, then walked in groups of 4 row-blocks so that
 // workgroups resident together on one XCD share A and B blocks in its L2.
 __device__ inline void tile_coords(int bid, int tiles_m, int tiles_n, int &tm, int &tn) {
   const int total = tiles_m * tiles_n;
   const int pid = (total % 8 == 0) ? (bid % 8) * (total / 8) + bid / 8 : bid;
-  constexpr int G = 4;
-  const int first_m = (pid / (G * tiles_n)) * G;
-  const int gsize = min(tiles_m - first_m, G);
-  const int in_group = pid % (G * tiles_n);
-  tm = first_m + in_group % gsize;
-  tn = in_group / gsize;
+  group_tile(pid, tiles_m, tiles_n, tm, tn);
 }
 
 // Tile of workgroup bid for kernels of one tile per workgroup, XCD-aware in

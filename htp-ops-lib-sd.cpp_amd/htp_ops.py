@@ -75,6 +75,7 @@ _SIGNATURES = {
     "hb_w8a8_static_setup": (_c_int, [_c_int]),
     "hb_w8a8_linear_noalloc": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_void_p]),
     "hb_w8a8_force_tile": (_c_int, [_c_int]),
+    "hb_f16_force_stream": (_c_int, [_c_int]),
     "hb_w8a8_gemm_choice": (_c_int, [_c_int, _c_int, _c_int]),
     "hb_w8a8_gemm_tile": (_c_int, [_c_int, _c_int, _c_int, ctypes.POINTER(_c_int), ctypes.POINTER(_c_int)]),
     # F16
@@ -340,6 +341,15 @@ def w8a8_force_tile(index):
     prev = lib().hb_w8a8_force_tile(index)
     if prev < -1:
         check(prev, "hb_w8a8_force_tile")
+    return prev
+
+
+def f16_force_stream(setting):
+    """Pins the F16 large-M kernel: -1 automatic, 0 the ring kernel, 1 the
+    streaming kernel; returns the previous setting."""
+    prev = lib().hb_f16_force_stream(setting)
+    if prev < -1:
+        check(prev, "hb_f16_force_stream")
     return prev
 
 

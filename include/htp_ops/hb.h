@@ -235,6 +235,16 @@ int hb_f16_gemm(float *d_y, const float *d_x, const uint16_t *d_packed, const fl
  * neither applies (the tiled kernel needs none). */
 size_t hb_f16_workspace_bytes(int m, int k, int n);
 
+/* Tuning and test hook of the F16 path for 64 rows or more with a workspace:
+ * -1 restores the automatic choice (the persistent streaming kernel with
+ * 256 x 128 tiles where they occupy at least half of the CUs and spread more
+ * evenly than the ring kernel's, else the one-tile-per-workgroup ring
+ * kernel), 0 keeps the ring
+ * kernel, 1 runs the streaming kernel wherever it applies (k >= 160).
+ * Returns the previous setting.  Results are identical either way.  The
+ * environment variable HTP_OPS_AMD_F16_STREAM gives the initial value. */
+int hb_f16_force_stream(int setting);
+
 /* hb_f16_gemm with a workspace: for m <= 128, a workspace of at least
  * hb_f16_workspace_bytes, and either m <= 16 or a shape whose output tiles
  * (of the size hb_f16_gemm would use) number fewer than the device's CUs, K

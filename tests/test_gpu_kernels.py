@@ -496,11 +496,52 @@ def test_f16_ring_matches_tiles(hip, orc, m, k, n, mode, bias, check_oracle):
     xd = hip.DeviceBuffer.from_array(x)
     bd = hip.DeviceBuffer.from_array(b) if bias else None
     y_ring, y_tiles = hip.DeviceBuffer(m * n * 4), hip.DeviceBuffer(m * n * 4)
-    hip.f16_gemm(y_ring, xd, packed, bd, m, k, n, n, mode, workspace=hip.DeviceBuffer(ws_bytes))
+    prev = hip.f16_force_stream(0)
+    try:
+        hip.f16_gemm(y_ring, xd, packed, bd, m, k, n, n, mode, workspace=hip.DeviceBuffer(ws_bytes))
+    finally:
+        hip.f16_force_stream(prev)
     hip.f16_gemm(y_tiles, xd, packed, bd, m, k, n, n, mode)
     hip.sync()
     got = y_ring.read(np.uint32, m * n)
     np.testing.assert_array_equal(got, y_tiles.read(np.uint32, m * n))
+    if check_oracle:
+        ref = orc.f16_gemm_epilogue(x, perm, b, m, k, n, n, mode)
+        v_ref = orc.f16_gemm_epilogue(x, perm, None, m, k, n, n, 0)
+        bias_cols = np.abs(b)[None, :] if b is not None else 0.0
+        assert_f16_close(got.view(np.float32).reshape(m, n), ref, v_ref, bias_cols, f16_abs_dot(x, w), k)
+
+
+@pytest.mark.parametrize("m,k,n,mode,bias,check_oracle", [
+    (512, 256, 1024, 0, True, True),      # one tile per workgroup
+    (700, 160, 576, 1, False, True),      # rows past m, columns past n, k at the 6-stage minimum, GELU
+    (700, 192, 640, 2, True, True),       # QuickGELU
+    (4096, 256, 3072, 0, False, False),   # 384 tiles: some workgroups take two
+    (4096, 320, 4096, 2, True, False),    # two whole rounds: the odd slots start late
+    (4096, 256, 6144, 1, True, False),    # three rounds, GELU
+    (2048, 1536, 1152, 0, True, False),   # long k, few tiles
+])
+def test_f16_stream_matches_ring(hip, orc, m, k, n, mode, bias, check_oracle):
+    """The persistent streaming F16 kernel gives the same bits as the ring
+    kernel (same MFMA sequence per output element, weights as the first
+    operand) and stays within the F16 bound of the oracle."""
+    ws = hip.DeviceBuffer(hip.f16_workspace_bytes(m, k, n))
+    x, w, perm, b = f16_case(orc, m, k, n, seed=m + k + n + 7, bias=bias)
+    packed = hip.f16_prepack(hip.DeviceBuffer.from_array(perm), k, n)
+    xd = hip.DeviceBuffer.from_array(x)
+    bd = hip.DeviceBuffer.from_array(b) if bias else None
+    y_stream, y_ring = hip.DeviceBuffer(m * n * 4), hip.DeviceBuffer(m * n * 4)
+    y_stream.fill(0xFF)
+    prev = hip.f16_force_stream(1)
+    try:
+        hip.f16_gemm(y_stream, xd, packed, bd, m, k, n, n, mode, workspace=ws)
+        hip.f16_force_stream(0)
+        hip.f16_gemm(y_ring, xd, packed, bd, m, k, n, n, mode, workspace=ws)
+    finally:
+        hip.f16_force_stream(prev)
+    hip.sync()
+    got = y_stream.read(np.uint32, m * n)
+    np.testing.assert_array_equal(got, y_ring.read(np.uint32, m * n))
     if check_oracle:
         ref = orc.f16_gemm_epilogue(x, perm, b, m, k, n, n, mode)
         v_ref = orc.f16_gemm_epilogue(x, perm, None, m, k, n, n, 0)
