@@ -405,7 +405,15 @@ def read_traffic():
 def decode_case(m, k, n, steps, warmup, rotate):
     r = run_w8a8(m, k, n, steps, warmup, rotate, scale=(5e-5, 5e-4))
     op_bytes = w8a8_bytes(m, k, n)
-    return {"shape": f"M={m} K={k} N={n}", "path": "fused quantize+GEMM kernel" if m == 1 else "quantize, GEMM",
+    # the path hb_w8a8_linear takes at these shapes (k % 32 == 0, n % 16 == 0)
+    kp = (k + 63) // 64 * 64
+    if m == 1 and kp <= 32 * 512:
+        path = "fused quantize+GEMM kernel"
+    elif 2 <= m <= 4 and kp <= 8 * 8 * 64:
+        path = "fused few-row quantize+GEMM kernel"
+    else:
+        path = "quantize, GEMM"
+    return {"shape": f"M={m} K={k} N={n}", "path": path,
             "us_per_call": round(r["ms_per_step"] * 1e3, 3),
             "gbps": round(op_bytes / (r["ms_per_step"] * 1e-3) / 1e9, 1),
             "frac_hbm": round(op_bytes / (r["ms_per_step"] * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
