@@ -14,6 +14,7 @@
 #include <stdlib.h>
 #include <string.h>
 #include <time.h>
+#include <unistd.h>
 
 #include "host_internal.h"
 #include "htp_ops/executor.h"
@@ -82,7 +83,7 @@ static inline uint64_t rotl64(uint64_t v, int r) { return (v << r) | (v >> (64 -
 
 /* Hash of every byte of a host buffer: four independent 64-bit
  * multiply-rotate lanes over 32-byte blocks, then the tail bytes (about
- * 10 GB/s on one core, so a 9.4 MB weight costs about 1 ms). */
+ * 10 GB/s on one core). */
 static uint64_t content_hash(const uint8_t *p, size_t n) {
   const uint64_t k1 = 0x9e3779b97f4a7c15ull, k2 = 0xc2b2ae3d27d4eb4full;
   uint64_t lane[4] = {k1, k2, k1 ^ 0x5555555555555555ull, k2 ^ 0xaaaaaaaaaaaaaaaaull};
@@ -95,6 +96,67 @@ static uint64_t content_hash(const uint8_t *p, size_t n) {
   uint64_t h = (uint64_t)n * k2;
   for (int j = 0; j < 4; ++j) h = rotl64(h ^ lane[j], 31) * k1;
   for (; i < n; ++i) h = (h ^ p[i]) * 1099511628211ull;
+  return h ^ (h >> 32);
+}
+
+/* Hash of every byte of a large host buffer: content_hash of each 1 MiB
+ * chunk, combined in chunk order, the chunks shared out over up to 8 threads
+ * (the caller's among them).  The signature is the same whatever the thread
+ * count or whether a thread could be started: a share that finds no thread
+ * is hashed by the caller. */
+#define HASH_CHUNK ((size_t)1 << 20)
+#define HASH_MAX_THREADS 8
+
+typedef struct {
+  const uint8_t *p;
+  size_t n, c0, c1;
+  uint64_t *out;
+} hash_share;
+
+static void hash_chunks(const hash_share *sh) {
+  for (size_t c = sh->c0; c < sh->c1; ++c) {
+    const size_t off = c * HASH_CHUNK;
+    sh->out[c] = content_hash(sh->p + off, sh->n - off < HASH_CHUNK ? sh->n - off : HASH_CHUNK);
+  }
+}
+
+static void *hash_worker(void *arg) {
+  hash_chunks((const hash_share *)arg);
+  return NULL;
+}
+
+static uint64_t content_signature(const uint8_t *p, size_t n) {
+  if (n < 4 * HASH_CHUNK) return content_hash(p, n);
+  const uint64_t k1 = 0x9e3779b97f4a7c15ull, k2 = 0xc2b2ae3d27d4eb4full;
+  const size_t chunks = (n + HASH_CHUNK - 1) / HASH_CHUNK;
+  uint64_t *hc = malloc(chunks * sizeof(uint64_t));
+  uint64_t h = (uint64_t)n * k2;
+  if (!hc) {
+    for (size_t c = 0; c < chunks; ++c) {
+      const size_t off = c * HASH_CHUNK;
+      const uint64_t v = content_hash(p + off, n - off < HASH_CHUNK ? n - off : HASH_CHUNK);
+      h = rotl64(h ^ (v + (uint64_t)c * k1), 27) * k1;
+    }
+    return h ^ (h >> 32);
+  }
+  long cpus = sysconf(_SC_NPROCESSORS_ONLN);
+  size_t threads = cpus > 0 ? (size_t)cpus : 1;
+  if (threads > HASH_MAX_THREADS) threads = HASH_MAX_THREADS;
+  if (threads > chunks / 2) threads = chunks / 2;
+  hash_share share[HASH_MAX_THREADS];
+  pthread_t tid[HASH_MAX_THREADS];
+  int started[HASH_MAX_THREADS] = {0};
+  for (size_t t = 0; t < threads; ++t) {
+    share[t] = (hash_share){p, n, chunks * t / threads, chunks * (t + 1) / threads, hc};
+    if (t > 0) started[t] = pthread_create(&tid[t], NULL, hash_worker, &share[t]) == 0;
+  }
+  hash_chunks(&share[0]);
+  for (size_t t = 1; t < threads; ++t) {
+    if (started[t]) pthread_join(tid[t], NULL);
+    else hash_chunks(&share[t]);
+  }
+  for (size_t c = 0; c < chunks; ++c) h = rotl64(h ^ (hc[c] + (uint64_t)c * k1), 27) * k1;
+  free(hc);
   return h ^ (h >> 32);
 }
 
@@ -116,7 +178,7 @@ static uint64_t weight_signature(const htp_view *v, size_t tail) {
     const char *e = getenv("HTP_OPS_AMD_WEIGHT_CACHE");
     sampled = e && strcmp(e, "sampled") == 0;
   }
-  if (!sampled || v->bytes <= 128 + tail + 64 * 64) return content_hash(v->host, v->bytes);
+  if (!sampled || v->bytes <= 128 + tail + 64 * 64) return content_signature(v->host, v->bytes);
   uint64_t h = content_hash(v->host, 128) ^ rotl64(content_hash(v->host + v->bytes - tail, tail), 17);
   const size_t span = v->bytes - 128 - tail;
   for (int i = 0; i < 64; ++i) {

@@ -215,6 +215,27 @@ def test_opcode15_host_blob_rewritten_in_place(hip, orc, section):
     assert np.array_equal(out.read(np.float32, m * n).reshape(m, n).view(np.uint32), ref.view(np.uint32))
 
 
+def test_opcode15_large_host_blob_rewrites_in_every_share(hip, orc):
+    """Blobs of 4 MiB and more are hashed in 1 MiB chunks spread over
+    threads: one byte rewritten in place in the first, a middle and the last
+    chunk is seen by the next call each time."""
+    m, k, n = 8, 4096, 2048
+    x, blob = w8a8_inputs(orc, m, k, n, seed=61)
+    assert blob.nbytes >= 8 << 20
+    out, act, cst = rpc(m * n * 4, False), rpc(m * k * 4, False), rpc(blob.nbytes, False)
+    act.write(x)
+    cst.write(blob)
+    params = h.w8a8_params((out.fd, 0), (act.fd, 0), (cst.fd, 0), m, k, n)
+    assert h.execute(15, params)[0] == 0
+    cur = blob.copy()
+    for off in (128 + 999, (5 << 20) + 12345, 128 + k * n - 7):
+        cur[off] = np.uint8((int(cur[off]) + 101) & 0xff)
+        cst.host_view()[off:off + 1] = cur[off:off + 1]
+        assert h.execute(15, params)[0] == 0
+        ref = orc.linear(x, cur, k, n)
+        assert np.array_equal(out.read(np.float32, m * n).reshape(m, n).view(np.uint32), ref.view(np.uint32))
+
+
 def test_opcode15_device_blob_header_after_cache_hit(hip, orc):
     """A cached device blob skips the header read-back; a rewrite with a bad
     header is still rejected (-3), and a good rewrite runs again."""
