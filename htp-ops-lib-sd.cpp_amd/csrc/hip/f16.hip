@@ -1480,11 +1480,12 @@ int pick_ring_shape(int m, int n, long long *cost_out = nullptr) {
 // The streaming kernel (f16_gemm_stream, one persistent workgroup per CU,
 // 256 x 128 tiles, 6 stages of 24 KB) where its tiles occupy at least half of
 // the CUs and its cost in the ring shapes' model (rounds of tiles x work per
-// tile per CU) is strictly lower than the best ring shape's.  Measured, us,
-// streaming / ring kernel (one box): chosen at 2048x4096x14336 253 / 264,
-// 4096x6144x1536 99.6 / 114, 1024x4096x4096 51.4 / 59.6; not chosen at
-// 4096x1536x6144 88.0 / 90.3 (equal cost), 4096x1536x4608 80.9 / 75.6 (equal
-// cost), 2048x4096x6144 111 / 106, 2048x1536x6144 50.9 / 49.0 (one whole
+// tile per CU) is lower than the best ring shape's, or equal with whole
+// rounds of tiles.  Measured, us, streaming / ring kernel (one box): chosen at
+// 2048x4096x14336 253 / 264, 4096x6144x1536 99.6 / 114, 4096x1536x6144
+// 88.0 / 90.3 (equal cost, 3 whole rounds); not chosen at 1024x4096x4096
+// 51.4 / 59.6 (the model rates the 64x64 ring tiles cheaper), 4096x1536x4608
+// 80.9 / 75.6 (equal cost, 2.25 rounds), 2048x4096x6144 111 / 106, 2048x1536x6144 50.9 / 49.0 (one whole
 // round of 128 x 192 ring tiles against one and a half of streaming tiles),
 // 512x14336x4096 222 / 125 (64 tiles).  One barrier per two k-steps instead
 // of one per k-step measured within 3 %; the 256 x 192 form needs more
@@ -1529,7 +1530,8 @@ bool f16_stream_applies(int m, int k, int n) {
       (long long)((m + kF16StreamBM - 1) / kF16StreamBM) * ((n + kF16StreamBN - 1) / kF16StreamBN);
   long long ring_cost = 0;
   pick_ring_shape(m, n, &ring_cost);
-  return 2 * tiles >= cus && (tiles + cus - 1) / cus * kF16StreamBM * kF16StreamBN < ring_cost;
+  const long long cost = (tiles + cus - 1) / cus * kF16StreamBM * kF16StreamBN;
+  return 2 * tiles >= cus && (cost < ring_cost || (cost == ring_cost && tiles % cus == 0));
 }
 
 int launch_f16_stream(float *y, const int8_t *a, const int8_t *w, const float *bias, int m, int k, int n, int mode,

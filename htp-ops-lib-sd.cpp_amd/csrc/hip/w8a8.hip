@@ -59,29 +59,48 @@ __global__ __launch_bounds__(256) void w8a8_prepack_weights(uint4 *__restrict__ 
   }
 }
 
-__global__ __launch_bounds__(256) void w8a8_prepack_columns(float *__restrict__ sw_out, int32_t *__restrict__ delta,
-                                                           int32_t *__restrict__ wsum128,
-                                                           float *__restrict__ inv_out,
-                                                           const uint8_t *__restrict__ blob, int k, int n,
-                                                           int kp) {
-  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+// Column parameters: a workgroup per 64-column group, whose weights are one
+// contiguous run of 64*k blob bytes (per 32 k, 2 KB: the two 32-column halves,
+// each 8 rows of 4 k x 32 columns); its 16 waves take the 32-k blocks in turn
+// and lane l sums column l of the group; the waves' sums are added in LDS
+// (exact integer sums, so the split does not change them).  The grid's
+// threads also copy the smoothing vector, zero-padded to kp.
+__global__ __launch_bounds__(1024) void w8a8_prepack_columns(float *__restrict__ sw_out, int32_t *__restrict__ delta,
+                                                            int32_t *__restrict__ wsum128,
+                                                            float *__restrict__ inv_out,
+                                                            const uint8_t *__restrict__ blob, int k, int n,
+                                                            int kp) {
+  __shared__ int32_t part[16][64];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const size_t kn = (size_t)k * (size_t)n;
-  if (t < n) {
-    int32_t sum = 0;
-    for (int kk = 0; kk < k; kk += 4) {
-      const uint32_t w = *(const uint32_t *)(blob + blob_weight_offset(k, t, kk));
-      sum += (int32_t)(int8_t)(w & 0xffu) + (int32_t)(int8_t)((w >> 8) & 0xffu) +
-             (int32_t)(int8_t)((w >> 16) & 0xffu) + (int32_t)(int8_t)(w >> 24);
-    }
+  const uint8_t *grp =
+      blob + 128u + (size_t)blockIdx.x * 64u * (size_t)k + (size_t)(lane / 32) * 1024u + (size_t)(lane % 32) * 4u;
+  int32_t sum = 0;
+  for (int kb = wave; kb < k / 32; kb += 16) {
+    const uint8_t *p = grp + (size_t)kb * 2048u;
+    uint32_t w[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) w[r] = *(const uint32_t *)(p + r * 128);
+#pragma unroll
+    for (int r = 0; r < 8; ++r)
+      sum += (int32_t)(int8_t)(w[r] & 0xffu) + (int32_t)(int8_t)((w[r] >> 8) & 0xffu) +
+             (int32_t)(int8_t)((w[r] >> 16) & 0xffu) + (int32_t)(int8_t)(w[r] >> 24);
+  }
+  part[wave][lane] = sum;
+  __syncthreads();
+  if (wave == 0) {
+    const int t = blockIdx.x * 64 + lane;
+    uint32_t tot = 0;
+#pragma unroll
+    for (int w = 0; w < 16; ++w) tot += (uint32_t)part[w][lane];
     const float sw = *(const float *)(blob + 128u + kn + 4u * (size_t)t);
     const int32_t sums = *(const int32_t *)(blob + 128u + kn + 4u * (size_t)n + 4u * (size_t)t);
     sw_out[t] = sw;
-    wsum128[t] = (int32_t)((uint32_t)sum << 7);
-    delta[t] = (int32_t)(((uint32_t)sum - (uint32_t)sums) << 7);
+    wsum128[t] = (int32_t)(tot << 7);
+    delta[t] = (int32_t)((tot - (uint32_t)sums) << 7);
   }
-  if (t < kp) {
+  for (int t = blockIdx.x * 1024 + threadIdx.x; t < kp; t += gridDim.x * 1024)
     inv_out[t] = t < k ? *(const float *)(blob + 128u + kn + 8u * (size_t)n + 4u * (size_t)t) : 0.0f;
-  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1778,8 +1797,7 @@ int hb_w8a8_prepack(void *d_packed, const uint8_t *d_blob, int k, int n, hb_stre
                      (uint4 *)(base + hb_w8a8_packed_offset(k, n, HB_W8A8_WEIGHTS)), d_blob, k, n, kp);
   int rc = hb_check_launch("w8a8_prepack_weights");
   if (rc) return rc;
-  const int cols = n > kp ? n : kp;
-  hipLaunchKernelGGL(w8a8_prepack_columns, dim3((cols + 255) / 256), dim3(256), 0, st,
+  hipLaunchKernelGGL(w8a8_prepack_columns, dim3(n / 64), dim3(1024), 0, st,
                      (float *)(base + hb_w8a8_packed_offset(k, n, HB_W8A8_SW)),
                      (int32_t *)(base + hb_w8a8_packed_offset(k, n, HB_W8A8_DELTA)),
                      (int32_t *)(base + hb_w8a8_packed_offset(k, n, HB_W8A8_WSUM128)),

@@ -71,9 +71,13 @@ def test_quantize_bit_exact(hip, orc, m, k, inv_kind):
     assert sh[0] == np.float32(1e-12) and (u_ref[0] == 128).all()
 
 
-def test_prepack_layout(hip, orc):
-    k, n = 96, 64  # k % 64 == 32 exercises the zero padding
-    _, w, blob = make_w8a8(orc, 2, k, n, seed=3, sums_kind="random")
+@pytest.mark.parametrize("k,n", [
+    (96, 64),       # k % 64 == 32 exercises the zero padding; fewer 32-k blocks than waves
+    (14336, 128),   # long k: every wave of a column group sums many blocks
+    (4096, 1024),   # many column groups
+])
+def test_prepack_layout(hip, orc, k, n):
+    _, w, blob = make_w8a8(orc, 2, k, n, seed=3, inv_kind="uniform", sums_kind="random")
     packed = hip.w8a8_prepack(upload_blob(hip, blob), k, n)
     kp = hip.kp_of(k)
     img = packed.read(np.int8, n * kp)
@@ -88,6 +92,11 @@ def test_prepack_layout(hip, orc):
     wsum128 = packed.read(np.int32, n, hip.w8a8_packed_offset(k, n, hip.SECTION_WSUM128))
     np.testing.assert_array_equal(delta, ((wsum - sums) * 128).astype(np.int64).astype(np.uint32).view(np.int32))
     np.testing.assert_array_equal(wsum128, (wsum * 128).astype(np.int32))
+    sw = np.frombuffer(blob[128 + k * n:128 + k * n + 4 * n].tobytes(), np.float32)
+    np.testing.assert_array_equal(packed.read(np.float32, n, hip.w8a8_packed_offset(k, n, hip.SECTION_SW)), sw)
+    inv = np.zeros(kp, np.float32)
+    inv[:k] = np.frombuffer(blob[128 + k * n + 8 * n:128 + k * n + 8 * n + 4 * k].tobytes(), np.float32)
+    np.testing.assert_array_equal(packed.read(np.float32, kp, hip.w8a8_packed_offset(k, n, hip.SECTION_INV)), inv)
 
 
 GEMM_SHAPES = [
