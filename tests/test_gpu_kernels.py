@@ -529,6 +529,7 @@ def test_f16_ring_matches_tiles(hip, orc, m, k, n, mode, bias, check_oracle):
     (4096, 320, 4096, 2, True, False),    # two whole rounds: the odd slots start late
     (4096, 256, 6144, 1, True, False),    # three rounds, GELU
     (2048, 1536, 1152, 0, True, False),   # long k, few tiles
+    (333, 224, 2080, 2, True, True),      # n % 128 == 32: a last tile of one column pair, its bias clamped
 ])
 def test_f16_stream_matches_ring(hip, orc, m, k, n, mode, bias, check_oracle):
     """The persistent streaming F16 kernel gives the same bits as the ring
