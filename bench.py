@@ -538,7 +538,7 @@ def qk0_cases(steps, warmup, rotate=4):
             image_sets.append(packed)
         else:
             packed.free()
-        for m in (1, 16):
+        for m in (1, 4, 16):
             x = hip.DeviceBuffer.from_array(rng.standard_normal((m, k), dtype=np.float32))
             y = hip.DeviceBuffer(m * n * 4)
             ws = hip.DeviceBuffer(hip.f16_workspace_bytes(m, k, n))

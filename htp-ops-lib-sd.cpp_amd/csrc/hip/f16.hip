@@ -1161,6 +1161,152 @@ __global__ __launch_bounds__(64 * WAVES) void qk0_decode_ring(float *__restrict_
   y[tile * 32 + threadIdx.x] = (float)(_Float16)sum;
 }
 
+// 2 to 16 rows on the one-row kernel's plan, 64 columns per workgroup: wave
+// w streams the runs of k-blocks [KB*w, KB*w + KB) of both 32-column tiles
+// of its workgroup through two LDS rings (piece c of both runs requested
+// together), so a workgroup reads each activation value once for 64 columns
+// and the 224 workgroups of N = 14336 take one round of the CUs.  Each wave
+// owns a k-range and loads only that range of the rows: lane l's share of
+// activation row l % 16 (eight values per k-block; rows past m repeat row
+// m - 1 and are never stored), requested before any weight piece so that
+// every piece wait also covers them.  The waves' 16 x 64 partial products
+// are added in wave order in LDS (the rings, free by then), then read out to
+// fp16.  n % 64 == 0.
+template <int TYPE, int WAVES, int KB>
+__global__ __launch_bounds__(64 * WAVES) void qk0_rows_ring(float *__restrict__ y, const float *__restrict__ x,
+                                                           const uint8_t *__restrict__ blocks, int m, int k, int n) {
+  constexpr int BB = qk0_block_bytes<TYPE>(), BLK = 4 * BB;  // bytes of one 32-k block of a 32-column tile
+  constexpr int RUN = KB * BLK, NCH = (RUN + 1023) / 1024, RS = 4;
+  constexpr int NQ = TYPE == HB_GGML_Q8_0 ? 4 : 1;  // code words per fragment
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[WAVES][2][RS * 1024];
+  static_assert(WAVES == 16, "one output value per thread: 16 rows x 64 columns");
+  static_assert(sizeof(ring) >= WAVES * 1024 * sizeof(float), "the partial products fit in the rings");
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int kblocks = k / 32;
+  const int kb0 = wave * KB;
+  // this wave's k-range of the rows (blocks past k repeat the last one and are not multiplied)
+  const float *xr = x + (size_t)min(lane & 15, m - 1) * (size_t)k + 8 * (lane >> 4);
+  float4 alo[KB], ahi[KB];
+#pragma unroll
+  for (int t = 0; t < KB; ++t) {
+    const int kb = min(kb0 + t, kblocks - 1);
+    alo[t] = *(const float4 *)(xr + kb * 32);
+    ahi[t] = *(const float4 *)(xr + kb * 32 + 4);
+  }
+  const size_t total = (size_t)(n / 32) * (size_t)kblocks * (size_t)BLK;
+  size_t run0[2];
+  uint32_t ring_lds[2];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    run0[r] = ((size_t)(2 * blockIdx.x + r) * (size_t)kblocks + (size_t)kb0) * (size_t)BLK;
+    ring_lds[r] = (uint32_t)(uintptr_t)HB_LDS_PTR(ring[wave][r]);
+  }
+  auto pieces = [&](int c) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const size_t off = min(run0[r] + (size_t)c * 1024u + (size_t)lane * 16u, total - 16u);
+      __builtin_amdgcn_global_load_lds(blocks + off, HB_LDS_PTR(ring[wave][r] + (c % RS) * 1024), 16, 0, 0);
+    }
+  };
+#pragma unroll
+  for (int c = 0; c < RS && c < NCH; ++c) pieces(c);
+  const int q = lane >> 4, c16 = lane & 15;
+  hb_f32x4 acc[2][2];
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[r][j] = hb_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  int issued = RS < NCH ? RS : NCH;
+#pragma unroll
+  for (int t = 0; t < KB; ++t) {
+    // piece `last` of both runs has landed (and every row load, requested
+    // before the pieces): at most two younger pieces per later index
+    const int last = (t * BLK + BLK - 1) / 1024;
+    switch (issued - 1 - last) {
+      case 0: wait_vmcnt<0>(); break;
+      case 1: wait_vmcnt<2>(); break;
+      case 2: wait_vmcnt<4>(); break;
+      default: wait_vmcnt<6>(); break;
+    }
+    const bool live = kb0 + t < kblocks;
+    const hb_f16x8 a = live ? hb_f16x8{(_Float16)alo[t].x, (_Float16)alo[t].y, (_Float16)alo[t].z,
+                                       (_Float16)alo[t].w, (_Float16)ahi[t].x, (_Float16)ahi[t].y,
+                                       (_Float16)ahi[t].z, (_Float16)ahi[t].w}
+                            : hb_f16x8{};
+    // LDS reads the compiler does not track, as in the one-row kernel
+    const int sb = (t * BLK + q * BB) % (RS * 1024);
+    hb_u32x4 scales[2];
+    uint32_t codes[2][2][NQ];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      asm volatile("ds_read_b128 %0, %1" : "=v"(scales[r]) : "v"(ring_lds[r] + (uint32_t)sb));
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int c = j * 16 + c16;
+        if constexpr (TYPE == HB_GGML_Q8_0) {
+#pragma unroll
+          for (int p = 0; p < 4; ++p)
+            asm volatile("ds_read_u16 %0, %1"
+                         : "=v"(codes[r][j][p])
+                         : "v"(ring_lds[r] + (uint32_t)((sb + 16 + 64 * p + 2 * c) % (RS * 1024))));
+        } else {
+          asm volatile("ds_read_b32 %0, %1"
+                       : "=v"(codes[r][j][0])
+                       : "v"(ring_lds[r] + (uint32_t)((sb + 16 + 4 * c) % (RS * 1024))));
+        }
+      }
+    }
+    if constexpr (TYPE == HB_GGML_Q8_0)
+      asm volatile("s_waitcnt lgkmcnt(0)"
+                   : "+v"(scales[0]), "+v"(scales[1]), "+v"(codes[0][0][0]), "+v"(codes[0][0][1]),
+                     "+v"(codes[0][0][2]), "+v"(codes[0][0][3]), "+v"(codes[0][1][0]), "+v"(codes[0][1][1]),
+                     "+v"(codes[0][1][2]), "+v"(codes[0][1][3]), "+v"(codes[1][0][0]), "+v"(codes[1][0][1]),
+                     "+v"(codes[1][0][2]), "+v"(codes[1][0][3]), "+v"(codes[1][1][0]), "+v"(codes[1][1][1]),
+                     "+v"(codes[1][1][2]), "+v"(codes[1][1][3]));
+    else
+      asm volatile("s_waitcnt lgkmcnt(0)"
+                   : "+v"(scales[0]), "+v"(scales[1]), "+v"(codes[0][0][0]), "+v"(codes[0][1][0]),
+                     "+v"(codes[1][0][0]), "+v"(codes[1][1][0]));
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        Qk0Raw<TYPE> raw;
+        raw.s = scales[r];
+#pragma unroll
+        for (int p = 0; p < NQ; ++p) raw.q[p] = codes[r][j][p];
+        const hb_f16x8 w = live ? qk0_fragment<TYPE>(raw, j) : hb_f16x8{};
+        acc[r][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, a, acc[r][j], 0, 0, 0);
+      }
+    const int next_first = t + 1 < KB ? ((t + 1) * BLK) / 1024 : NCH;
+    if (issued < NCH && issued < next_first + RS) {
+      __builtin_amdgcn_sched_barrier(0);
+      while (issued < NCH && issued < next_first + RS) pieces(issued++);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  // every piece has been waited for and every ring read is done once all
+  // waves pass the barrier: the rings hold the partial products, [wave][1024]
+  __syncthreads();
+  float *red = (float *)&ring[0][0][0];
+  // lane l holds row l % 16, columns 32*r + 16*j + 4*(l/16) + e
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) red[wave * 1024 + (r * 2 + j) * 256 + e * 64 + lane] = acc[r][j][e];
+  __syncthreads();
+  const int i = threadIdx.x, l = i & 63;  // one output value per thread
+  const int row = l & 15;
+  if (row >= m) return;
+  float sum = red[i];
+#pragma unroll
+  for (int w = 1; w < WAVES; ++w) sum += red[w * 1024 + i];
+  const int col = blockIdx.x * 64 + 16 * (i >> 8) + 4 * (l >> 4) + ((i >> 6) & 3);
+  y[(size_t)row * n + col] = (float)(_Float16)sum;
+}
+
 template <int RF, int CF, int KPW, int TYPE>
 __global__ __launch_bounds__(64 * kSkinnyWaves) void qk0_skinny_partial(float *__restrict__ ws,
                                                                         const float *__restrict__ x,
@@ -1683,10 +1829,23 @@ int hb_qk0_gemm_ws(float *d_y, const float *d_x, const uint8_t *d_blocks, int m,
   // One row: the whole-K kernel (measured at k=4096, n=14336, m=1: Q4_0 11.0
   // against 14.1 us split-K; Q8_0 25.3 either way, 16 waves keep its
   // registers at one round).
-  // One row through the LDS ring (k <= 4096).  HTP_OPS_AMD_QK0_RING=0 keeps
-  // the register-load kernel below (comparisons only).
-  static const int ring_on = getenv("HTP_OPS_AMD_QK0_RING") ? atoi(getenv("HTP_OPS_AMD_QK0_RING")) : 1;
-  if (ring_on && m == 1 && k <= 16 * 8 * 32) {
+  // One row through the LDS ring (k <= 4096); 2-16 rows on the same plan.
+  // HTP_OPS_AMD_QK0_RING (comparisons only): bit 0 off keeps the one-row
+  // register-load kernel below, bit 1 off the split-K path for 2-16 rows.
+  static const int ring_on = getenv("HTP_OPS_AMD_QK0_RING") ? atoi(getenv("HTP_OPS_AMD_QK0_RING")) : 3;
+  if ((ring_on & 2) && m >= 2 && k <= 16 * 8 * 32 && n % 64 == 0) {
+    if (type == HB_GGML_Q4_0)
+      hipLaunchKernelGGL((qk0_rows_ring<HB_GGML_Q4_0, 16, 8>), dim3(n / 64), dim3(1024), 0, st, d_y, d_x, d_blocks,
+                         m, k, n);
+    else if (type == HB_GGML_IQ4_NL)
+      hipLaunchKernelGGL((qk0_rows_ring<HB_GGML_IQ4_NL, 16, 8>), dim3(n / 64), dim3(1024), 0, st, d_y, d_x,
+                         d_blocks, m, k, n);
+    else
+      hipLaunchKernelGGL((qk0_rows_ring<HB_GGML_Q8_0, 16, 8>), dim3(n / 64), dim3(1024), 0, st, d_y, d_x, d_blocks,
+                         m, k, n);
+    return hb_check_launch("qk0_rows_ring");
+  }
+  if ((ring_on & 1) && m == 1 && k <= 16 * 8 * 32) {
     if (type == HB_GGML_Q4_0)
       hipLaunchKernelGGL((qk0_decode_ring<HB_GGML_Q4_0, 16, 8>), dim3(n / 32), dim3(1024), 0, st, d_y, d_x, d_blocks,
                          k, n);

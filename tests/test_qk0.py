@@ -274,19 +274,24 @@ def test_qk0_prepack_bit_exact(hip, orc, wtype, kind, k, n):
 @pytest.mark.gpu
 @pytest.mark.parametrize("wtype,kind", TYPES)
 @pytest.mark.parametrize("m,k,n,scale_lo,scale_hi", [
-    (1, 4096, 1024, -12, -6),    # one row: the whole-K decode kernel
+    (1, 4096, 1024, -12, -6),    # one row: the whole-K ring kernel
     (1, 1536, 320, -12, -6),     # one row, K shorter than the waves cover
-    (1, 4128, 64, -12, -6),      # one row, K past the decode kernel: split-K
-    (5, 1536, 320, -12, -6),     # n % 64 != 0: 32-column workgroups
+    (1, 4128, 64, -12, -6),      # one row, K past the ring kernels: split-K
+    (2, 4096, 1024, -12, -6),    # two rows: the few-row ring kernel
+    (16, 4096, 512, -12, -6),    # sixteen rows
+    (5, 1536, 320, -12, -6),     # n % 64 != 0: the split-K path
+    (5, 1536, 384, -12, -6),     # 64-column workgroups, K shorter than the waves cover
     (16, 96, 64, -12, -6),       # full 16 rows, k-blocks fewer than the waves
+    (7, 32, 128, -12, -6),       # a single k-block
+    (3, 4160, 64, -12, -6),      # few rows, K past the ring kernels: split-K
     (3, 512, 128, -24, -20),     # scales near the fp16 subnormal range: subnormal weights
     (1, 512, 128, -24, -20),
 ])
 def test_qk0_direct_matches_prepacked(hip, orc, wtype, kind, m, k, n, scale_lo, scale_hi):
     """Few rows straight from the blocks: within the F16 bound of the oracle,
-    and, where both take the split-K path (m > 1 or k > 4096), equal to the
-    F16 path on the prepacked image bit for bit (same fp16 weights, same
-    summation order)."""
+    and, where both take the split-K path (k > 4096), equal to the F16 path
+    on the prepacked image bit for bit (same fp16 weights, same summation
+    order)."""
     rng = np.random.default_rng(m * 7 + k + n + wtype)
     blocks = random_blocks(rng, k, n, wtype, scale_lo, scale_hi)
     x = orc.normal(m * k, 0, 1, m + n).reshape(m, k)
@@ -297,7 +302,7 @@ def test_qk0_direct_matches_prepacked(hip, orc, wtype, kind, m, k, n, scale_lo, 
     packed = hip.qk0_prepack(bd, k, n, wtype)
     hip.f16_gemm(y2, xd, packed, None, m, k, n, n, 0, workspace=ws)
     hip.sync()
-    if m > 1 or k > 4096:
+    if k > 4096:
         np.testing.assert_array_equal(y1.read(np.uint32, m * n), y2.read(np.uint32, m * n))
     ref = orc.f16_gemm_epilogue(x, orc.qk0_dequant(blocks, k, n, wtype), None, m, k, n, n, 0)
     img = orc.qk0_dequant(blocks, k, n, wtype)
