@@ -1918,14 +1918,16 @@ int hb_f16_gemm_ws(float *d_y, const float *d_x, const uint16_t *d_packed, const
   // The split-K path holds m <= 128 rows (8 row fragments) of partial sums.
   const size_t need = split_k_bytes(m, k, n);
   // Tiled variant by output size; the split-K path takes over when that grid
-  // leaves CUs idle, and for m <= 16, where a tile's rows are mostly padding
-  // (measured at k=4096, n=14336: m=1 65 -> 28 us; 77x14336x4096: 264 -> 80 us).
+  // has no more workgroups than CUs, and for m <= 16, where a tile's rows are
+  // mostly padding (measured at k=4096, n=14336: m=1 65 -> 28 us;
+  // 77x14336x4096: 264 -> 80 us; 64x4096x4096, 256 tiles of 32x32: 40.6 ->
+  // 19.7 us).
   const long long big = ((m + 127) / 128) * (long long)((n + 127) / 128);
   const long long mid = ((m + 63) / 64) * (long long)((n + 63) / 64);
   const long long small = ((m + 31) / 32) * (long long)((n + 31) / 32);
   const long long tiled_wgs = big >= 256 ? big : mid >= 128 ? mid : small;
   if (m <= 128 && d_workspace && need && workspace_bytes >= need && aligned(d_workspace, 16) &&
-      (tiled_wgs < compute_units() || m <= 16)) {
+      (tiled_wgs <= compute_units() || m <= 16)) {
     int splits = 1, kpw = 1;
     skinny_plan(k, n, splits, kpw);
     const int cols = skinny_cols(n);

@@ -247,7 +247,7 @@ int hb_f16_force_stream(int setting);
 
 /* hb_f16_gemm with a workspace: for m <= 128, a workspace of at least
  * hb_f16_workspace_bytes, and either m <= 16 or a shape whose output tiles
- * (of the size hb_f16_gemm would use) number fewer than the device's CUs, K
+ * (of the size hb_f16_gemm would use) number no more than the device's CUs, K
  * is split across workgroups and the partial sums are added in a fixed order
  * before the fp16 readout rounding and the epilogue (two kernels).
  * Otherwise, for modes 0-2 with a workspace of at least

@@ -450,6 +450,7 @@ def f16_case(orc, m, k, n, seed, bias=True):
     (128, 3072, 768, 3, 704, True),   # eight row fragments, channel-major, split-K
     (17, 1024, 96, 1, 96, False),     # two row fragments, a single split
     (48, 4096, 2048, 2, 2048, True),  # three row fragments -> four-fragment variant
+    (64, 4096, 4096, 0, 4096, True),  # as many 32x32 tiles as CUs: split-K with a workspace
 ])
 @pytest.mark.parametrize("split_k", [False, True])
 def test_f16_gemm_epilogue(hip, orc, m, k, n, mode, channels, bias, split_k):
