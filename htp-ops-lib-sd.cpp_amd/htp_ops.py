@@ -367,7 +367,8 @@ def w8a8_gemm_kernel(m, k, n):
         return "w8a8_gemm_stream<256,128>"
     if choice == W8A8_STREAM_WIDE_TILE:
         return "w8a8_gemm_stream<256,192>"
-    check(choice, "hb_w8a8_gemm_choice")
+    if choice < 0:
+        check(choice, "hb_w8a8_gemm_choice")
     bm, bn = W8A8_TILE_SHAPES[choice]
     return f"w8a8_gemm_tiles<{bm},{bn}>"
 
