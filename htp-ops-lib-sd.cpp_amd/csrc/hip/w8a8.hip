@@ -1449,7 +1449,9 @@ __global__ __launch_bounds__(256) void w8a8_planes(uint8_t *__restrict__ out, co
 // is why 128x192 leads (measured at 4096x1536x6144: 128x192 57 us,
 // 128x128 62 us, 256x192 64 us, 256x256 73 us).
 // eff = measured MAC throughput of a full round of that shape relative to
-// 128x192 (LDS traffic per MAC grows as tiles shrink; 64x64 is an estimate).
+// 128x192 (LDS traffic per MAC grows as tiles shrink; 64x64 is an estimate);
+// it carries the effect of occupancy, which the cost model (tiles on the
+// busiest CU x tile work / eff) does not count separately.
 struct TileShape {
   int bm, bn, occ, eff;
 };
@@ -1494,8 +1496,20 @@ int compute_units() {
   return v;
 }
 
-// Picks the shape minimising (rounds of resident workgroups) x (work per
-// round per CU) / eff; ties go to the earlier entry of kTileShapes.
+// Picks the kernel for m > 16.  The streaming kernel keeps one workgroup per
+// CU for the whole launch, so it runs outright where its tiles spread evenly
+// over the CUs: the 256x192 form where its tiles fill whole rounds, the
+// 256x128 form where they fill whole rounds or one round of at least half of
+// the CUs (fewer tiles leave most CUs idle).  Otherwise every candidate is
+// costed as (tiles on the busiest CU) x (work per tile) / (relative
+// efficiency), the streaming forms with efficiency 110 where their tiles
+// occupy at least half of the CUs; ties go to the earlier tiled entry.
+// Measured (GEMM alone, us, automatic / best forced, one box) on the shapes
+// this rule changed: 256x1536x4608 13.65 -> 7.40 (64x64 tiles instead of 36
+// streaming tiles), 512x4096x4096 24.4 -> 16.2, 1024x6144x1536 33.1 -> 19.9,
+// 256x4096x14336 25.5 -> 23.0, 512x1536x6144 14.3 -> 11.5, 1024x4096x14336
+// 69.2 -> 59.6 (streaming instead of 256x256 tiles, 1.75 rounds),
+// 2048x4096x14336 136 -> 119, 2048x1536x4608 21.3 -> 19.8.
 // The streaming kernel needs kp / 64 >= kStreamStages - 1 (its parameter
 // double buffer).
 bool stream_applies(int kp) { return kp / kKStep >= kStreamStages - 1; }
@@ -1510,32 +1524,30 @@ int pick_tile_shape(int m, int n, int kp) {
   if (forced == kStreamWideShape && stream_wide_applies(n, kp)) return kStreamWideShape;
   if (forced == kStreamShape && stream_applies(kp)) return kStreamShape;
   if (forced >= 0 && forced < kNumShapes && (kTileShapes[forced].bn != 192 || n % 192 == 0)) return forced;
-  const int cus = compute_units();
+  const long long cus = compute_units();
   const long long stream_tiles = (long long)((m + kStreamBM - 1) / kStreamBM) * ((n + kStreamBN - 1) / kStreamBN);
-  // The streaming kernel when its tiles spread evenly over the CUs (it keeps
-  // one workgroup per CU for the whole launch, so a partial last round costs a
-  // whole tile): measured against the automatic tiled choice, in us,
-  // 4096x6144x1536 41.9 vs 46.9, 2048x4096x4096 36.9 vs 40.1, 1024x4096x4096
-  // 30.2 vs 31.7, 4096x1536x6144 50.0 vs 50.4; with uneven rounds it loses
-  // (4096x1536x4608, 2.25 tiles per CU: 46.4 vs 40.5; 2048x4096x6144, 1.5:
-  // 60.8 vs 54.0).  HTP_OPS_AMD_W8A8_STREAM=1 / 0 forces it on / off.
-  const bool stream_even = stream_tiles <= cus || stream_tiles % cus == 0;
-  // The 192-column form when its tiles fill whole rounds (fewer tiles than CUs
-  // leave CUs idle): 4096x1536x6144 42.4 vs 43.1 us; at 4096x6144x1536
-  // (128 tiles) it would take 44.1 vs 35.2.
   const long long wide_tiles =
       (long long)((m + kStreamBM - 1) / kStreamBM) * ((n + kStreamWideBN - 1) / kStreamWideBN);
-  if (stream_mode() != 0 && stream_wide_applies(n, kp) && wide_tiles >= cus && wide_tiles % cus == 0)
-    return kStreamWideShape;
-  if (stream_mode() != 0 && stream_applies(kp) && (stream_mode() == 1 || stream_even)) return kStreamShape;
+  const bool stream_ok = stream_mode() != 0 && stream_applies(kp) && (stream_mode() == 1 || 2 * stream_tiles >= cus);
+  const bool wide_ok = stream_mode() != 0 && stream_wide_applies(n, kp) && 2 * wide_tiles >= cus;
+  if (wide_ok && wide_tiles >= cus && wide_tiles % cus == 0) return kStreamWideShape;
+  if (stream_ok && (stream_mode() == 1 || stream_tiles <= cus || stream_tiles % cus == 0)) return kStreamShape;
   int best = 0;
   long long best_cost = -1;
-  for (int i = 0; i < kNumShapes; ++i) {
-    const TileShape t = kTileShapes[i];
-    if (t.bn == 192 && n % 192 != 0) continue;
-    const long long tiles = (long long)((m + t.bm - 1) / t.bm) * ((n + t.bn - 1) / t.bn);
-    const long long slots = (long long)cus * t.occ;
-    const long long cost = (tiles + slots - 1) / slots * t.bm * t.bn * t.occ * 100 / t.eff;
+  for (int i = 0; i < kNumShapes + 2; ++i) {
+    int bm, bn, eff;
+    if (i < kNumShapes) {
+      bm = kTileShapes[i].bm, bn = kTileShapes[i].bn, eff = kTileShapes[i].eff;
+      if (bn == 192 && n % 192 != 0) continue;
+    } else if (i == kStreamShape) {
+      if (!stream_ok) continue;
+      bm = kStreamBM, bn = kStreamBN, eff = 110;
+    } else {
+      if (!wide_ok) continue;
+      bm = kStreamBM, bn = kStreamWideBN, eff = 110;
+    }
+    const long long tiles = (long long)((m + bm - 1) / bm) * ((n + bn - 1) / bn);
+    const long long cost = (tiles + cus - 1) / cus * bm * bn * 100 / eff;
     if (best_cost < 0 || cost < best_cost) {
       best_cost = cost;
       best = i;
