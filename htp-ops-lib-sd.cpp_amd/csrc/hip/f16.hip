@@ -311,7 +311,7 @@ __global__ __launch_bounds__(256) void f16_pack_a(uint4 *__restrict__ img, const
 template <int BM, int BN, int WM, int WN, int S>
 __device__ inline void ring_mainloop(hb_f32x4 (&acc)[BM / WM / 16][BN / WN / 16], int8_t *lds,
                                      const int8_t *__restrict__ aimg, const int8_t *__restrict__ wpack, int m, int k,
-                                     int n, int m0, int n0, int wave, int lane) {
+                                     int n, int m0, int n0, int wave, int lane, int kt0 = 0, int kt_n = -1) {
   constexpr int NW = WM * WN;
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int FM = WTM / 16, FN = WTN / 16;
@@ -321,8 +321,10 @@ __device__ inline void ring_mainloop(hb_f32x4 (&acc)[BM / WM / 16][BN / WN / 16]
   constexpr int PW_LO = NB / NW;
   static_assert(PW_LO >= 1, "every wave takes part in the DMA");
   constexpr int STAGE = NB * kFragBytes;
-  const int kt_count = k / 32;
+  const int kt_count = k / 32;  // k-steps of a whole row (the operand block stride)
   const int wm = wave / WN, wn = wave % WN;
+  // k-steps [kt0, kt0 + steps) of the product (all of them by default)
+  const int steps = kt_n < 0 ? kt_count : kt_n;
 
   const int8_t *src[PW];
   int stride[PW];
@@ -347,15 +349,15 @@ __device__ inline void ring_mainloop(hb_f32x4 (&acc)[BM / WM / 16][BN / WN / 16]
 
 #pragma unroll
   for (int s = 0; s < S - 1; ++s)
-    if (s < kt_count) dma_stage<PW, NW, NB>(lds + (s % S) * STAGE, src, stride, s, wave, lane);
-  for (int kt = 0; kt < kt_count; ++kt) {
+    if (s < steps) dma_stage<PW, NW, NB>(lds + (s % S) * STAGE, src, stride, kt0 + s, wave, lane);
+  for (int kt = 0; kt < steps; ++kt) {
     if (PW == PW_LO || wave < NB % NW)
-      wait_stage<PW, S - 2>(kt_count - 1 - kt);
+      wait_stage<PW, S - 2>(steps - 1 - kt);
     else
-      wait_stage<PW_LO, S - 2>(kt_count - 1 - kt);
+      wait_stage<PW_LO, S - 2>(steps - 1 - kt);
     block_barrier();
-    if (kt + S - 1 < kt_count)
-      dma_stage<PW, NW, NB>(lds + ((kt + S - 1) % S) * STAGE, src, stride, kt + S - 1, wave, lane);
+    if (kt + S - 1 < steps)
+      dma_stage<PW, NW, NB>(lds + ((kt + S - 1) % S) * STAGE, src, stride, kt0 + kt + S - 1, wave, lane);
     const int8_t *base = lds + (kt % S) * STAGE;
     const int8_t *la = base + (wm * FM) * kFragBytes + lane * 16;
     const int8_t *lb = base + (ABLK + wn * FN) * kFragBytes + lane * 16;
@@ -423,6 +425,49 @@ __global__ __launch_bounds__(64 * WM *WN) void f16_gemm_ring(float *__restrict__
       }
     }
   }
+}
+
+// Split-K form of the ring kernel for up to 128 rows: grid (tiles, splits),
+// split s multiplies k-steps [s*kps, s*kps + kps) of its BM x BN tile (the
+// k loop of f16_gemm_ring on that range) and stores the raw fp32 sums to
+// slice s of the workspace ([mp][n] per slice, rows past m dropped by the
+// buffer bound); f16_skinny_epilogue then adds the slices in order, reads
+// out to fp16 and applies bias and activation.  A tile covers every row, so
+// the fp16 weights are read once, and the splits give the launch enough
+// workgroups.
+template <int BM, int BN, int WM, int WN, int S>
+__global__ __launch_bounds__(64 * WM *WN) void f16_ring_splitk(float *__restrict__ ws, const int8_t *__restrict__ aimg,
+                                                               const int8_t *__restrict__ wpack, int m, int k, int n,
+                                                               int kps) {
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int FM = WTM / 16, FN = WTN / 16;
+  constexpr int STAGE = (BM / 16 + BN / 16) * kFragBytes;
+  __shared__ __attribute__((aligned(1024))) int8_t lds[S * STAGE];
+  const int tiles_m = (m + BM - 1) / BM, tiles_n = (n + BN - 1) / BN;
+  int tm, tn;
+  tile_coords_2d<BM, BN>(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int wm = wave / WN, wn = wave % WN;
+  const int kt0 = blockIdx.y * kps, kt_n = min(kps, k / 32 - kt0);
+  hb_f32x4 acc[FM][FN];
+  ring_mainloop<BM, BN, WM, WN, S>(acc, lds, aimg, wpack, m, k, n, m0, n0, wave, lane, kt0, kt_n);
+  // lane l holds rows 4*(l/16)..+3 and column l%16 of each 16x16 block
+  const int mp = (m + 15) / 16 * 16;
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(ws + (size_t)blockIdx.y * mp * n, 0, (uint32_t)m * (uint32_t)n * 4u, 0x00020000);
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int col = n0 + wn * WTN + j * 16 + (lane & 15);
+      if (col >= n) continue;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = m0 + wm * WTM + i * 16 + 4 * (lane >> 4) + r;
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[i][j][r]), rs, (uint32_t)(row * n + col) * 4u, 0, 0);
+      }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1680,9 +1725,9 @@ bool f16_stream_applies(int m, int k, int n) {
   return 2 * tiles >= cus && (cost < ring_cost || (cost == ring_cost && tiles % cus == 0));
 }
 
-int launch_f16_stream(float *y, const int8_t *a, const int8_t *w, const float *bias, int m, int k, int n, int mode,
-                      hipStream_t st) {
-  constexpr int BM = kF16StreamBM, BN = kF16StreamBN, S = kF16StreamStages;
+template <int BM, int BN, int S>
+int launch_f16_stream_t(float *y, const int8_t *a, const int8_t *w, const float *bias, int m, int k, int n, int mode,
+                        hipStream_t st) {
   const int tiles_m = (m + BM - 1) / BM, tiles_n = (n + BN - 1) / BN;
   const int tiles = tiles_m * tiles_n;
   const int grid = std::min(compute_units(), (tiles + 7) / 8 * 8) / 8 * 8;
@@ -1700,6 +1745,19 @@ int launch_f16_stream(float *y, const int8_t *a, const int8_t *w, const float *b
   return hb_check_launch("f16_gemm_stream");
 }
 
+// Narrow streaming tiles for few rows: 128 x 64 (12 stages of 12 KB) and
+// 256 x 64 (7 stages of 20 KB).  HTP_OPS_AMD_F16_STREAM_SHAPE=2 / 3 selects
+// them where they apply (measurement hook).
+int f16_stream_narrow() {
+  static const int v = getenv("HTP_OPS_AMD_F16_STREAM_SHAPE") ? atoi(getenv("HTP_OPS_AMD_F16_STREAM_SHAPE")) : 0;
+  return v;
+}
+
+int launch_f16_stream(float *y, const int8_t *a, const int8_t *w, const float *bias, int m, int k, int n, int mode,
+                      hipStream_t st) {
+  return launch_f16_stream_t<kF16StreamBM, kF16StreamBN, kF16StreamStages>(y, a, w, bias, m, k, n, mode, st);
+}
+
 int launch_ring(float *y, const float *x, const uint16_t *packed, const float *bias, int m, int k, int n, int mode,
                 void *ws, hipStream_t st) {
   const int mp = (m + 15) / 16 * 16;
@@ -1708,6 +1766,10 @@ int launch_ring(float *y, const float *x, const uint16_t *packed, const float *b
   hipLaunchKernelGGL(f16_pack_a, dim3(pg), dim3(256), 0, st, (uint4 *)ws, x, m, k, mp);
   int rc = hb_check_launch("f16_pack_a");
   if (rc) return rc;
+  if (f16_stream_mode() != 0 && f16_stream_narrow() == 2 && k / 32 >= 6)
+    return launch_f16_stream_t<256, 64, 7>(y, (const int8_t *)ws, (const int8_t *)packed, bias, m, k, n, mode, st);
+  if (f16_stream_mode() != 0 && f16_stream_narrow() == 3 && k / 32 >= 11)
+    return launch_f16_stream_t<128, 64, 12>(y, (const int8_t *)ws, (const int8_t *)packed, bias, m, k, n, mode, st);
   if (f16_stream_applies(m, k, n))
     return launch_f16_stream(y, (const int8_t *)ws, (const int8_t *)packed, bias, m, k, n, mode, st);
   const int shape = pick_ring_shape(m, n);
@@ -1729,6 +1791,63 @@ int launch_ring(float *y, const float *x, const uint16_t *packed, const float *b
       break;
   }
   return hb_check_launch("f16_gemm_ring");
+}
+
+// Split-K ring path for m <= 128: fp16 activation image, f16_ring_splitk on
+// 128 x 128 tiles with K split so that the launch has about two workgroups
+// per CU (at most kMaxRingSplits slices), then f16_skinny_epilogue.  It
+// replaces the few-rows split-K kernel from 33 rows on, whose every column
+// group re-reads the fp32 rows (measured, us, few-rows / this path:
+// 77x10240x4096 60.7 / 25.0, 128x10240x4096 120 / 31, 77x4096x4096 25.4 /
+// 16.6, 64x4096x4096 19.3 / 16.0, 48x2048x8192 20.4 / 17.0, 77x1280x5120
+// 17.1 / 14.3; at 32 rows and fewer the few-rows kernel stays ahead:
+// 32x4096x4096 13.3 / 14.4, 20x1536x6144 9.5 / 12.5, 1x4096x14336 25.6 /
+// 32.7).  Where the ring or the one-launch kernel applies they stay ahead
+// too (77x4096x14336 38.7 / 44.2, 77x768x3072 6.7 / 11.1).
+constexpr int kMaxRingSplits = 8;
+
+int ring_splits(int m, int k, int n) {
+  const long long tiles = (long long)((m + 127) / 128) * ((n + 127) / 128);
+  const long long want = (2LL * compute_units() + tiles - 1) / tiles;
+  const int kblocks = k / 32;
+  int splits = (int)std::min<long long>(std::min<long long>(want, kMaxRingSplits), kblocks);
+  return splits < 1 ? 1 : splits;
+}
+
+size_t ring_splitk_bytes(int m, int k, int n) {
+  if (m < 1 || m > 128 || k < 32 || n < 32) return 0;
+  return a_image_bytes(m, k) + (size_t)kMaxRingSplits * (size_t)((m + 15) / 16 * 16) * (size_t)n * 4u;
+}
+
+int launch_ring_splitk(float *y, const float *x, const uint16_t *packed, const float *bias, int m, int k, int n,
+                       int channels, int mode, void *ws, hipStream_t st) {
+  const int mp = (m + 15) / 16 * 16;
+  const size_t slots = (size_t)mp * k / 8u;
+  const int pg = (int)((slots + 255) / 256 < 65536 ? (slots + 255) / 256 : 65536);
+  hipLaunchKernelGGL(f16_pack_a, dim3(pg), dim3(256), 0, st, (uint4 *)ws, x, m, k, mp);
+  int rc = hb_check_launch("f16_pack_a");
+  if (rc) return rc;
+  const int splits = ring_splits(m, k, n);
+  const int kps = (k / 32 + splits - 1) / splits;
+  const int used = (k / 32 + kps - 1) / kps;  // slices that hold k-steps
+  float *part = (float *)((uint8_t *)ws + a_image_bytes(m, k));
+  const int tiles = ((m + 127) / 128) * ((n + 127) / 128);
+  hipLaunchKernelGGL((f16_ring_splitk<128, 128, 2, 2, 4>), dim3(tiles, used), dim3(256), 0, st, part,
+                     (const int8_t *)ws, (const int8_t *)packed, m, k, n, kps);
+  rc = hb_check_launch("f16_ring_splitk");
+  if (rc) return rc;
+  const size_t outs = (size_t)m * (size_t)(mode == 3 ? channels : n);
+  const int eg = (int)((outs + 255) / 256 < 4096 ? (outs + 255) / 256 : 4096);
+  hipLaunchKernelGGL(f16_skinny_epilogue, dim3(eg), dim3(256), 0, st, y, part, bias, m, n, channels, mode, used);
+  return hb_check_launch("f16_skinny_epilogue");
+}
+
+// -1 (default): the split-K ring path for 33 to 128 rows where the few-rows
+// split-K path would run; 0: never; 1: for every m <= 128 with a workspace
+// (HTP_OPS_AMD_F16_SPLITK, comparisons only).
+int ring_splitk_mode() {
+  static const int v = getenv("HTP_OPS_AMD_F16_SPLITK") ? atoi(getenv("HTP_OPS_AMD_F16_SPLITK")) : -1;
+  return v;
 }
 
 // Few rows in one launch (f16_small): m <= 128, k <= 3072, a weight image
@@ -1901,7 +2020,8 @@ size_t hb_f16_workspace_bytes(int m, int k, int n) {
   if (m < 1 || k < 32 || n < 32) return 0;
   const size_t ring = ring_worth_it(m, k, n) ? a_image_bytes(m, k) : 0;
   const size_t partials = split_k_bytes(m, k, n);
-  return ring > partials ? ring : partials;
+  const size_t ring_partials = ring_splitk_bytes(m, k, n);
+  return std::max(std::max(ring, partials), ring_partials);
 }
 
 int hb_f16_gemm_ws(float *d_y, const float *d_x, const uint16_t *d_packed, const float *d_bias, int m, int k, int n,
@@ -1913,11 +2033,11 @@ int hb_f16_gemm_ws(float *d_y, const float *d_x, const uint16_t *d_packed, const
   if (!aligned(d_x, 16) || !aligned(d_packed, 16) || !aligned(d_y, 4) || (d_bias && !aligned(d_bias, 4)))
     return hb_invalid("hb_f16_gemm alignment");
   hipStream_t st = hb_resolve_stream(s);
-  if (const int cf = aligned(d_y, 16) ? small_cf(m, k, n) : 0)
-    return launch_small<0>(cf, d_y, d_x, d_packed, d_bias, m, k, n, channels, mode, st);
-  // The split-K path holds m <= 128 rows (8 row fragments) of partial sums.
-  const size_t need = split_k_bytes(m, k, n);
-  // Tiled variant by output size; the split-K path takes over when that grid
+  const bool splitk_ok = ring_splitk_mode() != 0 && m <= 128 && d_workspace &&
+                         workspace_bytes >= ring_splitk_bytes(m, k, n) && aligned(d_workspace, 256);
+  if (splitk_ok && ring_splitk_mode() == 1)
+    return launch_ring_splitk(d_y, d_x, d_packed, d_bias, m, k, n, channels, mode, d_workspace, st);
+  // Tiled variant by output size; the split-K paths take over when that grid
   // has no more workgroups than CUs, and for m <= 16, where a tile's rows are
   // mostly padding (measured at k=4096, n=14336: m=1 65 -> 28 us;
   // 77x14336x4096: 264 -> 80 us; 64x4096x4096, 256 tiles of 32x32: 40.6 ->
@@ -1926,6 +2046,21 @@ int hb_f16_gemm_ws(float *d_y, const float *d_x, const uint16_t *d_packed, const
   const long long mid = ((m + 63) / 64) * (long long)((n + 63) / 64);
   const long long small = ((m + 31) / 32) * (long long)((n + 31) / 32);
   const long long tiled_wgs = big >= 256 ? big : mid >= 128 ? mid : small;
+  // From 33 rows the split-K ring path, except where the ring kernel has
+  // more tiles than CUs at 4 GFLOP or more (77x4096x14336: 38.4 against
+  // 44.2 us) and where the one-launch kernel applies to under 12 MB of
+  // weights (77x768x3072: 6.7 against 11.1 us, 64x2048x2048 10.4 against
+  // 11.3).  Measured, us, previous choice / split-K ring: 100x3072x3072 28.6
+  // / 14.4 and 128x3072x3072 28.8 / 15.1 (one launch), 48x2048x8192 20.4 /
+  // 17.0 and 77x1280x5120 17.1 / 14.3 (one launch, 13-34 MB of weights).
+  const bool ring_here = ring_worth_it(m, k, n) && tiled_wgs > compute_units();
+  const bool splitk_here = splitk_ok && m > 32 && !ring_here;
+  const int cf = aligned(d_y, 16) ? small_cf(m, k, n) : 0;
+  if (splitk_here && (!cf || (size_t)n * (size_t)k * 2u >= ((size_t)12 << 20)))
+    return launch_ring_splitk(d_y, d_x, d_packed, d_bias, m, k, n, channels, mode, d_workspace, st);
+  if (cf) return launch_small<0>(cf, d_y, d_x, d_packed, d_bias, m, k, n, channels, mode, st);
+  // The split-K path holds m <= 128 rows (8 row fragments) of partial sums.
+  const size_t need = split_k_bytes(m, k, n);
   if (m <= 128 && d_workspace && need && workspace_bytes >= need && aligned(d_workspace, 16) &&
       (tiled_wgs <= compute_units() || m <= 16)) {
     int splits = 1, kpw = 1;

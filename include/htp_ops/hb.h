@@ -229,10 +229,11 @@ int hb_qk0_gemm_ws(float *d_y, const float *d_x, const uint8_t *d_blocks, int m,
 int hb_f16_gemm(float *d_y, const float *d_x, const uint16_t *d_packed, const float *d_bias, int m, int k, int n,
                 int channels, int mode, hb_stream s);
 
-/* Workspace of hb_f16_gemm_ws: the larger of the few-rows (m <= 128) split-K
- * partial sums and, for 64 or more rows and at least 4 GFLOP, the fp16
- * activation image of the ring path (2 * ceil(m/16)*16 * k bytes); 0 when
- * neither applies (the tiled kernel needs none). */
+/* Workspace of hb_f16_gemm_ws: the largest of the few-rows (m <= 128) split-K
+ * partial sums, for 64 or more rows and at least 4 GFLOP the fp16 activation
+ * image of the ring path (2 * ceil(m/16)*16 * k bytes), and for m <= 128 that
+ * image plus eight fp32 partial-sum slices of ceil(m/16)*16 x n (the split-K
+ * ring path); 0 when none applies (the tiled kernel needs none). */
 size_t hb_f16_workspace_bytes(int m, int k, int n);
 
 /* Tuning and test hook of the F16 path for 64 rows or more with a workspace:
@@ -249,7 +250,9 @@ int hb_f16_force_stream(int setting);
  * hb_f16_workspace_bytes, and either m <= 16 or a shape whose output tiles
  * (of the size hb_f16_gemm would use) number no more than the device's CUs, K
  * is split across workgroups and the partial sums are added in a fixed order
- * before the fp16 readout rounding and the epilogue (two kernels).
+ * before the fp16 readout rounding and the epilogue (two kernels; from 33
+ * rows on, x is first converted to fp16 MFMA tiles and each split covers all
+ * rows of a 128 x 128 tile, so the weights are read once).
  * Otherwise, for modes 0-2 with a workspace of at least
  * hb_f16_workspace_bytes, a 16-byte aligned output and 64 or more rows (4
  * GFLOP or more), x is converted once into fp16 MFMA tiles in the workspace

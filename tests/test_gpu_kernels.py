@@ -451,6 +451,8 @@ def f16_case(orc, m, k, n, seed, bias=True):
     (17, 1024, 96, 1, 96, False),     # two row fragments, a single split
     (48, 4096, 2048, 2, 2048, True),  # three row fragments -> four-fragment variant
     (64, 4096, 4096, 0, 4096, True),  # as many 32x32 tiles as CUs: split-K with a workspace
+    (77, 1280, 5120, 1, 5120, True),  # 13 MB of weights: the split-K ring path rather than one launch
+    (100, 10240, 512, 3, 480, True),  # long K, channel-major, split-K ring path
 ])
 @pytest.mark.parametrize("split_k", [False, True])
 def test_f16_gemm_epilogue(hip, orc, m, k, n, mode, channels, bias, split_k):

@@ -593,15 +593,22 @@ def gpu_case(orc, op, bias_kind, device, shape=None):
                 n_heads=n_heads, hd=hd, k=k, tokens=tokens, tiles=tiles, qkv_bytes=qkv_bytes, rope=rope)
 
 
-def library_raw(c):
-    """The library's own F16 GEMM output for the case (mode 0, no bias)."""
+def library_raw(c, parts=None):
+    """The library's own F16 GEMM output for the case (mode 0, no bias), one
+    call per part of `parts` rows (the executor multiplies each part of a
+    dual request on its own, and the kernel a call takes depends on its row
+    count)."""
     m, k, n = c["tokens"], c["k"], 3 * c["n_heads"] * c["hd"]
     packed = h.f16_prepack(dev(c["permuted"]), k, n)
-    y = h.DeviceBuffer(m * n * 4)
-    ws = h.DeviceBuffer(max(h.f16_workspace_bytes(m, k, n), 1))
-    h.f16_gemm(y, dev(c["act"]), packed, None, m, k, n, n, 0, workspace=ws)
-    h.sync()
-    return y.read(np.float32, m * n).reshape(m, n)
+    out = []
+    for r0, r1 in (parts or [(0, m)]):
+        rows = r1 - r0
+        y = h.DeviceBuffer(rows * n * 4)
+        ws = h.DeviceBuffer(max(h.f16_workspace_bytes(rows, k, n), 1))
+        h.f16_gemm(y, dev(np.ascontiguousarray(c["act"][r0:r1])), packed, None, rows, k, n, n, 0, workspace=ws)
+        h.sync()
+        out.append(y.read(np.float32, rows * n).reshape(rows, n))
+    return np.concatenate(out)
 
 
 @pytest.mark.gpu
@@ -622,7 +629,7 @@ def test_qkv_opcodes_end_to_end(hip, orc, op, bias_kind, device, shape):
     assert elapsed >= 0
     got = [c["buf"].read(np.uint16, c["qkv_bytes"] // 2, c["offs"][n]) for n in ("q", "k", "v")]
     # bit-exact: the oracle's post-processing of the library's GEMM output
-    raw = library_raw(c)
+    raw = library_raw(c, [(0, 32), (32, c["tokens"])] if op in (10, 12) else None)
     bias = None if bias_kind == "none" else c["bias"]
     t, nh, hd, tiles = c["tokens"], c["n_heads"], c["hd"], c["tiles"]
     if op in (10, 12):
