@@ -1747,7 +1747,8 @@ int launch_f16_stream_t(float *y, const int8_t *a, const int8_t *w, const float 
 
 // Narrow streaming tiles for few rows: 128 x 64 (12 stages of 12 KB) and
 // 256 x 64 (7 stages of 20 KB).  HTP_OPS_AMD_F16_STREAM_SHAPE=2 / 3 selects
-// them where they apply (measurement hook).
+// them wherever the ring path runs (measurement hook); the 256 x 64 form
+// also runs by itself at one 256-row tile (below).
 int f16_stream_narrow() {
   static const int v = getenv("HTP_OPS_AMD_F16_STREAM_SHAPE") ? atoi(getenv("HTP_OPS_AMD_F16_STREAM_SHAPE")) : 0;
   return v;
@@ -1766,7 +1767,12 @@ int launch_ring(float *y, const float *x, const uint16_t *packed, const float *b
   hipLaunchKernelGGL(f16_pack_a, dim3(pg), dim3(256), 0, st, (uint4 *)ws, x, m, k, mp);
   int rc = hb_check_launch("f16_pack_a");
   if (rc) return rc;
-  if (f16_stream_mode() != 0 && f16_stream_narrow() == 2 && k / 32 >= 6)
+  // One 256-row tile (193-256 rows): 256 x 64 streaming tiles read the
+  // weights once where they cover half of the CUs (256x4096x14336 70.0 ->
+  // 56.4 us, 256x4096x10240 39.5 -> 37.6; at 192 rows the ring kernel stays
+  // ahead: 192x4096x10240 31.4 against 35.3).
+  const bool narrow_auto = f16_stream_narrow() == 0 && m > 192 && m <= 256 && 2 * ((n + 63) / 64) >= compute_units();
+  if (f16_stream_mode() != 0 && (f16_stream_narrow() == 2 || narrow_auto) && k / 32 >= 6)
     return launch_f16_stream_t<256, 64, 7>(y, (const int8_t *)ws, (const int8_t *)packed, bias, m, k, n, mode, st);
   if (f16_stream_mode() != 0 && f16_stream_narrow() == 3 && k / 32 >= 11)
     return launch_f16_stream_t<128, 64, 12>(y, (const int8_t *)ws, (const int8_t *)packed, bias, m, k, n, mode, st);
@@ -1793,7 +1799,7 @@ int launch_ring(float *y, const float *x, const uint16_t *packed, const float *b
   return hb_check_launch("f16_gemm_ring");
 }
 
-// Split-K ring path for m <= 128: fp16 activation image, f16_ring_splitk on
+// Split-K ring path for m <= 256: fp16 activation image, f16_ring_splitk on
 // 128 x 128 tiles with K split so that the launch has about two workgroups
 // per CU (at most kMaxRingSplits slices), then f16_skinny_epilogue.  It
 // replaces the few-rows split-K kernel from 33 rows on, whose every column
@@ -1803,7 +1809,10 @@ int launch_ring(float *y, const float *x, const uint16_t *packed, const float *b
 // 17.1 / 14.3; at 32 rows and fewer the few-rows kernel stays ahead:
 // 32x4096x4096 13.3 / 14.4, 20x1536x6144 9.5 / 12.5, 1x4096x14336 25.6 /
 // 32.7).  Where the ring or the one-launch kernel applies they stay ahead
-// too (77x4096x14336 38.7 / 44.2, 77x768x3072 6.7 / 11.1).
+// too (77x4096x14336 38.7 / 44.2, 77x768x3072 6.7 / 11.1).  Up to 256 rows
+// (two row tiles) it replaces the ring kernel where that has no more tiles
+// than CUs: 256x10240x4096 68.3 -> 50.8 us, 160x3072x3072 21.7 -> 18.1
+// (256x4096x4096 27.7 -> 28.4).
 constexpr int kMaxRingSplits = 8;
 
 int ring_splits(int m, int k, int n) {
@@ -1815,7 +1824,7 @@ int ring_splits(int m, int k, int n) {
 }
 
 size_t ring_splitk_bytes(int m, int k, int n) {
-  if (m < 1 || m > 128 || k < 32 || n < 32) return 0;
+  if (m < 1 || m > 256 || k < 32 || n < 32) return 0;
   return a_image_bytes(m, k) + (size_t)kMaxRingSplits * (size_t)((m + 15) / 16 * 16) * (size_t)n * 4u;
 }
 
@@ -2033,7 +2042,7 @@ int hb_f16_gemm_ws(float *d_y, const float *d_x, const uint16_t *d_packed, const
   if (!aligned(d_x, 16) || !aligned(d_packed, 16) || !aligned(d_y, 4) || (d_bias && !aligned(d_bias, 4)))
     return hb_invalid("hb_f16_gemm alignment");
   hipStream_t st = hb_resolve_stream(s);
-  const bool splitk_ok = ring_splitk_mode() != 0 && m <= 128 && d_workspace &&
+  const bool splitk_ok = ring_splitk_mode() != 0 && m <= 256 && d_workspace &&
                          workspace_bytes >= ring_splitk_bytes(m, k, n) && aligned(d_workspace, 256);
   if (splitk_ok && ring_splitk_mode() == 1)
     return launch_ring_splitk(d_y, d_x, d_packed, d_bias, m, k, n, channels, mode, d_workspace, st);

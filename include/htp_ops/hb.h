@@ -232,8 +232,8 @@ int hb_f16_gemm(float *d_y, const float *d_x, const uint16_t *d_packed, const fl
 /* Workspace of hb_f16_gemm_ws: the largest of the few-rows (m <= 128) split-K
  * partial sums, for 64 or more rows and at least 4 GFLOP the fp16 activation
  * image of the ring path (2 * ceil(m/16)*16 * k bytes), and for m <= 128 that
- * image plus eight fp32 partial-sum slices of ceil(m/16)*16 x n (the split-K
- * ring path); 0 when none applies (the tiled kernel needs none). */
+ * image plus eight fp32 partial-sum slices of ceil(m/16)*16 x n for m <= 256
+ * (the split-K ring path); 0 when none applies (the tiled kernel needs none). */
 size_t hb_f16_workspace_bytes(int m, int k, int n);
 
 /* Tuning and test hook of the F16 path for 64 rows or more with a workspace:

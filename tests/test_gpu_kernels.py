@@ -453,6 +453,7 @@ def f16_case(orc, m, k, n, seed, bias=True):
     (64, 4096, 4096, 0, 4096, True),  # as many 32x32 tiles as CUs: split-K with a workspace
     (77, 1280, 5120, 1, 5120, True),  # 13 MB of weights: the split-K ring path rather than one launch
     (100, 10240, 512, 3, 480, True),  # long K, channel-major, split-K ring path
+    (200, 4096, 1024, 2, 1024, True), # two 128-row tiles on the split-K ring path
 ])
 @pytest.mark.parametrize("split_k", [False, True])
 def test_f16_gemm_epilogue(hip, orc, m, k, n, mode, channels, bias, split_k):
@@ -533,6 +534,7 @@ def test_f16_ring_matches_tiles(hip, orc, m, k, n, mode, bias, check_oracle):
     (4096, 256, 6144, 1, True, False),    # three rounds, GELU
     (2048, 1536, 1152, 0, True, False),   # long k, few tiles
     (333, 224, 2080, 2, True, True),      # n % 128 == 32: a last tile of one column pair, its bias clamped
+    (256, 256, 8192, 1, True, False),     # one 256-row tile: 256 x 64 streaming tiles
 ])
 def test_f16_stream_matches_ring(hip, orc, m, k, n, mode, bias, check_oracle):
     """The persistent streaming F16 kernel gives the same bits as the ring
