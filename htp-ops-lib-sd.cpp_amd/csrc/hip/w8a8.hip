@@ -13,6 +13,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <cmath>
 #include <cstdint>
 #include <cstdlib>
 
@@ -1419,6 +1420,122 @@ __global__ __launch_bounds__(256) void w8a8_readout(float *__restrict__ y, int l
 // One thread per output byte position (row, 32-column half, byte in 128).
 // ---------------------------------------------------------------------------
 
+// Split-K GEMM for up to 256 rows: grid (tiles, splits), split s multiplies
+// k-steps [s*kps, s*kps + kps) of its BM x BN tile with the tiled kernel's
+// k loop and stores the plain int32 sums (no column correction) to slice s
+// of the workspace ([mp][n] per slice; rows past m dropped by the buffer
+// bound).  w8a8_splitk_readout adds the slices and applies the epilogue;
+// 32-bit wrapping sums are exact in any order, so the result equals the
+// one-pass GEMM bit for bit.
+template <int BM, int BN, int WM, int WN, int S>
+__global__ __launch_bounds__(64 * WM *WN) void w8a8_splitk_partial(int32_t *__restrict__ ws,
+                                                                  const int8_t *__restrict__ q,
+                                                                  const int8_t *__restrict__ wpack, int m, int n,
+                                                                  int kp, int kps) {
+  constexpr int NW = WM * WN;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int FM = WTM / 16, FN = WTN / 16;
+  constexpr int ABLK = BM / 16, BBLK = BN / 16;
+  constexpr int NB = ABLK + BBLK;
+  constexpr int PW = (NB + NW - 1) / NW;
+  constexpr int PW_LO = NB / NW;
+  static_assert(PW_LO >= 1 && PW == PW_LO, "every wave issues the same DMA count");
+  constexpr int STAGE = NB * kFragBytes;
+  __shared__ __attribute__((aligned(1024))) int8_t lds[S * STAGE];
+
+  const int tiles_m = (m + BM - 1) / BM, tiles_n = (n + BN - 1) / BN;
+  int tm, tn;
+  tile_coords_2d<BM, BN>(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int kt_count = kp / kKStep;
+  const int kt0 = blockIdx.y * kps, steps = min(kps, kt_count - kt0);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int wm = wave / WN, wn = wave % WN;
+  const int8_t *src[PW];
+  int stride[PW];
+  const int nblocks = n / 16;
+#pragma unroll
+  for (int i = 0; i < PW; ++i) {
+    const int b = i * NW + wave;
+    if (b < ABLK) {
+      const int mb = min(m0 / 16 + b, (m + 15) / 16 - 1);
+      src[i] = q + (size_t)mb * kt_count * kFragBytes + lane * 16;
+    } else {
+      const int nb = min(n0 / 16 + (b - ABLK), nblocks - 1);
+      src[i] = wpack + (size_t)nb * kt_count * kFragBytes + lane * 16;
+    }
+    stride[i] = kFragBytes;
+  }
+  hb_i32x4 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = hb_i32x4{0, 0, 0, 0};
+#pragma unroll
+  for (int st = 0; st < S - 1; ++st)
+    if (st < steps) dma_stage<PW, NW, NB>(lds + (st % S) * STAGE, src, stride, kt0 + st, wave, lane);
+  for (int kt = 0; kt < steps; ++kt) {
+    wait_stage<PW, S - 2>(steps - 1 - kt);
+    block_barrier();
+    if (kt + S - 1 < steps)
+      dma_stage<PW, NW, NB>(lds + ((kt + S - 1) % S) * STAGE, src, stride, kt0 + kt + S - 1, wave, lane);
+    const int8_t *base = lds + (kt % S) * STAGE;
+    const int8_t *la = base + (wm * FM) * kFragBytes + lane * 16;
+    const int8_t *lb = base + (ABLK + wn * FN) * kFragBytes + lane * 16;
+    hb_i32x4 bf[FN];
+#pragma unroll
+    for (int j = 0; j < FN; ++j) bf[j] = *(const hb_i32x4 *)(lb + j * kFragBytes);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const hb_i32x4 af = *(const hb_i32x4 *)(la + i * kFragBytes);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf[j], acc[i][j], 0, 0, 0);
+    }
+  }
+  // lane l holds rows 4*(l/16)+r, column l%16 of each 16x16 block
+  const int mp = (m + 15) / 16 * 16;
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(ws + (size_t)blockIdx.y * mp * n, 0,
+                                                                      (uint32_t)m * (uint32_t)n * 4u, 0x00020000);
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int col = n0 + wn * WTN + j * 16 + (lane & 15);
+      if (col >= n) continue;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = m0 + wm * WTM + i * 16 + 4 * (lane >> 4) + r;
+        __builtin_amdgcn_raw_buffer_store_b32((uint32_t)acc[i][j][r], rs, (uint32_t)(row * n + col) * 4u, 0, 0);
+      }
+    }
+}
+
+// The split-K slices added in slice order (32-bit wrapping), then the GEMM
+// epilogue: corr is delta (scaled epilogues) or wsum128 (raw sums).  Four
+// outputs per thread, 16-byte loads and stores.
+template <int EPI>
+__global__ __launch_bounds__(256) void w8a8_splitk_readout(void *__restrict__ y, int ldy,
+                                                          const int32_t *__restrict__ part, int splits,
+                                                          const float *__restrict__ scales,
+                                                          const float *__restrict__ sw,
+                                                          const int32_t *__restrict__ corr, int m, int n) {
+  const size_t quads = (size_t)m * (size_t)(n / 4);
+  const size_t slice = (size_t)((m + 15) / 16 * 16) * (size_t)n;
+  for (size_t qd = (size_t)blockIdx.x * blockDim.x + threadIdx.x; qd < quads; qd += (size_t)gridDim.x * blockDim.x) {
+    const int row = (int)(qd / (size_t)(n / 4)), col = (int)(qd % (size_t)(n / 4)) * 4;
+    const int32_t *p = part + (size_t)row * n + col;
+    hb_u32x4 sum = *(const hb_u32x4 *)p;
+    for (int t = 1; t < splits; ++t) sum += *(const hb_u32x4 *)(p + (size_t)t * slice);
+    const hb_i32x4 c = *(const hb_i32x4 *)(corr + col);
+    const hb_f32x4 w = *(const hb_f32x4 *)(sw + col);
+    const float sr = EPI == HB_W8A8_EPI_RAW ? 0.0f : scales[row];
+    hb_u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = epilogue_bits<EPI>((int32_t)sum[e], c[e], w[e], sr);
+    __builtin_nontemporal_store(o, (hb_u32x4 *)((uint32_t *)y + (size_t)row * ldy + col));
+  }
+}
+
 __global__ __launch_bounds__(256) void w8a8_planes(uint8_t *__restrict__ out, const int32_t *__restrict__ raw, int m,
                                                   int n) {
   const size_t total = (size_t)m * (size_t)n * 4u;
@@ -1679,8 +1796,12 @@ int launch_gemm(void *y, int ldy, const int8_t *q, const float *scales, const in
 
 bool aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
-// Rows up to which quantization runs one workgroup per row.
-constexpr int kWgRowsMax = 64;
+// Quantization runs one workgroup per row up to these row counts (rows of
+// more than 2048 values up to the second): measured against the 8-row
+// blocks, 77x4096 6.44 -> 3.39 us, 256x4096 7.36 -> 3.49, 512x1536 3.97 ->
+// 3.27, 1024x4096 8.33 -> 6.87; the blocks lead from 1024x1536 (4.44
+// against 4.60) and 2048x4096 (10.27 against 11.75).
+constexpr int kWgRowsMax = 768, kWgRowsMaxLong = 1024;
 
 template <int NV, int ROWS, int MINB = 1, bool INV_LDS = false>
 void launch_quant_block(int8_t *d_q, float *d_scales, const float *d_x, const float *d_inv, int m, int k, int kp,
@@ -1832,8 +1953,9 @@ int hb_w8a8_quantize(int8_t *d_q, float *d_scales, const float *d_x, const float
   const int kp = (int)kp_of(k);
   const dim3 grid((m + 3) / 4), block(256);
   const bool vec = aligned(d_x, 16) && aligned(d_inv, 16);
-  // Few rows, or rows longer than the block kernel holds: a workgroup per row.
-  if (vec && (m <= kWgRowsMax || k > 256 * 24) && k <= kRowThreads * 4 * 16) {
+  // Up to about a thousand rows, or rows longer than the block kernel holds:
+  // a workgroup per row.
+  if (vec && (m <= kWgRowsMax || (m <= kWgRowsMaxLong && k > 2048) || k > 256 * 24) && k <= kRowThreads * 4 * 16) {
     const dim3 rows(m), threads(kRowThreads);
     if (k <= kRowThreads * 4 * 1) {
       hipLaunchKernelGGL(w8a8_quant_rows_wg<1>, rows, threads, 0, st, d_q, d_scales, d_x, d_inv, k, kp);
@@ -1935,6 +2057,79 @@ int hb_w8a8_gemm_tile(int m, int k, int n, int *bm, int *bn) {
   return choice;
 }
 
+}  // extern "C"
+
+namespace {
+
+// Split-K path of hb_w8a8_linear for 33 to 256 rows with long rows and few
+// 128 x 128 tiles: slices of the K loop on more CUs, their int32 sums in the
+// workspace after q and the scales (at most kMaxW8a8Splits slices), then
+// w8a8_splitk_readout.  It pays where the K loop is long: from 128 k-steps
+// (K 8192), or 80 with more than 128 rows (77x10240x4096 38.0 -> 22.8 us,
+// 128x10240x4096 39.1 -> 25.7, 256x10240x4096 41.5 -> 30.8, 256x5120x1280
+// 19.7 -> 16.2); at 64 k-steps and below the one-pass GEMM leads (48, 77 and
+// 256 rows at 4096x4096, 77x4096x14336, 128x4096x10240).  Slices: s k-steps
+// at about 0.28 us each on a 128 x 128 tile against s slices of 8 * mp * n
+// bytes written and read back at about 3 TB/s, least at
+// s = sqrt(steps * 105000 / (mp * n)) (measured best: 6-8, 6 and 4 slices at
+// the three K = 10240 shapes).
+constexpr int kMaxW8a8Splits = 8;
+
+// HTP_OPS_AMD_W8A8_SPLITK (measurement hook): unset or -1 automatic, 0 off,
+// 2..8 that many slices wherever 33-256 rows allow a split.
+int w8a8_splitk_mode() {
+  static const int mode = getenv("HTP_OPS_AMD_W8A8_SPLITK") ? atoi(getenv("HTP_OPS_AMD_W8A8_SPLITK")) : -1;
+  return mode;
+}
+
+int w8a8_splits(int m, int kp, int n) {
+  const long long tiles = (long long)((m + 127) / 128) * ((n + 127) / 128);
+  const int mode = w8a8_splitk_mode(), steps = kp / kKStep;
+  if (m < 33 || m > 256 || n % 16 || mode == 0) return 0;
+  int splits;
+  if (mode >= 2) {
+    splits = mode;
+  } else {
+    if (2 * tiles >= compute_units() || !(steps >= 128 || (steps >= 80 && m > 128))) return 0;
+    splits = (int)std::lround(std::sqrt((double)steps * 105000.0 / ((double)mp_of(m) * (double)n)));
+  }
+  splits = std::min(std::min(splits, kMaxW8a8Splits), steps);
+  return splits >= 2 ? splits : 0;
+}
+
+size_t w8a8_linear_workspace(int m, int k, int n) {
+  const size_t base = hb_w8a8_workspace_bytes(m, k);
+  if (!base || n < 16) return base;
+  return base + (w8a8_splits(m, (int)kp_of(k), n) ? (size_t)kMaxW8a8Splits * mp_of(m) * (size_t)n * 4u : 0);
+}
+
+template <int EPI>
+int launch_w8a8_splitk(float *y, const int8_t *q, const float *scales, const void *packed, int m, int k, int n,
+                       int splits, int32_t *part, hipStream_t st) {
+  const uint8_t *base = (const uint8_t *)packed;
+  const int8_t *wpack = (const int8_t *)(base + hb_w8a8_packed_offset(k, n, HB_W8A8_WEIGHTS));
+  const float *sw = (const float *)(base + hb_w8a8_packed_offset(k, n, HB_W8A8_SW));
+  const int32_t *delta = (const int32_t *)(base + hb_w8a8_packed_offset(k, n, HB_W8A8_DELTA));
+  const int kp = (int)kp_of(k), steps = kp / kKStep;
+  const int kps = (steps + splits - 1) / splits, used = (steps + kps - 1) / kps;
+  const int tiles = ((m + 127) / 128) * ((n + 127) / 128);
+  hipLaunchKernelGGL((w8a8_splitk_partial<128, 128, 2, 2, 4>), dim3(tiles, used), dim3(256), 0, st, part, q, wpack, m,
+                     n, kp, kps);
+  int rc = hb_check_launch("w8a8_splitk_partial");
+  if (rc) return rc;
+  const size_t quads = (size_t)m * (size_t)(n / 4);
+  const int grid = (int)std::min<size_t>((quads + 255) / 256, 65536);
+  hipLaunchKernelGGL((w8a8_splitk_readout<EPI>), dim3(grid), dim3(256), 0, st, y, n, part, used, scales, sw, delta,
+                     m, n);
+  return hb_check_launch("w8a8_splitk_readout");
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t hb_w8a8_linear_workspace_bytes(int m, int k, int n) { return w8a8_linear_workspace(m, k, n); }
+
 int hb_w8a8_linear(float *d_y, const float *d_x, const void *d_packed, int m, int k, int n, int epilogue,
                    void *d_workspace, size_t workspace_bytes, hb_stream s) {
   if (!d_workspace || workspace_bytes < hb_w8a8_workspace_bytes(m, k))
@@ -2008,6 +2203,19 @@ int hb_w8a8_linear(float *d_y, const float *d_x, const void *d_packed, int m, in
   }
   int rc = hb_w8a8_quantize(q, scales, d_x, inv, m, k, s);
   if (rc) return rc;
+  // 33-256 rows with few tiles: K split over the workspace's int32 slices,
+  // when the caller's workspace holds them (hb_w8a8_linear_workspace_bytes)
+  if (const int splits = w8a8_splits(m, kp, n)) {
+    if (workspace_bytes >= w8a8_linear_workspace(m, k, n) && d_y && aligned(d_y, 16) && aligned(d_packed, 256) &&
+        (epilogue == HB_W8A8_EPI_SCALE || epilogue == HB_W8A8_EPI_SCALE_GELU) &&
+        (size_t)(n / 16) * (size_t)kp * 16u < ((size_t)1 << 32)) {
+      int32_t *part = (int32_t *)((uint8_t *)d_workspace + hb_w8a8_workspace_bytes(m, k));
+      hipStream_t st = hb_resolve_stream(s);
+      return epilogue == HB_W8A8_EPI_SCALE
+                 ? launch_w8a8_splitk<HB_W8A8_EPI_SCALE>(d_y, q, scales, d_packed, m, k, n, splits, part, st)
+                 : launch_w8a8_splitk<HB_W8A8_EPI_SCALE_GELU>(d_y, q, scales, d_packed, m, k, n, splits, part, st);
+    }
+  }
   return hb_w8a8_gemm(d_y, n, q, scales, d_packed, m, k, n, epilogue, s);
 }
 

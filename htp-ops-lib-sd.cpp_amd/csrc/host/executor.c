@@ -481,12 +481,12 @@ static int exec_w8a8(uint8_t *payload, size_t payload_size) {
   if (stage_in(&act, s)) return -5;
   const float *x = (const float *)aligned_input(&act, 16, 2, s);
   if (!x) return -5;
-  const size_t ws_bytes = hb_w8a8_workspace_bytes(m, k);
+  const size_t ws_bytes = hb_w8a8_linear_workspace_bytes(m, k, n);
   uint8_t *ws = (uint8_t *)htp_executor_scratch(0, ws_bytes);
   if (!ws) return -5;
   int8_t *q = (int8_t *)ws;
   const size_t q_bytes = ((size_t)(m + 15) / 16 * 16) * ((size_t)(k + 63) / 64 * 64);
-  float *scales = (float *)(ws + (q_bytes + 255u) / 256u * 256u); /* layout of hb_w8a8_workspace_bytes */
+  float *scales = (float *)(ws + (q_bytes + 255u) / 256u * 256u); /* layout of hb_w8a8_workspace_bytes, the prefix */
   const float *inv = (const float *)((const uint8_t *)packed + hb_w8a8_packed_offset(k, n, HB_W8A8_INV));
   /* The GEMM writes 16-byte vectors: a misaligned output is produced in scratch and copied. */
   float *y = ((uintptr_t)out.dev % 16u) == 0 ? (float *)out.dev : (float *)htp_executor_scratch(3, out.bytes);

@@ -64,6 +64,7 @@ _SIGNATURES = {
     "hb_w8a8_packed_offset": (_c_size_t, [_c_int, _c_int, _c_int]),
     "hb_w8a8_prepack": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
     "hb_w8a8_workspace_bytes": (_c_size_t, [_c_int, _c_int]),
+    "hb_w8a8_linear_workspace_bytes": (_c_size_t, [_c_int, _c_int, _c_int]),
     "hb_w8a8_quantize": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
     "hb_w8a8_gemm": (_c_int, [_c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int,
                               _c_int, _c_void_p]),
@@ -303,6 +304,11 @@ def w8a8_prepack(blob_dev, k, n):
 
 def w8a8_workspace_bytes(m, k):
     return lib().hb_w8a8_workspace_bytes(m, k)
+
+
+def w8a8_linear_workspace_bytes(m, k, n):
+    """Workspace with room for hb_w8a8_linear's split-K slices where they apply."""
+    return lib().hb_w8a8_linear_workspace_bytes(m, k, n)
 
 
 def w8a8_quantize(x_dev, inv_ptr, m, k):

@@ -151,6 +151,15 @@ int hb_w8a8_gemm_choice(int m, int k, int n);
  * choice, or HB_E_INVAL.  Fills opcode 15's profile mode 3. */
 int hb_w8a8_gemm_tile(int m, int k, int n, int *bm, int *bn);
 
+/* Workspace that lets hb_w8a8_linear take its split-K path where one applies
+ * (33-256 rows with long rows, K from 8192 or from 5120 above 128 rows, whose
+ * 128 x 128 output tiles number fewer than half of the CUs: eight int32
+ * partial-sum slices of ceil(m/16)*16 x n after the quantized rows and
+ * scales); equal to hb_w8a8_workspace_bytes(m, k) where none applies.  The
+ * results are the same bits with either workspace.  No counterpart in the
+ * reference, whose executor sizes its own scratch (op_executor.cc). */
+size_t hb_w8a8_linear_workspace_bytes(int m, int k, int n);
+
 /* Full opcode-15 computation: quantize + GEMM + epilogue (workspace from hb_w8a8_workspace_bytes).
  * With the SCALE or SCALE_GELU epilogue, 16-byte aligned x and y and K a
  * multiple of 32, small problems run as one launch that quantizes its own
@@ -166,7 +175,8 @@ int hb_w8a8_linear(float *d_y, const float *d_x, const void *d_packed, int m, in
  * hb_w8a8_linear, with its workspace in a library-owned static device array
  * of HB_W8A8_STATIC_SCRATCH_BYTES (32 MiB) per GPU, held until the process
  * ends; hb_w8a8_workspace_bytes(m, k) must not exceed it (e.g. 4096 x 6144
- * fits, 4096 x 8192 does not), else HB_E_INVAL.  Allocates nothing: no
+ * fits, 4096 x 8192 does not), else HB_E_INVAL.  The split-K path runs where
+ * hb_w8a8_linear_workspace_bytes(m, k, n) fits too.  Allocates nothing: no
  * hipMalloc, no allocating library call.  Every call on one GPU shares that
  * GPU's array, so calls that overlap on one GPU (other streams, other
  * threads) race; calls in one stream are ordered.  hb_init(device) prepares

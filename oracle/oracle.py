@@ -144,13 +144,19 @@ def weight_offset(k, n_idx, k_idx):
 
 
 def pack_blob(w_nk, sw, sums=None, inv=None, signature=0):
-    """w_nk: int8 [n][k] -> constants blob (uint8)."""
+    """w_nk: int8 [n][k] -> constants blob (uint8).  The weight section holds
+    64-column groups of 32-row blocks, so only k % 32 == 0 and n % 64 == 0
+    address inside it; other shapes are refused before the C packer runs."""
     w_nk = np.ascontiguousarray(w_nk, np.int8)
     n, k = w_nk.shape
+    if k < 32 or k % 32 or n < 64 or n % 64:
+        raise ValueError(f"W8A8 blob needs k % 32 == 0 and n % 64 == 0 (k={k}, n={n})")
     blob = np.zeros(blob_bytes(k, n), np.uint8)
     sw = np.ascontiguousarray(sw, np.float32)
     sums = None if sums is None else np.ascontiguousarray(sums, np.int32)
     inv = None if inv is None else np.ascontiguousarray(inv, np.float32)
+    if sw.size != n or (sums is not None and sums.size != n) or (inv is not None and inv.size != k):
+        raise ValueError("W8A8 blob: sw and sums need n entries, inv k entries")
     lib().oracle_w8a8_pack_blob(_ptr(blob), _ptr(w_nk), _ptr(sw), _ptr(sums), _ptr(inv), k, n, signature)
     return blob
 

@@ -38,14 +38,17 @@ def upload_blob(hip, blob):
 
 @pytest.mark.parametrize("m,k,inv_kind", [(77, 768, "ones"), (77, 768, "uniform"), (1, 96, "ones"), (5, 32, "uniform"),
                                           (33, 6144, "uniform"), (4, 14336, "ones"), (130, 1536, "uniform"),
-                                          # one workgroup per row: few rows (<= 64) or rows past 6144
+                                          # one workgroup per row: up to 768 rows (1024 for rows past 2048
+                                          # values) or rows past 6144 values
                                           (64, 1536, "uniform"), (65, 1536, "uniform"), (2, 2080, "uniform"),
                                           (3, 8192, "uniform"), (1, 16416, "ones"), (70, 14336, "uniform"),
-                                          (2, 32768, "uniform"),
-                                          # 16-row and 8-row blocks (m > 64, k <= 6144), ragged m and k % 64 == 32
-                                          (100, 480, "uniform"), (97, 1024, "ones"), (72, 2048, "uniform"),
-                                          (81, 3040, "uniform"), (90, 4096, "uniform"), (75, 6144, "uniform"),
-                                          (129, 5152, "uniform"),
+                                          (2, 32768, "uniform"), (100, 480, "uniform"), (256, 4096, "ones"),
+                                          (768, 1536, "uniform"), (1024, 4096, "uniform"), (2049, 8192, "uniform"),
+                                          # 8-row blocks (769+ rows at up to 2048 values, 1025+ beyond),
+                                          # ragged m and k % 64 == 32
+                                          (1001, 480, "uniform"), (777, 1024, "ones"), (801, 1536, "uniform"),
+                                          (1030, 2048, "uniform"), (1100, 3040, "uniform"), (1031, 4096, "uniform"),
+                                          (1029, 6144, "uniform"), (1025, 5152, "uniform"),
                                           # from 2048 rows: 16-row blocks at one per CU (4096 x 1536 in the
                                           # baseline tests), else 8-row blocks with the smoothing vector in LDS
                                           (2100, 1536, "uniform"), (2048, 1248, "ones")])
@@ -311,6 +314,34 @@ def test_w8a8_decode_fused_bit_exact(hip, orc, m, k, n):
     hip.sync()
     ref = orc.linear(x, blob, k, n)
     np.testing.assert_array_equal(y.read(np.uint32, m * n).reshape(m, n), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("m,k,n,gelu,check_oracle", [
+    (77, 8192, 1024, False, True),    # 128 k-steps: eight slices of 16
+    (40, 8224, 512, True, False),     # 129 k-steps in slices of 17: a short last slice
+    (200, 5120, 512, False, True),    # 80 k-steps over 129-256 rows: two row tiles
+    (100, 8192, 1088, True, False),   # n % 128 == 64: a last tile half past n
+])
+def test_w8a8_linear_splitk_bit_exact(hip, orc, m, k, n, gelu, check_oracle):
+    """33-256 rows with few output tiles: with hb_w8a8_linear_workspace_bytes
+    the GEMM splits K over int32 slices, which add exactly, so the result
+    equals the one-pass GEMM (the smaller workspace) bit for bit."""
+    big, small = hip.w8a8_linear_workspace_bytes(m, k, n), hip.w8a8_workspace_bytes(m, k)
+    assert big > small
+    x, _, blob = make_w8a8(orc, m, k, n, seed=k + n + m, inv_kind="uniform", sums_kind="random", outliers=0.01)
+    x[m - 1] *= 7.0
+    packed = hip.w8a8_prepack(upload_blob(hip, blob), k, n)
+    xd = hip.DeviceBuffer.from_array(x)
+    epi = hip.EPI_SCALE_GELU if gelu else hip.EPI_SCALE
+    y1, y2 = hip.DeviceBuffer(m * n * 4), hip.DeviceBuffer(m * n * 4)
+    y1.fill(0xFF)
+    hip.w8a8_linear(y1, xd, packed, m, k, n, hip.DeviceBuffer(big), epilogue=epi)
+    hip.w8a8_linear(y2, xd, packed, m, k, n, hip.DeviceBuffer(small), epilogue=epi)
+    hip.sync()
+    got = y1.read(np.uint32, m * n)
+    np.testing.assert_array_equal(got, y2.read(np.uint32, m * n))
+    if check_oracle:
+        np.testing.assert_array_equal(got.reshape(m, n), orc.linear(x, blob, k, n).view(np.uint32))
 
 
 @pytest.mark.parametrize("m,k,n", [
