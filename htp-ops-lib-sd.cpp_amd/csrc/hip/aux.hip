@@ -192,22 +192,38 @@ __global__ __launch_bounds__(T) void aux_norm(float *__restrict__ y, const float
 }
 
 // Group norm over few long groups: each group is split into `chunks` pieces
-// of `chunk` values (a multiple of 4) handled by separate workgroups, in
-// three launches that keep the reference's two-pass statistics: the chunk
-// sums, then the centered sums of squares about the group's float mean, then
-// the output.  Every workgroup of a group adds the per-chunk partials in the
-// same order, so all of them derive the same mean and inv.
+// of `chunk` values (a multiple of 4) handled by separate workgroups, in two
+// launches.  The first reads x once for shifted sums per chunk: with s the
+// group's first value and d = x - s (exact in double for floats within 2^29
+// of each other, otherwise below 1e-16 relative), sum d and sum d^2.
+// The second adds the chunk partials in chunk order (so every workgroup of a
+// group derives the same mean and inv), takes the reference's float mean
+// (float)(sum x / len) with sum x = sum d + len * s, and its centered sum of
+// squares about that mean, sum (x - mean)^2 = sum d^2 - 2 e sum d + len e^2
+// with e = mean - s (exact in double), then writes the output.  The
+// reference's second pass rounds each x - mean to float before squaring;
+// the two sums differ by about 1e-10 relative (1e-16 * len in the worst
+// case, a shift far from every other value), so inv is the same float but
+// at rounding ties.  Centering on a sample of the group keeps the
+// cancellation bounded where |mean| >> standard deviation.
 // ws: double sum[tasks][chunks], then double sq[tasks][chunks].
-__device__ inline double ordered_total(const double *part, int chunks, double *red) {
-  // thread 0 adds the partials in chunk order; the block reads its result
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    double t = 0.0;
-    for (int c = 0; c < chunks; ++c) t += part[c];
-    red[0] = t;
-  }
-  __syncthreads();
-  return red[0];
+constexpr int kGnUnroll = 4;
+
+__device__ inline void shifted_add(const float4 v, double shift, double &s, double &q) {
+  const double d0 = (double)v.x - shift, d1 = (double)v.y - shift, d2 = (double)v.z - shift,
+               d3 = (double)v.w - shift;
+  s += (d0 + d1) + (d2 + d3);
+  q = fma(d3, d3, fma(d2, d2, fma(d1, d1, fma(d0, d0, q))));
+}
+
+// n / d for quotients below 2^22: the float estimate n * (1/d) is within one
+// of the quotient there (three roundings of 2^-24 each), and one step against
+// the remainder makes it exact.
+__device__ inline unsigned small_quotient(unsigned n, unsigned d, float rd) {
+  int q = (int)__fmul_rn((float)n, rd);
+  const int r = (int)n - q * (int)d;
+  q += r < 0 ? -1 : (r >= (int)d ? 1 : 0);
+  return (unsigned)q;
 }
 
 template <int PASS>
@@ -217,47 +233,98 @@ __global__ __launch_bounds__(kAuxThreads) void aux_group_norm_chunk(float *__res
                                                                     int chunk, int chunks, int tasks, int channels,
                                                                     int spatial, int groups, float eps, int act) {
   __shared__ double red[kAuxThreads / 64];
+  __shared__ float stats[2];
+  constexpr int T = kAuxThreads;
   const int c = blockIdx.x, task = blockIdx.y;
   const size_t offset = (size_t)task * (size_t)len;
-  const int begin = c * chunk, end = min(begin + chunk, len);
+  const int v0 = c * (chunk / 4), v1 = min(c * chunk + chunk, len) / 4;  // the chunk's float4 range
   const float4 *xr = (const float4 *)(x + offset);
   double *sum = ws + (size_t)task * chunks, *sq = ws + (size_t)tasks * chunks + (size_t)task * chunks;
+  const float shift = x[offset];
   if (PASS == 0) {
-    double s = 0.0;
-    for (int i = begin / 4 + threadIdx.x; i < end / 4; i += kAuxThreads) {
-      const float4 v = xr[i];
-      s += (double)v.x + (double)v.y + (double)v.z + (double)v.w;
-    }
-    s = block_sum(s, red);
-    if (threadIdx.x == 0) sum[c] = s;
-    return;
-  }
-  const float mean = (float)(ordered_total(sum, chunks, red) / (double)len);
-  if (PASS == 1) {
-    double q = 0.0;
-    for (int i = begin / 4 + threadIdx.x; i < end / 4; i += kAuxThreads) {
-      const float4 v = xr[i];
-      const double d0 = __fsub_rn(v.x, mean), d1 = __fsub_rn(v.y, mean), d2 = __fsub_rn(v.z, mean),
-                   d3 = __fsub_rn(v.w, mean);
-      q += d0 * d0 + d1 * d1 + d2 * d2 + d3 * d3;
-    }
-    q = block_sum(q, red);
-    if (threadIdx.x == 0) sq[c] = q;
-    return;
-  }
-  const float inv = __fdiv_rn(1.0f, __fsqrt_rn((float)(ordered_total(sq, chunks, red) / (double)len + (double)eps)));
-  const size_t pbase = (size_t)(task % groups) * (size_t)(channels / groups);
-  float4 *yr = (float4 *)(y + offset);
-  for (int i = begin / 4 + threadIdx.x; i < end / 4; i += kAuxThreads) {
-    const float4 v = xr[i];
-    float o[4] = {v.x, v.y, v.z, v.w};
+    double s = 0.0, q = 0.0;
+    int i = v0 + (int)threadIdx.x;
+    for (; i + (kGnUnroll - 1) * T < v1; i += kGnUnroll * T) {
+      float4 v[kGnUnroll];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float t = norm_affine<2>(__fmul_rn(__fsub_rn(o[e], mean), inv), 4 * i + e, w, b, pbase, spatial);
-      o[e] = act ? activate(t, 4) : t;
+      for (int u = 0; u < kGnUnroll; ++u) v[u] = xr[i + u * T];
+#pragma unroll
+      for (int u = 0; u < kGnUnroll; ++u) shifted_add(v[u], (double)shift, s, q);
     }
-    yr[i] = make_float4(o[0], o[1], o[2], o[3]);
+    for (; i < v1; i += T) shifted_add(xr[i], (double)shift, s, q);
+    s = block_sum(s, red);
+    q = block_sum(q, red);
+    if (threadIdx.x == 0) {
+      sum[c] = s;
+      sq[c] = q;
+    }
+    return;
   }
+  if (threadIdx.x == 0) {
+    double ts = 0.0, tq = 0.0;
+    for (int k = 0; k < chunks; ++k) {
+      ts += sum[k];
+      tq += sq[k];
+    }
+    const double n = (double)len;
+    const float mean = (float)((ts + n * (double)shift) / n);
+    const double e = (double)mean - (double)shift;
+    const double centered = (tq - 2.0 * e * ts) + n * e * e;
+    stats[0] = mean;
+    stats[1] = __fdiv_rn(1.0f, __fsqrt_rn((float)(centered / n + (double)eps)));
+  }
+  __syncthreads();
+  const float mean = stats[0], inv = stats[1];
+  const int cpg = channels / groups;
+  const size_t pbase = (size_t)(task % groups) * (size_t)cpg;
+  const float rsp = __fdiv_rn(1.0f, (float)spatial);
+  const bool fast = cpg < (1 << 22);  // the channel within the group by small_quotient
+  // spatial % 4 == 0: a quad lies in one channel, and a lane's channel changes
+  // only every spatial / 4 quads, so its parameters stay in registers until then
+  const bool quad_channel = spatial % 4 == 0 && fast;
+  size_t held = ~(size_t)0;
+  float hw = 1.0f, hb = 0.0f;
+  float4 *yr = (float4 *)(y + offset);
+  auto finish = [&](float4 v, int idx) {
+    float o[4] = {v.x, v.y, v.z, v.w};
+    if (quad_channel && (w || b)) {
+      const size_t ch = pbase + small_quotient(4u * (unsigned)idx, (unsigned)spatial, rsp);
+      if (ch != held) {
+        held = ch;
+        hw = w ? w[ch] : 1.0f;
+        hb = b ? b[ch] : 0.0f;
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float t = __fmul_rn(__fsub_rn(o[e], mean), inv);
+        if (w) t = __fmul_rn(t, hw);
+        if (b) t = __fadd_rn(t, hb);
+        o[e] = act ? activate(t, 4) : t;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float t = __fmul_rn(__fsub_rn(o[e], mean), inv);
+        if (w || b) {
+          const unsigned i = 4u * (unsigned)idx + (unsigned)e;
+          const size_t ch = pbase + (fast ? small_quotient(i, (unsigned)spatial, rsp) : i / (unsigned)spatial);
+          if (w) t = __fmul_rn(t, w[ch]);
+          if (b) t = __fadd_rn(t, b[ch]);
+        }
+        o[e] = act ? activate(t, 4) : t;
+      }
+    }
+    __builtin_nontemporal_store(hb_f32x4{o[0], o[1], o[2], o[3]}, (hb_f32x4 *)(yr + idx));
+  };
+  int i = v0 + (int)threadIdx.x;
+  for (; i + (kGnUnroll - 1) * T < v1; i += kGnUnroll * T) {
+    float4 v[kGnUnroll];
+#pragma unroll
+    for (int u = 0; u < kGnUnroll; ++u) v[u] = xr[i + u * T];
+#pragma unroll
+    for (int u = 0; u < kGnUnroll; ++u) finish(v[u], i + u * T);
+  }
+  for (; i < v1; i += T) finish(xr[i], i);
 }
 
 // Modes 3, 4, 5, 6, 7, 10, 12: one thread per output value, grid-stride.
@@ -508,8 +575,6 @@ extern "C" int hb_model_aux_ws(float *d_y, const float *d_x, const float *d_w, c
         hipLaunchKernelGGL(aux_group_norm_chunk<0>, grid, block, 0, st, d_y, d_x, d_w, d_b, ws, len, gp.chunk,
                            gp.chunks, groups * batch, channels, spatial, groups, eps, activation);
         hipLaunchKernelGGL(aux_group_norm_chunk<1>, grid, block, 0, st, d_y, d_x, d_w, d_b, ws, len, gp.chunk,
-                           gp.chunks, groups * batch, channels, spatial, groups, eps, activation);
-        hipLaunchKernelGGL(aux_group_norm_chunk<2>, grid, block, 0, st, d_y, d_x, d_w, d_b, ws, len, gp.chunk,
                            gp.chunks, groups * batch, channels, spatial, groups, eps, activation);
         break;
       }

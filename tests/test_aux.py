@@ -340,13 +340,23 @@ def test_aux_norms_gpu(hip, orc, case):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("batch,channels,groups,spatial,affine,act", [
-    (1, 512, 32, 4096, True, 0), (2, 128, 32, 16384, False, 1), (1, 256, 32, 16388, True, 0),
-    (1, 64, 8, 65536 * 2, True, 0)])
-def test_aux_group_norm_split_gpu(hip, orc, batch, channels, groups, spatial, affine, act):
-    """Group norm split over many workgroups per group (hb_model_aux_ws)."""
+@pytest.mark.parametrize("batch,channels,groups,spatial,affine,act,kind", [
+    (1, 512, 32, 4096, True, 0, "normal"), (2, 128, 32, 16384, False, 1, "normal"),
+    (1, 256, 32, 16388, True, 0, "normal"), (1, 64, 8, 65536 * 2, True, 0, "normal"),
+    (1, 128, 32, 4096, True, 0, "offset"), (2, 64, 16, 8192, False, 0, "outlier"),
+    (1, 256, 16, 4097, True, 0, "normal"),   # odd spatial: a quad spans two channels
+    (1, 64, 8, 8192, True, 2, "normal")])    # affine then activation
+def test_aux_group_norm_split_gpu(hip, orc, batch, channels, groups, spatial, affine, act, kind):
+    """Group norm split over many workgroups per group (hb_model_aux_ws): the
+    statistics come from sums shifted by each group's first value.  "offset"
+    puts the mean far above the spread (1000 + 0.01 N(0, 1)), "outlier" makes
+    every group's first value (the shift) 1e4 against values near 1."""
     count = batch * channels * spatial
     x = rng_normal(count, 150, 2.0) + 0.75
+    if kind == "offset":
+        x = (rng_normal(count, 153, 0.01) + 1000.0).astype(np.float32)
+    elif kind == "outlier":
+        x[::count // (batch * groups)] = 1e4
     w = rng_normal(channels, 151) if affine else None
     b = rng_normal(channels, 152) if affine else None
     kw = dict(mode=2, count=count, width=spatial, channels=channels, spatial=spatial, groups=groups, batch=batch,

@@ -44,6 +44,7 @@ def rpc(nbytes, device):
     (16, 4096, 4096),  # few rows: quantize + decode GEMM
     (64, 1536, 1024),  # 5-128 rows, short K
     (300, 96, 512),    # quantize + tiled GEMM
+    (77, 8192, 1024),  # 33-256 rows, long K: split-K over int32 slices in the executor's workspace
 ])
 def test_opcode15_bit_exact(hip, orc, device, m, k, n):
     x, blob = w8a8_inputs(orc, m, k, n, seed=m + n, inv=True, sums=True)
