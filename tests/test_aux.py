@@ -299,6 +299,10 @@ NORM_CASES = [
     dict(mode=1, count=2050 * 9, width=2050, affine=True),                     # width % 4 != 0
     dict(mode=9, batch=2, spatial=77, width=1536, per_batch=True),
     dict(mode=9, batch=1, spatial=300, width=3072, per_batch=False, activation=1),
+    # two waves per row for 513-2048 values: 2, 3 and 4 float4 per thread
+    dict(mode=1, count=2048 * 40, width=2048, affine=True),
+    dict(mode=9, batch=2, spatial=50, width=2000, per_batch=True),
+    dict(mode=0, count=1028 * 33, width=1028, affine=True),
 ]
 
 
