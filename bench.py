@@ -458,6 +458,9 @@ def all_configs(steps, warmup, with_cpu=False, only=None):
     if wanted("C2_f16_text_mlp_77x768x3072x768"):
         progress("start C2")
         out["C2_f16_text_mlp_77x768x3072x768"] = f16_mlp_case(steps, warmup)
+    if wanted("f16_vae_mode3"):
+        progress("start F16 VAE convolutions")
+        out["f16_vae_mode3"] = f16_vae_cases(steps, warmup)
     if wanted("opcode19_aux"):
         progress("start opcode 19")
         out["opcode19_aux"] = aux_cases(steps, warmup, with_cpu=with_cpu)
@@ -830,6 +833,55 @@ def f16_mlp_case(steps, warmup, m=77, k=768, n=3072, rotate=6):
     return out
 
 
+VAE_CASES = {  # im2col GEMMs of a VAE decoder's 3x3 convolutions (512x512 output): M pixels, K = 9 x in-channels
+    "vae_conv_128x128_512ch": (16384, 4608, 512),
+    "vae_conv_256x256_256ch": (65536, 2304, 256),
+    "vae_conv_512x512_128ch": (262144, 1152, 128),
+}
+
+
+def f16_vae_cases(steps, warmup, rotate=2):
+    """Opcode 16 mode 3 (bias, channel-major [channels][M] output) at the
+    VAE decoder's convolution shapes: FP32 activations read once by the
+    activation-streaming kernel.  Graph-replayed mean per call with its
+    algorithmic bytes (4MK + 2NK + 4N + 4MN) and flops (2MNK)."""
+    lib = hip.lib()
+    stream = hip.default_stream()
+    rng = np.random.default_rng(5)
+    out = {}
+    for name, (m, k, n) in VAE_CASES.items():
+        sets = []
+        for _ in range(rotate):
+            w = (rng.standard_normal((k, n), dtype=np.float32) * 0.02).astype(np.float16)
+            pd = hip.DeviceBuffer.from_array(hip.permute_f16(w.view(np.uint16)))
+            packed = hip.f16_prepack(pd, k, n)
+            pd.free()
+            sets.append((packed, hip.DeviceBuffer.from_array(rng.standard_normal(n, dtype=np.float32) * 0.02)))
+        x = hip.DeviceBuffer.from_array(rng.standard_normal((m, k), dtype=np.float32))
+        y = hip.DeviceBuffer(m * n * 4)
+
+        def launch(i):
+            packed, bias = sets[i % rotate]
+            hip.check(lib.hb_f16_gemm_ws(y.ptr, x.ptr, packed.ptr, bias.ptr, m, k, n, n, 3, None, 0, stream),
+                      "hb_f16_gemm_ws")
+
+        for i in range(max(warmup, 3)):
+            launch(i)
+        hip.check(lib.hb_stream_sync(stream), "sync")
+        us = _timed_graph_us(launch, max(steps // 10, 20), 0, stream)
+        nbytes = 4 * m * k + 2 * n * k + 4 * n + 4 * m * n
+        out[name] = {"shape": f"M={m} K={k} N={n} mode=3", "us": round(us, 2),
+                     "tflops": round(2 * m * n * k / us * 1e-6, 1), "gbps": round(nbytes / us * 1e-3, 1),
+                     "frac_hbm": round(nbytes / us * 1e-3 / PEAK_HBM_GBPS, 4)}
+        progress(f"done {name}: {out[name]['us']} us")
+        for b in (x, y):
+            b.free()
+        for st in sets:
+            for b in st:
+                b.free()
+    return out
+
+
 def traffic_probe(steps=12, configs=False, only=None):
     """Workload of the counter passes (FETCH_SIZE, WRITE_SIZE, MFMA busy
     cycles): a plain elementwise copy of COPY_PROBE_BYTES (torch's unary
@@ -936,9 +988,10 @@ def main():
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--rotate", type=int, default=6)
-    ap.add_argument("--config", default="headline", choices=["headline", "all", "small", "aux", "qk0", "qkv"],
-                    help="small / aux / qk0 / qkv: only the C1 W8A8 and C2 F16 text-MLP cases / the opcode-19 "
-                         "cases / the opcode-2/3/4 cases / the opcode-12 fused QKV cases (print those cases alone)")
+    ap.add_argument("--config", default="headline", choices=["headline", "all", "small", "aux", "qk0", "qkv", "vae"],
+                    help="small / aux / qk0 / qkv / vae: only the C1 W8A8 and C2 F16 text-MLP cases / the opcode-19 "
+                         "cases / the opcode-2/3/4 cases / the opcode-12 fused QKV cases / the F16 mode-3 VAE "
+                         "convolution cases (print those cases alone)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true",
                     help="no HIP graph capture or replay (every timing stream-ordered); for profiler-traced runs")
@@ -976,6 +1029,9 @@ def main():
         return
     if args.config == "qk0":
         print(json.dumps({"opcodes_2_3_4_qk0": qk0_cases(args.steps, args.warmup)}), flush=True)
+        return
+    if args.config == "vae":
+        print(json.dumps({"f16_vae_mode3": f16_vae_cases(args.steps, args.warmup)}), flush=True)
         return
     if args.config == "qkv":
         print(json.dumps({"opcodes_8_10_11_12_qkv": qkv_cases(args.steps, args.warmup, with_cpu=not args.no_cpu)}),

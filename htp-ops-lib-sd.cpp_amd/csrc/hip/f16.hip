@@ -304,6 +304,201 @@ __global__ __launch_bounds__(256) void f16_pack_a(uint4 *__restrict__ img, const
   }
 }
 
+// ---------------------------------------------------------------------------
+// Many rows, few columns (VAE convolutions as im2col GEMMs: M pixels,
+// K = channels x 9, N output channels): the fp32 activations are the bulk of
+// the bytes, so they stream from HBM once, straight into registers (lane l
+// loads 8 values of row l % 16 per k-step as two float4, converted to fp16
+// there: the MFMA operand layout), while each k-step's weight fragments of
+// the workgroup's BN columns pass through an LDS ring that its waves fill
+// together (global_load_lds).  Each wave owns 16 rows x BN columns; the
+// loads of k-step kt + D are issued while k-step kt multiplies, unconditional
+// (past the end they repeat the last k-step, unused), so every wait counts
+// exactly D - 1 later k-steps of loads.  A workgroup covers BN columns;
+// larger n takes several column chunks, those of one row block dispatched
+// together so that the activation re-reads find the memory-side cache.
+// SWAP (row-major output, modes 0-2): the weights are the MFMA A operand, so
+// a lane holds 4 consecutive columns of one row and stores them as one
+// 16-byte vector; mode 3 (channel-major [channels][m]) keeps the activations
+// as the A operand, so a lane holds 4 consecutive rows of one channel.  The
+// k-steps are multiplied in order, one v_mfma_f32_16x16x32_f16 per 32 k, as
+// in f16_gemm_tiles, so the sums are the same.  Requires k % 32 == 0,
+// n % 16 == 0, 16-byte aligned x (and y for SWAP).
+// ---------------------------------------------------------------------------
+// k-step kt's weights into its ring stage (instruction i of the wave fills
+// fragment i * WAVES + wave); past the last k-step the last one is read
+// again (never used).
+template <int PW, int WAVES, int S, int STAGE>
+__device__ __attribute__((always_inline)) inline void xstream_issue_w(int8_t *lds, const int8_t *const *bsrc, int kt,
+                                                                     int kt_count, int wave) {
+  const int kc = min(kt, kt_count - 1);
+  int8_t *stage = lds + (kt % S) * STAGE;
+#pragma unroll
+  for (int i = 0; i < PW; ++i)
+    __builtin_amdgcn_global_load_lds(bsrc[i] + (size_t)kc * kFragBytes,
+                                     HB_LDS_PTR(stage + (i * WAVES + wave) * kFragBytes), 16, 0, 0);
+}
+
+// A wave's 16 rows x 32 activations of one k-step: two DMA instructions, each
+// bringing 8 whole 128-byte rows (16-byte piece p of row r' by the lane in
+// slot (8p + r') ^ 8i), into a 2 KB slot of the wave's own LDS queue.
+__device__ __attribute__((always_inline)) inline void xstream_issue_a(int8_t *slot, const float *const *arow, int kt,
+                                                                     int kt_count) {
+  const int kc = min(kt, kt_count - 1);
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+    __builtin_amdgcn_global_load_lds(arow[i] + 32 * kc, HB_LDS_PTR(slot + i * 1024), 16, 0, 0);
+}
+
+// DA: k-steps of activations in flight (a queue of DA 2 KB slots per wave in
+// LDS), DB: k-steps of weights in flight (a ring of DB + 1 stages shared by
+// the waves): the activations come from HBM and need the deeper queue, the
+// weights (a few MB read by every workgroup) mostly hit L2.
+template <int BN, int WAVES, int DA, int DB, bool SWAP>
+__global__ __launch_bounds__(64 * WAVES) void f16_gemm_xstream(float *__restrict__ y, const float *__restrict__ x,
+                                                              const int8_t *__restrict__ wpack,
+                                                              const float *__restrict__ bias, int m, int k, int n,
+                                                              int channels, int mode) {
+  constexpr int FN = BN / 16;                 // column fragments
+  constexpr int S = DB + 1;                   // weight ring stages
+  constexpr int STAGE = FN * kFragBytes;      // one k-step of the chunk's weights
+  constexpr int PW = FN / WAVES;              // weight DMA instructions per wave and k-step
+  constexpr int ASLOT = 2048;                 // one k-step of a wave's activations
+  // k-step kt waits for its weights (issued at step kt - DB, before that
+  // step's activation DMA) and its activations (issued at kt - DA <= kt - DB):
+  // younger are the 2 activation DMA of step kt - DB and the whole groups of
+  // the DB - 1 steps after it
+  constexpr int LATER = 2 + (DB - 1) * (PW + 2);
+  static_assert(PW * WAVES == FN && PW >= 1, "every wave issues the same weight DMA count");
+  static_assert(FN % 4 == 0, "fragments are read four at a time");
+  static_assert(DA >= DB && DB >= 1, "activations at least as far ahead as weights");
+  static_assert(LATER < 64, "vmcnt range");
+  __shared__ __attribute__((aligned(1024))) int8_t lds[S * STAGE + WAVES * DA * ASLOT];
+
+  const int chunks = (n + BN - 1) / BN;
+  const int tm = blockIdx.x / chunks, tn = blockIdx.x % chunks;
+  const int m0 = tm * 16 * WAVES, n0 = tn * BN;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int kt_count = k / 32, nblocks = n / 16;
+
+  const int8_t *bsrc[PW];
+#pragma unroll
+  for (int i = 0; i < PW; ++i) {
+    const int nb = min(n0 / 16 + i * WAVES + wave, nblocks - 1);
+    bsrc[i] = wpack + (size_t)nb * kt_count * kFragBytes + lane * 16;
+  }
+  // this lane's activation piece in DMA instruction i: row 8i + r', piece p
+  const float *arow[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int v = lane ^ (8 * i), p = v >> 3, r = v & 7;
+    arow[i] = x + (size_t)min(m0 + wave * 16 + 8 * i + r, m - 1) * k + 4 * p;
+  }
+  int8_t *const aq = lds + S * STAGE + wave * DA * ASLOT;  // this wave's activation queue
+  const uint32_t lds_addr = (uint32_t)(uintptr_t)HB_LDS_PTR(lds);
+  const uint32_t aq_addr = (uint32_t)(uintptr_t)HB_LDS_PTR(aq);
+  // where lane l (row l % 16, values 8 (l / 16) .. + 7) finds its two pieces
+  const int ar = lane & 15, aq2 = 2 * (lane >> 4);
+  const uint32_t a_lo = (uint32_t)((ar >> 3) * 64 + ((8 * aq2 + (ar & 7)) ^ (8 * (ar >> 3)))) * 16u;
+  const uint32_t a_hi = (uint32_t)((ar >> 3) * 64 + ((8 * (aq2 + 1) + (ar & 7)) ^ (8 * (ar >> 3)))) * 16u;
+  hb_f32x4 acc[FN];
+#pragma unroll
+  for (int j = 0; j < FN; ++j) acc[j] = hb_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // the groups of steps -DA .. -1, as the main loop would have issued them
+#pragma unroll
+  for (int s = -DA; s < 0; ++s) {
+    if (s + DB >= 0) xstream_issue_w<PW, WAVES, S, STAGE>(lds, bsrc, s + DB, kt_count, wave);
+    xstream_issue_a(aq + ((s + DA) % DA) * ASLOT, arow, s + DA, kt_count);
+  }
+  // One k-step.  After the wait this wave's DMA of k-step kt have landed;
+  // after the barrier every wave's have, and every wave is done with the
+  // weight stage k-step kt + DB reuses.  The activations are read (and their
+  // slot refilled with k-step kt + DA) first, then the weight fragments.
+  // All LDS reads are instructions the compiler does not track: it cannot
+  // tell the bytes read from the DMA targets in flight and would wait for
+  // every one of them (vmcnt(0)) before each read; the wait and the barrier
+  // cover the bytes read.
+#define XSTREAM_STEP(KT)                                                                                           \
+  do {                                                                                                             \
+    const int kt_ = (KT);                                                                                          \
+    wait_vmcnt<LATER>();                                                                                           \
+    block_barrier();                                                                                               \
+    const uint32_t aslot = aq_addr + (uint32_t)((kt_ % DA) * ASLOT);                                               \
+    hb_f32x4 lo, hi;                                                                                               \
+    asm volatile("ds_read_b128 %0, %1" : "=v"(lo) : "v"(aslot + a_lo));                                            \
+    asm volatile("ds_read_b128 %0, %1" : "=v"(hi) : "v"(aslot + a_hi));                                            \
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(lo), "+v"(hi));                                                     \
+    const hb_f16x8 af = {(_Float16)lo[0], (_Float16)lo[1], (_Float16)lo[2], (_Float16)lo[3],                      \
+                         (_Float16)hi[0], (_Float16)hi[1], (_Float16)hi[2], (_Float16)hi[3]};                      \
+    xstream_issue_w<PW, WAVES, S, STAGE>(lds, bsrc, kt_ + DB, kt_count, wave);                                    \
+    xstream_issue_a(aq + (kt_ % DA) * ASLOT, arow, kt_ + DA, kt_count);                                            \
+    const uint32_t base = lds_addr + (uint32_t)((kt_ % S) * STAGE + lane * 16);                                   \
+    _Pragma("unroll") for (int j0 = 0; j0 < FN; j0 += 4) {                                                        \
+      hb_u32x4 f[4];                                                                                               \
+      _Pragma("unroll") for (int q = 0; q < 4; ++q) asm volatile("ds_read_b128 %0, %1"                            \
+                                                                 : "=v"(f[q])                                     \
+                                                                 : "v"(base + (uint32_t)((j0 + q) * kFragBytes)));  \
+      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]));                     \
+      _Pragma("unroll") for (int q = 0; q < 4; ++q) {                                                             \
+        const hb_f16x8 bf = __builtin_bit_cast(hb_f16x8, f[q]);                                                    \
+        acc[j0 + q] = SWAP ? __builtin_amdgcn_mfma_f32_16x16x32_f16(bf, af, acc[j0 + q], 0, 0, 0)                 \
+                           : __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf, acc[j0 + q], 0, 0, 0);                \
+      }                                                                                                            \
+    }                                                                                                              \
+  } while (0)
+  for (int kt = 0; kt < kt_count; ++kt) XSTREAM_STEP(kt);
+#undef XSTREAM_STEP
+  wait_vmcnt<0>();  // no weight DMA may still write this workgroup's LDS when it ends
+
+  if constexpr (SWAP) {
+    // lane l: row m0 + 16 wave + l % 16, columns n0 + 16 j + 4 (l / 16) .. + 3
+    const int row = m0 + wave * 16 + (lane & 15);
+    if (row >= m) return;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int col = n0 + j * 16 + 4 * (lane >> 4);
+      if (col >= n) continue;
+      float b[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (bias) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) b[r] = bias[col + r];
+      }
+      hb_f32x4 out;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float v = (float)(_Float16)acc[j][r];
+        out[r] = apply_mode(bias ? __fadd_rn(v, b[r]) : v, mode);
+      }
+      __builtin_nontemporal_store(out, (hb_f32x4 *)(y + (size_t)row * n + col));
+    }
+  } else {
+    // lane l: rows m0 + 16 wave + 4 (l / 16) .. + 3, column n0 + 16 j + l % 16
+    const int row0 = m0 + wave * 16 + 4 * (lane >> 4);
+    const bool whole = row0 + 3 < m && (m & 3) == 0;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int col = n0 + j * 16 + (lane & 15);
+      if (col >= channels) continue;
+      const float b = bias ? bias[col] : 0.0f;
+      hb_f32x4 out;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float v = (float)(_Float16)acc[j][r];
+        out[r] = bias ? __fadd_rn(v, b) : v;
+      }
+      float *dst = y + (size_t)col * m + row0;
+      if (whole) {
+        __builtin_nontemporal_store(out, (hb_f32x4 *)dst);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (row0 + r < m) dst[r] = out[r];
+      }
+    }
+  }
+}
+
 // The k loop of the ring kernels: tile (m0, n0) of the product into acc (the
 // MFMA layout: lane l holds rows 4*(l/16)..+3 and column l%16 of each 16x16
 // block of this wave's WTM x WTN sub-tile).  On return every operand stage
@@ -1898,6 +2093,64 @@ int launch_small(int cf, float *y, const float *x, const void *weights, const fl
   return hb_check_launch("f16_small");
 }
 
+// -1: automatic, 0: off, 1: on wherever its alignment holds; the initial
+// value comes from HTP_OPS_AMD_F16_XSTREAM (hb_f16_force_xstream sets it).
+std::atomic<int> g_f16_xstream{-2};
+
+int xstream_mode() {
+  int mode = g_f16_xstream.load(std::memory_order_relaxed);
+  if (mode == -2) {
+    const char *v = getenv("HTP_OPS_AMD_F16_XSTREAM");
+    mode = (v && *v && f16_stream_setting_ok(atoi(v))) ? atoi(v) : -1;
+    int expected = -2;
+    if (!g_f16_xstream.compare_exchange_strong(expected, mode)) mode = expected;
+  }
+  return mode;
+}
+
+template <int BN, bool SWAP>
+void launch_xstream_t(float *y, const float *x, const uint16_t *packed, const float *bias, int m, int k, int n,
+                      int channels, int mode, hipStream_t st) {
+  constexpr int WAVES = 4, DA = 4, DB = 2;
+  const int grid = ((m + 16 * WAVES - 1) / (16 * WAVES)) * ((n + BN - 1) / BN);
+  hipLaunchKernelGGL((f16_gemm_xstream<BN, WAVES, DA, DB, SWAP>), dim3(grid), dim3(64 * WAVES), 0, st, y, x,
+                     (const int8_t *)packed, bias, m, k, n, channels, mode);
+}
+
+// Column chunk of the activation-streaming kernel: 128 or 256 columns.
+int xstream_bn(int n) { return n <= 128 ? 128 : 256; }
+
+bool xstream_aligned(const float *y, const float *x, int mode) {
+  return aligned(x, 16) && (mode == 3 || aligned(y, 16));
+}
+
+// Automatic use: many rows and few columns, where reading the fp32 rows once
+// beats converting them to an fp16 image first (the ring path: 8 bytes per
+// value moved before the GEMM reads 2 more) or re-reading them per
+// 128-column tile (the tiled kernel, which mode 3 takes otherwise).
+// Measured, us, previous path -> this kernel: mode 3 (VAE convolutions) at
+// 16384x2304x256 128 -> 49, 65536x2304x256 281 -> 185, 262144x1152x128 368
+// -> 291, 16384x4608x512 253 -> 161, 4096x1152x128 26.2 -> 15.9; mode 0 at
+// 65536x2304x256 267 -> 186, 262144x1152x128 477 -> 288, 16384x2304x256 74
+// -> 48, but 16384x4608x512 155 -> 162 and 4096x4608x512 54.6 -> 72.4 (two
+// column chunks against the ring kernel), so modes 0-2 stop at 256 columns.
+bool xstream_applies(int m, int n, int mode) {
+  return mode == 3 ? (m >= 2048 && n <= 512) : (m >= 4096 && n <= 256);
+}
+
+int launch_xstream(float *y, const float *x, const uint16_t *packed, const float *bias, int m, int k, int n,
+                   int channels, int mode, hipStream_t st) {
+  const int bn = xstream_bn(n);
+  if (mode == 3) {
+    if (bn == 128) launch_xstream_t<128, false>(y, x, packed, bias, m, k, n, channels, mode, st);
+    else launch_xstream_t<256, false>(y, x, packed, bias, m, k, n, channels, mode, st);
+  } else {
+    if (bn == 128) launch_xstream_t<128, true>(y, x, packed, bias, m, k, n, channels, mode, st);
+    else launch_xstream_t<256, true>(y, x, packed, bias, m, k, n, channels, mode, st);
+  }
+  return hb_check_launch("f16_gemm_xstream");
+}
+
 }  // namespace
 
 extern "C" {
@@ -2042,6 +2295,9 @@ int hb_f16_gemm_ws(float *d_y, const float *d_x, const uint16_t *d_packed, const
   if (!aligned(d_x, 16) || !aligned(d_packed, 16) || !aligned(d_y, 4) || (d_bias && !aligned(d_bias, 4)))
     return hb_invalid("hb_f16_gemm alignment");
   hipStream_t st = hb_resolve_stream(s);
+  const int xs = xstream_mode();
+  if (xs != 0 && xstream_aligned(d_y, d_x, mode) && (xs == 1 || xstream_applies(m, n, mode)))
+    return launch_xstream(d_y, d_x, d_packed, d_bias, m, k, n, channels, mode, st);
   const bool splitk_ok = ring_splitk_mode() != 0 && m <= 256 && d_workspace &&
                          workspace_bytes >= ring_splitk_bytes(m, k, n) && aligned(d_workspace, 256);
   if (splitk_ok && ring_splitk_mode() == 1)
@@ -2102,6 +2358,13 @@ int hb_f16_gemm_ws(float *d_y, const float *d_x, const uint16_t *d_packed, const
                        m, k, n, channels, mode);
   }
   return hb_check_launch("f16_gemm_tiles");
+}
+
+int hb_f16_force_xstream(int setting) {
+  if (!f16_stream_setting_ok(setting)) return hb_invalid("hb_f16_force_xstream setting");
+  const int prev = xstream_mode();
+  g_f16_xstream.store(setting, std::memory_order_relaxed);
+  return prev;
 }
 
 int hb_f16_force_stream(int setting) {

@@ -77,6 +77,7 @@ _SIGNATURES = {
     "hb_w8a8_linear_noalloc": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_void_p]),
     "hb_w8a8_force_tile": (_c_int, [_c_int]),
     "hb_f16_force_stream": (_c_int, [_c_int]),
+    "hb_f16_force_xstream": (_c_int, [_c_int]),
     "hb_w8a8_gemm_choice": (_c_int, [_c_int, _c_int, _c_int]),
     "hb_w8a8_gemm_tile": (_c_int, [_c_int, _c_int, _c_int, ctypes.POINTER(_c_int), ctypes.POINTER(_c_int)]),
     # F16
@@ -356,6 +357,15 @@ def f16_force_stream(setting):
     prev = lib().hb_f16_force_stream(setting)
     if prev < -1:
         check(prev, "hb_f16_force_stream")
+    return prev
+
+
+def f16_force_xstream(setting):
+    """Pins the activation-streaming F16 kernel: -1 automatic, 0 never, 1
+    wherever it applies; returns the previous setting."""
+    prev = lib().hb_f16_force_xstream(setting)
+    if prev < -1:
+        check(prev, "hb_f16_force_xstream")
     return prev
 
 

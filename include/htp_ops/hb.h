@@ -256,6 +256,14 @@ size_t hb_f16_workspace_bytes(int m, int k, int n);
  * environment variable HTP_OPS_AMD_F16_STREAM gives the initial value. */
 int hb_f16_force_stream(int setting);
 
+/* Pins the activation-streaming F16 kernel (f16_gemm_xstream: the fp32
+ * activations read once, converted in registers, for many rows and few
+ * columns): -1 restores the automatic choice, 0 never, 1 wherever x (and y
+ * outside mode 3) are 16-byte aligned.  Returns the previous setting.  The
+ * sums are those of the other F16 kernels.  No counterpart in the reference;
+ * HTP_OPS_AMD_F16_XSTREAM gives the initial value. */
+int hb_f16_force_xstream(int setting);
+
 /* hb_f16_gemm with a workspace: for m <= 128, a workspace of at least
  * hb_f16_workspace_bytes, and either m <= 16 or a shape whose output tiles
  * (of the size hb_f16_gemm would use) number no more than the device's CUs, K

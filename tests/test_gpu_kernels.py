@@ -595,6 +595,54 @@ def test_f16_stream_matches_ring(hip, orc, m, k, n, mode, bias, check_oracle):
         assert_f16_close(got.view(np.float32).reshape(m, n), ref, v_ref, bias_cols, f16_abs_dot(x, w), k)
 
 
+@pytest.mark.parametrize("m,k,n,channels,mode,bias,check_oracle", [
+    (4096, 1152, 128, 128, 3, True, True),      # VAE-like: channel-major, one 128-column chunk, 36 k-steps
+    (1000, 96, 256, 200, 3, True, True),        # channels < n, three k-steps
+    (997, 352, 128, 128, 3, False, True),       # m % 4 != 0: element stores; 11 k-steps (a tail of two)
+    (2050, 320, 96, 96, 0, True, True),         # row-major, n under one chunk, 10 k-steps (a tail of one)
+    (1500, 288, 320, 320, 1, True, True),       # two column chunks (256 + 64), GELU
+    (4096, 2304, 256, 256, 2, False, False),    # QuickGELU, 72 k-steps
+    (64, 32, 64, 64, 0, True, True),            # one k-step: fewer than the prefetch depth
+    (3000, 1152, 512, 384, 3, True, False),     # two chunks, channel-major, channels < n
+])
+def test_f16_xstream_matches_other_paths(hip, orc, m, k, n, channels, mode, bias, check_oracle):
+    """The activation-streaming F16 kernel (fp32 rows read once, converted in
+    registers) gives the same bits as the automatic choice without it (the
+    same v_mfma_f32_16x16x32_f16 sequence per output element) and stays
+    within the F16 bound of the oracle, in both output layouts."""
+    ws = hip.DeviceBuffer(max(hip.f16_workspace_bytes(m, k, n), 256))
+    x, w, perm, b = f16_case(orc, m, k, n, seed=m + k + n + 11, bias=bias)
+    packed = hip.f16_prepack(hip.DeviceBuffer.from_array(perm), k, n)
+    xd = hip.DeviceBuffer.from_array(x)
+    bvec = None if b is None else (b[:channels].copy() if mode == 3 else b)
+    bd = hip.DeviceBuffer.from_array(bvec) if bias else None
+    out_elems = m * (channels if mode == 3 else n)
+    y_x, y_o = hip.DeviceBuffer(out_elems * 4), hip.DeviceBuffer(out_elems * 4)
+    y_x.fill(0xFF)
+    prev = hip.f16_force_xstream(1)
+    try:
+        hip.f16_gemm(y_x, xd, packed, bd, m, k, n, channels, mode, workspace=ws)
+        hip.f16_force_xstream(0)
+        hip.f16_gemm(y_o, xd, packed, bd, m, k, n, channels, mode, workspace=ws)
+    finally:
+        hip.f16_force_xstream(prev)
+    hip.sync()
+    got = y_x.read(np.uint32, out_elems)
+    np.testing.assert_array_equal(got, y_o.read(np.uint32, out_elems))
+    if check_oracle:
+        ref = orc.f16_gemm_epilogue(x, perm, bvec, m, k, n, channels, mode)
+        v_ref = orc.f16_gemm_epilogue(x, perm, None, m, k, n, n, 0)
+        absdot = f16_abs_dot(x, w)
+        if mode == 3:
+            gotf = got.view(np.float32).reshape(channels, m)
+            v_ref, absdot = v_ref.T[:channels], absdot.T[:channels]
+            bias_cols = np.abs(bvec)[:, None] if bias else 0.0
+        else:
+            gotf = got.view(np.float32).reshape(m, n)
+            bias_cols = np.abs(b)[None, :] if bias else 0.0
+        assert_f16_close(gotf, ref, v_ref, bias_cols, absdot, k)
+
+
 def test_f16_all_ones_gives_k(hip, orc):
     m, k, n = 32, 256, 64
     x = np.ones((m, k), np.float32)
