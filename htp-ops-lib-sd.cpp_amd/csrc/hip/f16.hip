@@ -366,17 +366,30 @@ __global__ __launch_bounds__(64 * WAVES) void f16_gemm_xstream(float *__restrict
   constexpr int ASLOT = 2048;                 // one k-step of a wave's activations
   // k-step kt waits for its weights (issued at step kt - DB, before that
   // step's activation DMA) and its activations (issued at kt - DA <= kt - DB):
-  // younger are the 2 activation DMA of step kt - DB and the whole groups of
-  // the DB - 1 steps after it
-  constexpr int LATER = 2 + (DB - 1) * (PW + 2);
+  // younger are the whole groups of the DB - 1 steps after kt - DB, and the 2
+  // activation DMA of step kt - DB itself when they are a later k-step's
+  // (DA > DB; with DA == DB they are k-step kt's own)
+  constexpr int LATER = (DA > DB ? 2 : 0) + (DB - 1) * (PW + 2);
   static_assert(PW * WAVES == FN && PW >= 1, "every wave issues the same weight DMA count");
   static_assert(FN % 4 == 0, "fragments are read four at a time");
   static_assert(DA >= DB && DB >= 1, "activations at least as far ahead as weights");
   static_assert(LATER < 64, "vmcnt range");
   __shared__ __attribute__((aligned(1024))) int8_t lds[S * STAGE + WAVES * DA * ASLOT];
 
-  const int chunks = (n + BN - 1) / BN;
-  const int tm = blockIdx.x / chunks, tn = blockIdx.x % chunks;
+  // Workgroups are dealt to the 8 XCDs in turn (bid % 8).  With several
+  // column chunks and whole groups of 8 row blocks, the chunks of one row
+  // block are bid, bid + 8, ...: the same XCD, dispatched together, so the
+  // later chunks read the rows from that XCD's L2.
+  const int chunks = (n + BN - 1) / BN, tiles_m = (m + 16 * WAVES - 1) / (16 * WAVES);
+  const int bid = blockIdx.x;
+  int tm, tn;
+  if (chunks > 1 && tiles_m % 8 == 0) {
+    tm = (bid / (8 * chunks)) * 8 + bid % 8;
+    tn = (bid / 8) % chunks;
+  } else {
+    tm = bid / chunks;
+    tn = bid % chunks;
+  }
   const int m0 = tm * 16 * WAVES, n0 = tn * BN;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int kt_count = k / 32, nblocks = n / 16;
@@ -2108,13 +2121,28 @@ int xstream_mode() {
   return mode;
 }
 
-template <int BN, bool SWAP>
-void launch_xstream_t(float *y, const float *x, const uint16_t *packed, const float *bias, int m, int k, int n,
-                      int channels, int mode, hipStream_t st) {
-  constexpr int WAVES = 4, DA = 4, DB = 2;
+template <int BN, int WAVES, int DA, int DB, bool SWAP>
+void launch_xstream_form(float *y, const float *x, const uint16_t *packed, const float *bias, int m, int k, int n,
+                         int channels, int mode, hipStream_t st) {
   const int grid = ((m + 16 * WAVES - 1) / (16 * WAVES)) * ((n + BN - 1) / BN);
   hipLaunchKernelGGL((f16_gemm_xstream<BN, WAVES, DA, DB, SWAP>), dim3(grid), dim3(64 * WAVES), 0, st, y, x,
                      (const int8_t *)packed, bias, m, k, n, channels, mode);
+}
+
+// 8 waves (128 rows) per workgroup sharing one weight ring where their
+// workgroups still cover the CUs: 16384x4608x512 155 -> 122 us, 65536x2304x256
+// 184 -> 149, 262144x1152x128 291 -> 257 (mode 3); fewer rows keep 4-wave
+// workgroups, twice as many (16384x2304x256: 48 against 61.5 us).  A weight
+// ring one stage deeper (4 k-steps ahead) or activations 6 k-steps ahead
+// measured the same.
+template <int BN, bool SWAP>
+void launch_xstream_t(float *y, const float *x, const uint16_t *packed, const float *bias, int m, int k, int n,
+                      int channels, int mode, hipStream_t st) {
+  const long long blocks128 = (long long)((m + 127) / 128) * ((n + BN - 1) / BN);
+  if (blocks128 >= compute_units())
+    launch_xstream_form<BN, 8, 4, 3, SWAP>(y, x, packed, bias, m, k, n, channels, mode, st);
+  else
+    launch_xstream_form<BN, 4, 4, 2, SWAP>(y, x, packed, bias, m, k, n, channels, mode, st);
 }
 
 // Column chunk of the activation-streaming kernel: 128 or 256 columns.
@@ -2129,13 +2157,16 @@ bool xstream_aligned(const float *y, const float *x, int mode) {
 // value moved before the GEMM reads 2 more) or re-reading them per
 // 128-column tile (the tiled kernel, which mode 3 takes otherwise).
 // Measured, us, previous path -> this kernel: mode 3 (VAE convolutions) at
-// 16384x2304x256 128 -> 49, 65536x2304x256 281 -> 185, 262144x1152x128 368
-// -> 291, 16384x4608x512 253 -> 161, 4096x1152x128 26.2 -> 15.9; mode 0 at
-// 65536x2304x256 267 -> 186, 262144x1152x128 477 -> 288, 16384x2304x256 74
-// -> 48, but 16384x4608x512 155 -> 162 and 4096x4608x512 54.6 -> 72.4 (two
-// column chunks against the ring kernel), so modes 0-2 stop at 256 columns.
+// 16384x2304x256 128 -> 48, 65536x2304x256 281 -> 147, 262144x1152x128 368
+// -> 257, 16384x4608x512 253 -> 136, 4096x1152x128 26.2 -> 15.9; mode 0 at
+// 65536x2304x256 267 -> 145, 16384x2304x256 74 -> 47, but 4096x4608x512
+// 54.6 -> 72.4 (two column chunks of 4-wave workgroups against the ring
+// kernel), so modes 0-2 take 257-512 columns only where 128-row workgroups
+// fill the CUs.
 bool xstream_applies(int m, int n, int mode) {
-  return mode == 3 ? (m >= 2048 && n <= 512) : (m >= 4096 && n <= 256);
+  if (mode == 3) return m >= 2048 && n <= 512;
+  const long long blocks128 = (long long)((m + 127) / 128) * ((n + 255) / 256);
+  return m >= 4096 && (n <= 256 || (n <= 512 && blocks128 >= compute_units()));
 }
 
 int launch_xstream(float *y, const float *x, const uint16_t *packed, const float *bias, int m, int k, int n,

@@ -604,6 +604,10 @@ def test_f16_stream_matches_ring(hip, orc, m, k, n, mode, bias, check_oracle):
     (4096, 2304, 256, 256, 2, False, False),    # QuickGELU, 72 k-steps
     (64, 32, 64, 64, 0, True, True),            # one k-step: fewer than the prefetch depth
     (3000, 1152, 512, 384, 3, True, False),     # two chunks, channel-major, channels < n
+    # 128-row workgroups of 8 waves (row blocks x chunks fill the CUs)
+    (32818, 96, 128, 128, 3, True, True),       # ragged m (m % 128 == 50), one chunk
+    (16384, 64, 512, 448, 3, True, False),      # two chunks of one row block on one XCD (bid, bid + 8)
+    (16400, 160, 256, 256, 1, True, False),     # row-major, 129 row blocks, GELU
 ])
 def test_f16_xstream_matches_other_paths(hip, orc, m, k, n, channels, mode, bias, check_oracle):
     """The activation-streaming F16 kernel (fp32 rows read once, converted in
