@@ -461,6 +461,9 @@ def all_configs(steps, warmup, with_cpu=False, only=None):
     if wanted("f16_vae_mode3"):
         progress("start F16 VAE convolutions")
         out["f16_vae_mode3"] = f16_vae_cases(steps, warmup)
+    if wanted("f16_unet_mode3"):
+        progress("start F16 UNet convolutions")
+        out["f16_unet_mode3"] = f16_vae_cases(steps, warmup, cases=UNET_CASES, workspace=True)
     if wanted("opcode19_aux"):
         progress("start opcode 19")
         out["opcode19_aux"] = aux_cases(steps, warmup, with_cpu=with_cpu)
@@ -839,17 +842,25 @@ VAE_CASES = {  # im2col GEMMs of a VAE decoder's 3x3 convolutions (512x512 outpu
     "vae_conv_512x512_128ch": (262144, 1152, 128),
 }
 
+UNET_CASES = {  # the same for a 512x512 UNet's 3x3 convolutions (64x64 latent), with the F16 workspace
+    "unet_conv_16x16_1280ch": (256, 11520, 1280),
+    "unet_conv_32x32_640ch": (1024, 5760, 640),
+    "unet_conv_64x64_320ch": (4096, 2880, 320),
+}
 
-def f16_vae_cases(steps, warmup, rotate=2):
+
+def f16_vae_cases(steps, warmup, rotate=2, cases=None, workspace=False):
     """Opcode 16 mode 3 (bias, channel-major [channels][M] output) at the
     VAE decoder's convolution shapes: FP32 activations read once by the
-    activation-streaming kernel.  Graph-replayed mean per call with its
-    algorithmic bytes (4MK + 2NK + 4N + 4MN) and flops (2MNK)."""
+    activation-streaming kernel (no workspace); with workspace=True and
+    UNET_CASES the UNet's (the ring kernel and the split-K ring path).
+    Graph-replayed mean per call with its algorithmic bytes (4MK + 2NK + 4N
+    + 4MN) and flops (2MNK)."""
     lib = hip.lib()
     stream = hip.default_stream()
     rng = np.random.default_rng(5)
     out = {}
-    for name, (m, k, n) in VAE_CASES.items():
+    for name, (m, k, n) in (VAE_CASES if cases is None else cases).items():
         sets = []
         for _ in range(rotate):
             w = (rng.standard_normal((k, n), dtype=np.float32) * 0.02).astype(np.float16)
@@ -859,10 +870,12 @@ def f16_vae_cases(steps, warmup, rotate=2):
             sets.append((packed, hip.DeviceBuffer.from_array(rng.standard_normal(n, dtype=np.float32) * 0.02)))
         x = hip.DeviceBuffer.from_array(rng.standard_normal((m, k), dtype=np.float32))
         y = hip.DeviceBuffer(m * n * 4)
+        ws = hip.DeviceBuffer(max(hip.f16_workspace_bytes(m, k, n), 256)) if workspace else None
+        ws_ptr, ws_bytes = (ws.ptr, ws.nbytes) if ws else (None, 0)
 
         def launch(i):
             packed, bias = sets[i % rotate]
-            hip.check(lib.hb_f16_gemm_ws(y.ptr, x.ptr, packed.ptr, bias.ptr, m, k, n, n, 3, None, 0, stream),
+            hip.check(lib.hb_f16_gemm_ws(y.ptr, x.ptr, packed.ptr, bias.ptr, m, k, n, n, 3, ws_ptr, ws_bytes, stream),
                       "hb_f16_gemm_ws")
 
         for i in range(max(warmup, 3)):
@@ -874,7 +887,7 @@ def f16_vae_cases(steps, warmup, rotate=2):
                      "tflops": round(2 * m * n * k / us * 1e-6, 1), "gbps": round(nbytes / us * 1e-3, 1),
                      "frac_hbm": round(nbytes / us * 1e-3 / PEAK_HBM_GBPS, 4)}
         progress(f"done {name}: {out[name]['us']} us")
-        for b in (x, y):
+        for b in (x, y) + ((ws,) if ws else ()):
             b.free()
         for st in sets:
             for b in st:
@@ -1031,7 +1044,9 @@ def main():
         print(json.dumps({"opcodes_2_3_4_qk0": qk0_cases(args.steps, args.warmup)}), flush=True)
         return
     if args.config == "vae":
-        print(json.dumps({"f16_vae_mode3": f16_vae_cases(args.steps, args.warmup)}), flush=True)
+        print(json.dumps({"f16_vae_mode3": f16_vae_cases(args.steps, args.warmup),
+                          "f16_unet_mode3": f16_vae_cases(args.steps, args.warmup, cases=UNET_CASES,
+                                                          workspace=True)}), flush=True)
         return
     if args.config == "qkv":
         print(json.dumps({"opcodes_8_10_11_12_qkv": qkv_cases(args.steps, args.warmup, with_cpu=not args.no_cpu)}),

@@ -585,7 +585,7 @@ template <int BM, int BN, int WM, int WN, int S>
 __global__ __launch_bounds__(64 * WM *WN) void f16_gemm_ring(float *__restrict__ y, const int8_t *__restrict__ aimg,
                                                              const int8_t *__restrict__ wpack,
                                                              const float *__restrict__ bias, int m, int k, int n,
-                                                             int mode) {
+                                                             int channels, int mode) {
   constexpr int NW = WM * WN;
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int FM = WTM / 16, FN = WTN / 16;
@@ -601,10 +601,43 @@ __global__ __launch_bounds__(64 * WM *WN) void f16_gemm_ring(float *__restrict__
   hb_f32x4 acc[FM][FN];
   ring_mainloop<BM, BN, WM, WN, S>(acc, lds, aimg, wpack, m, k, n, m0, n0, wave, lane);
 
-  // Epilogue: fp16 readout, bias, activation, then each 16-row chunk staged
-  // in wave-private padded LDS and written as 16-byte vectors along rows.
   const int row0 = m0 + wm * WTM;
   const int col0 = n0 + wn * WTN;
+  if (mode == 3) {
+    // Channel-major output y[channels][m] (columns past channels dropped):
+    // lane l holds rows 4*(l/16)..+3 of column l%16 of each 16x16 block, one
+    // 16-byte store along M (element stores when m is not a multiple of 4).
+    const bool vec = (m & 3) == 0;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int col = col0 + j * 16 + (lane & 15);
+      if (col >= channels) continue;
+      const float b = bias ? bias[col] : 0.0f;
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int r0 = row0 + i * 16 + 4 * (lane >> 4);
+        if (r0 >= m) continue;
+        hb_f32x4 out;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float v = (float)(_Float16)acc[i][j][r];
+          out[r] = bias ? __fadd_rn(v, b) : v;
+        }
+        float *dst = y + (size_t)col * m + r0;
+        if (vec) {
+          __builtin_nontemporal_store(out, (hb_f32x4 *)dst);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (r0 + r < m) dst[r] = out[r];
+        }
+      }
+    }
+    return;
+  }
+
+  // Epilogue: fp16 readout, bias, activation, then each 16-row chunk staged
+  // in wave-private padded LDS and written as 16-byte vectors along rows.
   float bj[FN];
 #pragma unroll
   for (int j = 0; j < FN; ++j) bj[j] = bias ? bias[min(col0 + j * 16 + (lane & 15), n - 1)] : 0.0f;
@@ -646,7 +679,7 @@ __global__ __launch_bounds__(64 * WM *WN) void f16_gemm_ring(float *__restrict__
 template <int BM, int BN, int WM, int WN, int S>
 __global__ __launch_bounds__(64 * WM *WN) void f16_ring_splitk(float *__restrict__ ws, const int8_t *__restrict__ aimg,
                                                                const int8_t *__restrict__ wpack, int m, int k, int n,
-                                                               int kps) {
+                                                               int kps, int channel_major) {
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int FM = WTM / 16, FN = WTN / 16;
   constexpr int STAGE = (BM / 16 + BN / 16) * kFragBytes;
@@ -662,6 +695,19 @@ __global__ __launch_bounds__(64 * WM *WN) void f16_ring_splitk(float *__restrict
   ring_mainloop<BM, BN, WM, WN, S>(acc, lds, aimg, wpack, m, k, n, m0, n0, wave, lane, kt0, kt_n);
   // lane l holds rows 4*(l/16)..+3 and column l%16 of each 16x16 block
   const int mp = (m + 15) / 16 * 16;
+  if (channel_major) {
+    // slice s as [n][mp]: the lane's 4 rows of a column are one 16-byte store
+    float *slice = ws + (size_t)blockIdx.y * mp * n;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int col = n0 + wn * WTN + j * 16 + (lane & 15);
+        const int r0 = m0 + wm * WTM + i * 16 + 4 * (lane >> 4);
+        if (col < n && r0 < mp) *(hb_f32x4 *)(slice + (size_t)col * mp + r0) = acc[i][j];
+      }
+    return;
+  }
   const __amdgpu_buffer_rsrc_t rs =
       __builtin_amdgcn_make_buffer_rsrc(ws + (size_t)blockIdx.y * mp * n, 0, (uint32_t)m * (uint32_t)n * 4u, 0x00020000);
 #pragma unroll
@@ -1759,6 +1805,51 @@ __global__ __launch_bounds__(256) void f16_skinny_epilogue(float *__restrict__ y
   }
 }
 
+// Readout of channel-major split-K slices ([n][mp] each) for mode 3: one
+// thread per 4 rows of a column, slices added in order from zero as in
+// f16_skinny_epilogue, fp16 readout, bias, then one 16-byte store along M
+// (element stores when y + col * m is not 16-byte aligned).
+__global__ __launch_bounds__(256) void f16_splitk_readout_cm(float *__restrict__ y, const float *__restrict__ ws,
+                                                            const float *__restrict__ bias, int m, int n,
+                                                            int channels, int splits, int vec) {
+  const int mp = (m + 15) / 16 * 16;
+  const int quads = mp / 4;
+  const size_t total = (size_t)channels * quads;
+  const size_t slice = (size_t)mp * n;
+  for (size_t u = (size_t)blockIdx.x * blockDim.x + threadIdx.x; u < total; u += (size_t)gridDim.x * blockDim.x) {
+    const int col = (int)(u / (size_t)quads), row = 4 * (int)(u % (size_t)quads);
+    if (row >= m) continue;
+    const float *p = ws + (size_t)col * mp + row;
+    hb_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s0 = 0; s0 < splits; s0 += 4) {
+      hb_f32x4 v4[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) v4[t] = *(const hb_f32x4 *)(p + (size_t)min(s0 + t, splits - 1) * slice);
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        if (s0 + t < splits) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[r] += v4[t][r];
+        }
+    }
+    const float b = bias ? bias[col] : 0.0f;
+    hb_f32x4 out;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float v = (float)(_Float16)acc[r];
+      out[r] = bias ? __fadd_rn(v, b) : v;
+    }
+    float *dst = y + (size_t)col * m + row;
+    if (vec) {
+      __builtin_nontemporal_store(out, (hb_f32x4 *)dst);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (row + r < m) dst[r] = out[r];
+    }
+  }
+}
+
 bool aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
 int compute_units() {
@@ -1876,6 +1967,12 @@ int pick_ring_shape(int m, int n, long long *cost_out = nullptr) {
   return best;
 }
 
+// Workgroups of the ring kernel's launch for the shape pick_ring_shape takes.
+long long ring_tiles(int m, int n) {
+  const RingShape t = kRingShapes[pick_ring_shape(m, n)];
+  return (long long)((m + t.bm - 1) / t.bm) * ((n + t.bn - 1) / t.bn);
+}
+
 // The streaming kernel (f16_gemm_stream, one persistent workgroup per CU,
 // 256 x 128 tiles, 6 stages of 24 KB) where its tiles occupy at least half of
 // the CUs and its cost in the ring shapes' model (rounds of tiles x work per
@@ -1967,8 +2064,8 @@ int launch_f16_stream(float *y, const int8_t *a, const int8_t *w, const float *b
   return launch_f16_stream_t<kF16StreamBM, kF16StreamBN, kF16StreamStages>(y, a, w, bias, m, k, n, mode, st);
 }
 
-int launch_ring(float *y, const float *x, const uint16_t *packed, const float *bias, int m, int k, int n, int mode,
-                void *ws, hipStream_t st) {
+int launch_ring(float *y, const float *x, const uint16_t *packed, const float *bias, int m, int k, int n, int channels,
+                int mode, void *ws, hipStream_t st) {
   const int mp = (m + 15) / 16 * 16;
   const size_t slots = (size_t)mp * k / 8u;
   const int pg = (int)((slots + 255) / 256 < 65536 ? (slots + 255) / 256 : 65536);
@@ -1979,12 +2076,14 @@ int launch_ring(float *y, const float *x, const uint16_t *packed, const float *b
   // weights once where they cover half of the CUs (256x4096x14336 70.0 ->
   // 56.4 us, 256x4096x10240 39.5 -> 37.6; at 192 rows the ring kernel stays
   // ahead: 192x4096x10240 31.4 against 35.3).
+  // The streaming kernels write row-major rows only; mode 3 takes the ring kernel.
+  const bool rows_out = mode != 3;
   const bool narrow_auto = f16_stream_narrow() == 0 && m > 192 && m <= 256 && 2 * ((n + 63) / 64) >= compute_units();
-  if (f16_stream_mode() != 0 && (f16_stream_narrow() == 2 || narrow_auto) && k / 32 >= 6)
+  if (rows_out && f16_stream_mode() != 0 && (f16_stream_narrow() == 2 || narrow_auto) && k / 32 >= 6)
     return launch_f16_stream_t<256, 64, 7>(y, (const int8_t *)ws, (const int8_t *)packed, bias, m, k, n, mode, st);
-  if (f16_stream_mode() != 0 && f16_stream_narrow() == 3 && k / 32 >= 11)
+  if (rows_out && f16_stream_mode() != 0 && f16_stream_narrow() == 3 && k / 32 >= 11)
     return launch_f16_stream_t<128, 64, 12>(y, (const int8_t *)ws, (const int8_t *)packed, bias, m, k, n, mode, st);
-  if (f16_stream_applies(m, k, n))
+  if (rows_out && f16_stream_applies(m, k, n))
     return launch_f16_stream(y, (const int8_t *)ws, (const int8_t *)packed, bias, m, k, n, mode, st);
   const int shape = pick_ring_shape(m, n);
   const RingShape t = kRingShapes[shape];
@@ -1993,15 +2092,15 @@ int launch_ring(float *y, const float *x, const uint16_t *packed, const float *b
   switch (shape) {
     case 0:
       hipLaunchKernelGGL((f16_gemm_ring<128, 192, 2, 2, 4>), dim3(grid), dim3(256), 0, st, y, a, w, bias, m, k, n,
-                         mode);
+                         channels, mode);
       break;
     case 1:
       hipLaunchKernelGGL((f16_gemm_ring<128, 128, 2, 2, 4>), dim3(grid), dim3(256), 0, st, y, a, w, bias, m, k, n,
-                         mode);
+                         channels, mode);
       break;
     default:
       hipLaunchKernelGGL((f16_gemm_ring<64, 64, 2, 2, 4>), dim3(grid), dim3(256), 0, st, y, a, w, bias, m, k, n,
-                         mode);
+                         channels, mode);
       break;
   }
   return hb_check_launch("f16_gemm_ring");
@@ -2031,9 +2130,12 @@ int ring_splits(int m, int k, int n) {
   return splits < 1 ? 1 : splits;
 }
 
+constexpr int kRingSplitRows = 2048;
+
 size_t ring_splitk_bytes(int m, int k, int n) {
-  if (m < 1 || m > 256 || k < 32 || n < 32) return 0;
-  return a_image_bytes(m, k) + (size_t)kMaxRingSplits * (size_t)((m + 15) / 16 * 16) * (size_t)n * 4u;
+  if (m < 1 || m > kRingSplitRows || k < 32 || n < 32) return 0;
+  const int slices = m <= 256 ? kMaxRingSplits : ring_splits(m, k, n);
+  return a_image_bytes(m, k) + (size_t)slices * (size_t)((m + 15) / 16 * 16) * (size_t)n * 4u;
 }
 
 int launch_ring_splitk(float *y, const float *x, const uint16_t *packed, const float *bias, int m, int k, int n,
@@ -2049,22 +2151,38 @@ int launch_ring_splitk(float *y, const float *x, const uint16_t *packed, const f
   const int used = (k / 32 + kps - 1) / kps;  // slices that hold k-steps
   float *part = (float *)((uint8_t *)ws + a_image_bytes(m, k));
   const int tiles = ((m + 127) / 128) * ((n + 127) / 128);
+  const int cm = mode == 3;
   hipLaunchKernelGGL((f16_ring_splitk<128, 128, 2, 2, 4>), dim3(tiles, used), dim3(256), 0, st, part,
-                     (const int8_t *)ws, (const int8_t *)packed, m, k, n, kps);
+                     (const int8_t *)ws, (const int8_t *)packed, m, k, n, kps, cm);
   rc = hb_check_launch("f16_ring_splitk");
   if (rc) return rc;
+  if (cm) {
+    const size_t quads = (size_t)channels * (size_t)(mp / 4);
+    const int eg = (int)((quads + 255) / 256 < 4096 ? (quads + 255) / 256 : 4096);
+    const int vec = (m % 4 == 0) && aligned(y, 16);
+    hipLaunchKernelGGL(f16_splitk_readout_cm, dim3(eg), dim3(256), 0, st, y, part, bias, m, n, channels, used, vec);
+    return hb_check_launch("f16_splitk_readout_cm");
+  }
   const size_t outs = (size_t)m * (size_t)(mode == 3 ? channels : n);
   const int eg = (int)((outs + 255) / 256 < 4096 ? (outs + 255) / 256 : 4096);
   hipLaunchKernelGGL(f16_skinny_epilogue, dim3(eg), dim3(256), 0, st, y, part, bias, m, n, channels, mode, used);
   return hb_check_launch("f16_skinny_epilogue");
 }
 
-// -1 (default): the split-K ring path for 33 to 128 rows where the few-rows
-// split-K path would run; 0: never; 1: for every m <= 128 with a workspace
-// (HTP_OPS_AMD_F16_SPLITK, comparisons only).
+// -1 (default): the split-K ring path by the rules of hb_f16_gemm_ws; 0:
+// never; 1: for every m <= kRingSplitRows with a workspace
+// (hb_f16_force_splitk; HTP_OPS_AMD_F16_SPLITK gives the initial value).
+std::atomic<int> g_f16_splitk{-2};
+
 int ring_splitk_mode() {
-  static const int v = getenv("HTP_OPS_AMD_F16_SPLITK") ? atoi(getenv("HTP_OPS_AMD_F16_SPLITK")) : -1;
-  return v;
+  int mode = g_f16_splitk.load(std::memory_order_relaxed);
+  if (mode == -2) {
+    const char *v = getenv("HTP_OPS_AMD_F16_SPLITK");
+    mode = (v && *v && f16_stream_setting_ok(atoi(v))) ? atoi(v) : -1;
+    int expected = -2;
+    if (!g_f16_splitk.compare_exchange_strong(expected, mode)) mode = expected;
+  }
+  return mode;
 }
 
 // Few rows in one launch (f16_small): m <= 128, k <= 3072, a weight image
@@ -2154,19 +2272,18 @@ bool xstream_aligned(const float *y, const float *x, int mode) {
 
 // Automatic use: many rows and few columns, where reading the fp32 rows once
 // beats converting them to an fp16 image first (the ring path: 8 bytes per
-// value moved before the GEMM reads 2 more) or re-reading them per
-// 128-column tile (the tiled kernel, which mode 3 takes otherwise).
-// Measured, us, previous path -> this kernel: mode 3 (VAE convolutions) at
-// 16384x2304x256 128 -> 48, 65536x2304x256 281 -> 147, 262144x1152x128 368
-// -> 257, 16384x4608x512 253 -> 136, 4096x1152x128 26.2 -> 15.9; mode 0 at
-// 65536x2304x256 267 -> 145, 16384x2304x256 74 -> 47, but 4096x4608x512
-// 54.6 -> 72.4 (two column chunks of 4-wave workgroups against the ring
-// kernel), so modes 0-2 take 257-512 columns only where 128-row workgroups
-// fill the CUs.
+// value moved before the GEMM reads 2 more).  Below a few thousand rows the
+// kernel's k loop is latency-bound (its time is flat in m) and the ring
+// kernel, which writes every mode, stays ahead.  Measured, us, ring kernel /
+// this kernel (the same in modes 0 and 3): 16384x2304x256 74 / 49,
+// 65536x2304x256 267 / 145, 16384x4608x512 153 / 120, 8192x4608x512 99.6 /
+// 80.0, 8192x2304x256 41.3 / 40.4, 8192x1152x128 21.8 / 16.0, 4096x1152x128
+// 16.2 / 15.8; the ring kernel ahead at 4096x2304x256 28.5 / 40.4,
+// 4096x4608x512 55.3 / 72.5, 2048x2304x256 23.3 / 40.4.
 bool xstream_applies(int m, int n, int mode) {
-  if (mode == 3) return m >= 2048 && n <= 512;
-  const long long blocks128 = (long long)((m + 127) / 128) * ((n + 255) / 256);
-  return m >= 4096 && (n <= 256 || (n <= 512 && blocks128 >= compute_units()));
+  (void)mode;
+  if (n > 512) return false;
+  return m >= (n <= 128 ? 4096 : 8192);
 }
 
 int launch_xstream(float *y, const float *x, const uint16_t *packed, const float *bias, int m, int k, int n,
@@ -2329,7 +2446,7 @@ int hb_f16_gemm_ws(float *d_y, const float *d_x, const uint16_t *d_packed, const
   const int xs = xstream_mode();
   if (xs != 0 && xstream_aligned(d_y, d_x, mode) && (xs == 1 || xstream_applies(m, n, mode)))
     return launch_xstream(d_y, d_x, d_packed, d_bias, m, k, n, channels, mode, st);
-  const bool splitk_ok = ring_splitk_mode() != 0 && m <= 256 && d_workspace &&
+  const bool splitk_ok = ring_splitk_mode() != 0 && m <= kRingSplitRows && d_workspace &&
                          workspace_bytes >= ring_splitk_bytes(m, k, n) && aligned(d_workspace, 256);
   if (splitk_ok && ring_splitk_mode() == 1)
     return launch_ring_splitk(d_y, d_x, d_packed, d_bias, m, k, n, channels, mode, d_workspace, st);
@@ -2344,15 +2461,26 @@ int hb_f16_gemm_ws(float *d_y, const float *d_x, const uint16_t *d_packed, const
   const long long tiled_wgs = big >= 256 ? big : mid >= 128 ? mid : small;
   // From 33 rows the split-K ring path, except where the ring kernel has
   // more tiles than CUs at 4 GFLOP or more (77x4096x14336: 38.4 against
-  // 44.2 us) and where the one-launch kernel applies to under 12 MB of
+  // 44.2 us; counted in the ring's own tiles: 256x11520x1280, 80 tiles of
+  // 64 x 64, 67.7 on the ring against 27.3) and where the one-launch kernel applies to under 12 MB of
   // weights (77x768x3072: 6.7 against 11.1 us, 64x2048x2048 10.4 against
   // 11.3).  Measured, us, previous choice / split-K ring: 100x3072x3072 28.6
   // / 14.4 and 128x3072x3072 28.8 / 15.1 (one launch), 48x2048x8192 20.4 /
   // 17.0 and 77x1280x5120 17.1 / 14.3 (one launch, 13-34 MB of weights).
-  const bool ring_here = ring_worth_it(m, k, n) && tiled_wgs > compute_units();
-  const bool splitk_here = splitk_ok && m > 32 && !ring_here;
+  const bool ring_here = ring_worth_it(m, k, n) && tiled_wgs > compute_units() && ring_tiles(m, n) > compute_units();
+  const bool splitk_here = splitk_ok && m > 32 && m <= 256 && !ring_here;
   const int cf = aligned(d_y, 16) ? small_cf(m, k, n) : 0;
   if (splitk_here && (!cf || (size_t)n * (size_t)k * 2u >= ((size_t)12 << 20)))
+    return launch_ring_splitk(d_y, d_x, d_packed, d_bias, m, k, n, channels, mode, d_workspace, st);
+  // 257 to kRingSplitRows rows and k >= 2048: the split-K ring path where
+  // 128 x 128 tiles fill at most half of the CUs (the few-tile, long-k
+  // products of im2col convolutions).  Measured, us, ring kernel -> split-K, mode 0:
+  // 512x11520x1280 71.3 -> 43.5, 1024x11520x1280 84.5 -> 73.5, 1024x4608x512
+  // 34.8 -> 25.2, 1024x5760x640 41.3 -> 31.5, 512x5760x1280 38.0 -> 28.3,
+  // 2048x4608x512 39.9 -> 38.2, 1024x2880x640 23.4 -> 23.0; at 160 tiles
+  // (2048x11520x1280) 122.5 against 120.3.
+  const long long tiles128 = ((m + 127) / 128) * (long long)((n + 127) / 128);
+  if (splitk_ok && m > 256 && k >= 2048 && 2 * tiles128 <= compute_units())
     return launch_ring_splitk(d_y, d_x, d_packed, d_bias, m, k, n, channels, mode, d_workspace, st);
   if (cf) return launch_small<0>(cf, d_y, d_x, d_packed, d_bias, m, k, n, channels, mode, st);
   // The split-K path holds m <= 128 rows (8 row fragments) of partial sums.
@@ -2375,9 +2503,9 @@ int hb_f16_gemm_ws(float *d_y, const float *d_x, const uint16_t *d_packed, const
                        splits);
     return hb_check_launch("f16_skinny_epilogue");
   }
-  if (mode != 3 && d_workspace && ring_worth_it(m, k, n) && workspace_bytes >= a_image_bytes(m, k) &&
-      aligned(d_workspace, 256) && aligned(d_y, 16))
-    return launch_ring(d_y, d_x, d_packed, d_bias, m, k, n, mode, d_workspace, st);
+  if (d_workspace && ring_worth_it(m, k, n) && workspace_bytes >= a_image_bytes(m, k) && aligned(d_workspace, 256) &&
+      aligned(d_y, 16))
+    return launch_ring(d_y, d_x, d_packed, d_bias, m, k, n, channels, mode, d_workspace, st);
   if (big >= 256) {
     hipLaunchKernelGGL((f16_gemm_tiles<128, 128, 2, 2>), dim3((int)big), dim3(256), 0, st, d_y, d_x, d_packed, d_bias,
                        m, k, n, channels, mode);
@@ -2395,6 +2523,13 @@ int hb_f16_force_xstream(int setting) {
   if (!f16_stream_setting_ok(setting)) return hb_invalid("hb_f16_force_xstream setting");
   const int prev = xstream_mode();
   g_f16_xstream.store(setting, std::memory_order_relaxed);
+  return prev;
+}
+
+int hb_f16_force_splitk(int setting) {
+  if (!f16_stream_setting_ok(setting)) return hb_invalid("hb_f16_force_splitk setting");
+  const int prev = ring_splitk_mode();
+  g_f16_splitk.store(setting, std::memory_order_relaxed);
   return prev;
 }
 

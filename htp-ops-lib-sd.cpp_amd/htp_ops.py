@@ -78,6 +78,7 @@ _SIGNATURES = {
     "hb_w8a8_force_tile": (_c_int, [_c_int]),
     "hb_f16_force_stream": (_c_int, [_c_int]),
     "hb_f16_force_xstream": (_c_int, [_c_int]),
+    "hb_f16_force_splitk": (_c_int, [_c_int]),
     "hb_w8a8_gemm_choice": (_c_int, [_c_int, _c_int, _c_int]),
     "hb_w8a8_gemm_tile": (_c_int, [_c_int, _c_int, _c_int, ctypes.POINTER(_c_int), ctypes.POINTER(_c_int)]),
     # F16
@@ -366,6 +367,15 @@ def f16_force_xstream(setting):
     prev = lib().hb_f16_force_xstream(setting)
     if prev < -1:
         check(prev, "hb_f16_force_xstream")
+    return prev
+
+
+def f16_force_splitk(setting):
+    """Pins the F16 split-K ring path: -1 automatic, 0 never, 1 for every
+    m <= 2048 with a workspace; returns the previous setting."""
+    prev = lib().hb_f16_force_splitk(setting)
+    if prev < -1:
+        check(prev, "hb_f16_force_splitk")
     return prev
 
 

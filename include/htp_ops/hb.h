@@ -264,19 +264,29 @@ int hb_f16_force_stream(int setting);
  * HTP_OPS_AMD_F16_XSTREAM gives the initial value. */
 int hb_f16_force_xstream(int setting);
 
+/* Pins the split-K ring path of hb_f16_gemm_ws (f16_ring_splitk slices added
+ * in order by a readout kernel): -1 restores the automatic choice, 0 never
+ * (the ring or tiled kernel, whose sums are those of hb_f16_gemm), 1 for
+ * every m <= 2048 given a large enough workspace.  Returns the previous
+ * setting.  Split sums may differ from the unsplit ones in the last fp32 bit
+ * before the fp16 readout.  No counterpart in the reference;
+ * HTP_OPS_AMD_F16_SPLITK gives the initial value. */
+int hb_f16_force_splitk(int setting);
+
 /* hb_f16_gemm with a workspace: for m <= 128, a workspace of at least
  * hb_f16_workspace_bytes, and either m <= 16 or a shape whose output tiles
  * (of the size hb_f16_gemm would use) number no more than the device's CUs, K
  * is split across workgroups and the partial sums are added in a fixed order
  * before the fp16 readout rounding and the epilogue (two kernels; from 33
  * rows on, x is first converted to fp16 MFMA tiles and each split covers all
- * rows of a 128 x 128 tile, so the weights are read once).
- * Otherwise, for modes 0-2 with a workspace of at least
- * hb_f16_workspace_bytes, a 16-byte aligned output and 64 or more rows (4
- * GFLOP or more), x is converted once into fp16 MFMA tiles in the workspace
- * and both operands stream through the direct-to-LDS ring of the int8 GEMM;
- * the result equals hb_f16_gemm bit for bit.  Otherwise identical to
- * hb_f16_gemm. */
+ * rows of a 128 x 128 tile, so the weights are read once).  The same
+ * split-K ring path serves 257 to 2048 rows with k >= 2048 where 128 x 128
+ * output tiles would fill at most half of the CUs.
+ * Otherwise, with a workspace of at least hb_f16_workspace_bytes, a 16-byte
+ * aligned output and 64 or more rows (4 GFLOP or more), x is converted once
+ * into fp16 MFMA tiles in the workspace and both operands stream through the
+ * direct-to-LDS ring of the int8 GEMM; the result equals hb_f16_gemm bit for
+ * bit.  Otherwise identical to hb_f16_gemm. */
 int hb_f16_gemm_ws(float *d_y, const float *d_x, const uint16_t *d_packed, const float *d_bias, int m, int k, int n,
                    int channels, int mode, void *d_workspace, size_t workspace_bytes, hb_stream s);
 

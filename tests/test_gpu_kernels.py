@@ -485,11 +485,15 @@ def f16_case(orc, m, k, n, seed, bias=True):
     (77, 1280, 5120, 1, 5120, True),  # 13 MB of weights: the split-K ring path rather than one launch
     (100, 10240, 512, 3, 480, True),  # long K, channel-major, split-K ring path
     (200, 4096, 1024, 2, 1024, True), # two 128-row tiles on the split-K ring path
+    (1030, 512, 384, 3, 300, True),   # ring kernel, channel-major, m % 4 != 0: element stores
+    (600, 2048, 256, 3, 200, True),   # split-K ring from 257 rows: channel-major slices, channels < n
+    (999, 4096, 512, 3, 512, True),   # the same with m % 4 != 0 (element stores in the readout)
+    (1000, 2304, 384, 1, 384, True),  # split-K ring from 257 rows, row-major, GELU
 ])
 @pytest.mark.parametrize("split_k", [False, True])
 def test_f16_gemm_epilogue(hip, orc, m, k, n, mode, channels, bias, split_k):
-    """Tiled path, and (split_k) the few-rows split-K path of hb_f16_gemm_ws
-    where the shape allows it (m <= 128)."""
+    """Tiled path, and (split_k) hb_f16_gemm_ws with its workspace: the
+    split-K paths, the ring kernel or the tiled path as the shape selects."""
     ws_bytes = hip.f16_workspace_bytes(m, k, n)
     if split_k and not ws_bytes:
         pytest.skip("m > 128: hb_f16_gemm_ws takes the tiled path")
@@ -540,11 +544,12 @@ def test_f16_ring_matches_tiles(hip, orc, m, k, n, mode, bias, check_oracle):
     xd = hip.DeviceBuffer.from_array(x)
     bd = hip.DeviceBuffer.from_array(b) if bias else None
     y_ring, y_tiles = hip.DeviceBuffer(m * n * 4), hip.DeviceBuffer(m * n * 4)
-    prev = hip.f16_force_stream(0)
+    prev, prev_split = hip.f16_force_stream(0), hip.f16_force_splitk(0)
     try:
         hip.f16_gemm(y_ring, xd, packed, bd, m, k, n, n, mode, workspace=hip.DeviceBuffer(ws_bytes))
     finally:
         hip.f16_force_stream(prev)
+        hip.f16_force_splitk(prev_split)
     hip.f16_gemm(y_tiles, xd, packed, bd, m, k, n, n, mode)
     hip.sync()
     got = y_ring.read(np.uint32, m * n)
@@ -645,6 +650,36 @@ def test_f16_xstream_matches_other_paths(hip, orc, m, k, n, channels, mode, bias
             gotf = got.view(np.float32).reshape(m, n)
             bias_cols = np.abs(b)[None, :] if bias else 0.0
         assert_f16_close(gotf, ref, v_ref, bias_cols, absdot, k)
+
+
+@pytest.mark.parametrize("m,k,n,channels,ring", [
+    (1030, 512, 384, 300, True),    # ring kernel (k < 2048), m % 4 != 0
+    (2500, 1024, 1024, 1000, True), # ring kernel, 160 tiles of 128 x 128
+    (600, 2048, 256, 200, False),   # split-K ring from 257 rows
+    (999, 4096, 512, 512, False),   # split-K ring, m % 4 != 0
+    (2048, 5760, 640, 640, False),  # split-K ring at kRingSplitRows, 80 tiles
+])
+def test_f16_channel_major_matches_row_major(hip, orc, m, k, n, channels, ring):
+    """Mode 3 (channel-major y[channels][m]) gives the bits of mode 0's output
+    transposed on the same path, and on the ring kernel also the bits of the
+    tiled kernel (hb_f16_gemm without a workspace)."""
+    ws = hip.DeviceBuffer(max(hip.f16_workspace_bytes(m, k, n), 256))
+    x, w, perm, b = f16_case(orc, m, k, n, seed=m + k + n + 5, bias=True)
+    packed = hip.f16_prepack(hip.DeviceBuffer.from_array(perm), k, n)
+    xd = hip.DeviceBuffer.from_array(x)
+    bd_rows, bd_ch = hip.DeviceBuffer.from_array(b), hip.DeviceBuffer.from_array(b[:channels].copy())
+    y0, y3, yt = hip.DeviceBuffer(m * n * 4), hip.DeviceBuffer(m * channels * 4), hip.DeviceBuffer(m * channels * 4)
+    y3.fill(0xFF)
+    hip.f16_gemm(y0, xd, packed, bd_rows, m, k, n, n, 0, workspace=ws)
+    hip.f16_gemm(y3, xd, packed, bd_ch, m, k, n, channels, 3, workspace=ws)
+    if ring:
+        hip.f16_gemm(yt, xd, packed, bd_ch, m, k, n, channels, 3)
+    hip.sync()
+    rows = y0.read(np.uint32, m * n).reshape(m, n)
+    got = y3.read(np.uint32, m * channels).reshape(channels, m)
+    np.testing.assert_array_equal(got, np.ascontiguousarray(rows.T[:channels]))
+    if ring:
+        np.testing.assert_array_equal(got, yt.read(np.uint32, m * channels).reshape(channels, m))
 
 
 def test_f16_all_ones_gives_k(hip, orc):
