@@ -2130,10 +2130,24 @@ int ring_splits(int m, int k, int n) {
   return splits < 1 ? 1 : splits;
 }
 
+// 257 to kRingSplitRows rows and k >= 2048: the split-K ring path where
+// 128 x 128 tiles fill at most half of the CUs (the few-tile, long-k
+// products of im2col convolutions).  Measured, us, ring kernel -> split-K,
+// mode 0: 512x11520x1280 71.3 -> 43.5, 1024x11520x1280 84.5 -> 73.5,
+// 1024x4608x512 34.8 -> 25.2, 1024x5760x640 41.3 -> 31.5, 512x5760x1280
+// 38.0 -> 28.3, 2048x4608x512 39.9 -> 38.2, 1024x2880x640 23.4 -> 23.0; at
+// 160 tiles (2048x11520x1280) 122.5 against 120.3.
 constexpr int kRingSplitRows = 2048;
 
+bool wide_splitk_shape(int m, int k, int n) {
+  const long long tiles128 = ((m + 127) / 128) * (long long)((n + 127) / 128);
+  return m > 256 && m <= kRingSplitRows && k >= 2048 && 2 * tiles128 <= compute_units();
+}
+
+// Workspace of the split-K ring path: the fp16 image and the slices; 0 where
+// the path does not run (more than 256 rows outside wide_splitk_shape).
 size_t ring_splitk_bytes(int m, int k, int n) {
-  if (m < 1 || m > kRingSplitRows || k < 32 || n < 32) return 0;
+  if (m < 1 || k < 32 || n < 32 || (m > 256 && !wide_splitk_shape(m, k, n))) return 0;
   const int slices = m <= 256 ? kMaxRingSplits : ring_splits(m, k, n);
   return a_image_bytes(m, k) + (size_t)slices * (size_t)((m + 15) / 16 * 16) * (size_t)n * 4u;
 }
@@ -2170,8 +2184,9 @@ int launch_ring_splitk(float *y, const float *x, const uint16_t *packed, const f
 }
 
 // -1 (default): the split-K ring path by the rules of hb_f16_gemm_ws; 0:
-// never; 1: for every m <= kRingSplitRows with a workspace
-// (hb_f16_force_splitk; HTP_OPS_AMD_F16_SPLITK gives the initial value).
+// never; 1: for every m <= 256 with a workspace, and from 257 rows where the
+// automatic choice takes it (hb_f16_force_splitk; HTP_OPS_AMD_F16_SPLITK
+// gives the initial value).
 std::atomic<int> g_f16_splitk{-2};
 
 int ring_splitk_mode() {
@@ -2446,8 +2461,9 @@ int hb_f16_gemm_ws(float *d_y, const float *d_x, const uint16_t *d_packed, const
   const int xs = xstream_mode();
   if (xs != 0 && xstream_aligned(d_y, d_x, mode) && (xs == 1 || xstream_applies(m, n, mode)))
     return launch_xstream(d_y, d_x, d_packed, d_bias, m, k, n, channels, mode, st);
-  const bool splitk_ok = ring_splitk_mode() != 0 && m <= kRingSplitRows && d_workspace &&
-                         workspace_bytes >= ring_splitk_bytes(m, k, n) && aligned(d_workspace, 256);
+  const size_t splitk_need = ring_splitk_bytes(m, k, n);
+  const bool splitk_ok = ring_splitk_mode() != 0 && splitk_need && d_workspace && workspace_bytes >= splitk_need &&
+                         aligned(d_workspace, 256);
   if (splitk_ok && ring_splitk_mode() == 1)
     return launch_ring_splitk(d_y, d_x, d_packed, d_bias, m, k, n, channels, mode, d_workspace, st);
   // Tiled variant by output size; the split-K paths take over when that grid
@@ -2472,15 +2488,9 @@ int hb_f16_gemm_ws(float *d_y, const float *d_x, const uint16_t *d_packed, const
   const int cf = aligned(d_y, 16) ? small_cf(m, k, n) : 0;
   if (splitk_here && (!cf || (size_t)n * (size_t)k * 2u >= ((size_t)12 << 20)))
     return launch_ring_splitk(d_y, d_x, d_packed, d_bias, m, k, n, channels, mode, d_workspace, st);
-  // 257 to kRingSplitRows rows and k >= 2048: the split-K ring path where
-  // 128 x 128 tiles fill at most half of the CUs (the few-tile, long-k
-  // products of im2col convolutions).  Measured, us, ring kernel -> split-K, mode 0:
-  // 512x11520x1280 71.3 -> 43.5, 1024x11520x1280 84.5 -> 73.5, 1024x4608x512
-  // 34.8 -> 25.2, 1024x5760x640 41.3 -> 31.5, 512x5760x1280 38.0 -> 28.3,
-  // 2048x4608x512 39.9 -> 38.2, 1024x2880x640 23.4 -> 23.0; at 160 tiles
-  // (2048x11520x1280) 122.5 against 120.3.
-  const long long tiles128 = ((m + 127) / 128) * (long long)((n + 127) / 128);
-  if (splitk_ok && m > 256 && k >= 2048 && 2 * tiles128 <= compute_units())
+  // From 257 rows: the split-K ring path wherever it has a workspace
+  // (wide_splitk_shape).
+  if (splitk_ok && m > 256)
     return launch_ring_splitk(d_y, d_x, d_packed, d_bias, m, k, n, channels, mode, d_workspace, st);
   if (cf) return launch_small<0>(cf, d_y, d_x, d_packed, d_bias, m, k, n, channels, mode, st);
   // The split-K path holds m <= 128 rows (8 row fragments) of partial sums.

@@ -372,7 +372,7 @@ def f16_force_xstream(setting):
 
 def f16_force_splitk(setting):
     """Pins the F16 split-K ring path: -1 automatic, 0 never, 1 for every
-    m <= 2048 with a workspace; returns the previous setting."""
+    m <= 256 with a workspace; returns the previous setting."""
     prev = lib().hb_f16_force_splitk(setting)
     if prev < -1:
         check(prev, "hb_f16_force_splitk")

@@ -267,7 +267,8 @@ int hb_f16_force_xstream(int setting);
 /* Pins the split-K ring path of hb_f16_gemm_ws (f16_ring_splitk slices added
  * in order by a readout kernel): -1 restores the automatic choice, 0 never
  * (the ring or tiled kernel, whose sums are those of hb_f16_gemm), 1 for
- * every m <= 2048 given a large enough workspace.  Returns the previous
+ * every m <= 256 given a large enough workspace (from 257 rows it runs only
+ * where the automatic choice takes it).  Returns the previous
  * setting.  Split sums may differ from the unsplit ones in the last fp32 bit
  * before the fp16 readout.  No counterpart in the reference;
  * HTP_OPS_AMD_F16_SPLITK gives the initial value. */

@@ -682,6 +682,17 @@ def test_f16_channel_major_matches_row_major(hip, orc, m, k, n, channels, ring):
         np.testing.assert_array_equal(got, yt.read(np.uint32, m * channels).reshape(channels, m))
 
 
+def test_f16_workspace_covers_only_the_paths_that_run(hip):
+    """The workspace holds split-K slices only for shapes that take the
+    split-K ring path: many output tiles at 2048 rows need the fp16 image
+    alone, few tiles at k >= 2048 the image and the slices."""
+    image = lambda m, k: ((m + 15) // 16 * 16 * k * 2 + 255) // 256 * 256
+    assert hip.f16_workspace_bytes(2048, 1024, 14336) == image(2048, 1024)
+    assert hip.f16_workspace_bytes(2048, 2048, 14336) == image(2048, 2048)
+    assert hip.f16_workspace_bytes(1024, 4608, 512) > image(1024, 4608) + 1024 * 512 * 4
+    assert hip.f16_workspace_bytes(3000, 4608, 512) == image(3000, 4608)
+
+
 def test_f16_all_ones_gives_k(hip, orc):
     m, k, n = 32, 256, 64
     x = np.ones((m, k), np.float32)
