@@ -489,6 +489,7 @@ def f16_case(orc, m, k, n, seed, bias=True):
     (600, 2048, 256, 3, 200, True),   # split-K ring from 257 rows: channel-major slices, channels < n
     (999, 4096, 512, 3, 512, True),   # the same with m % 4 != 0 (element stores in the readout)
     (1000, 2304, 384, 1, 384, True),  # split-K ring from 257 rows, row-major, GELU
+    (256, 11520, 1280, 3, 1280, True),  # a 512x512 UNet's 16x16 3x3 convolution at full size (im2col)
 ])
 @pytest.mark.parametrize("split_k", [False, True])
 def test_f16_gemm_epilogue(hip, orc, m, k, n, mode, channels, bias, split_k):
