@@ -2295,8 +2295,7 @@ bool xstream_aligned(const float *y, const float *x, int mode) {
 // 80.0, 8192x2304x256 41.3 / 40.4, 8192x1152x128 21.8 / 16.0, 4096x1152x128
 // 16.2 / 15.8; the ring kernel ahead at 4096x2304x256 28.5 / 40.4,
 // 4096x4608x512 55.3 / 72.5, 2048x2304x256 23.3 / 40.4.
-bool xstream_applies(int m, int n, int mode) {
-  (void)mode;
+bool xstream_applies(int m, int n) {
   if (n > 512) return false;
   return m >= (n <= 128 ? 4096 : 8192);
 }
@@ -2459,7 +2458,7 @@ int hb_f16_gemm_ws(float *d_y, const float *d_x, const uint16_t *d_packed, const
     return hb_invalid("hb_f16_gemm alignment");
   hipStream_t st = hb_resolve_stream(s);
   const int xs = xstream_mode();
-  if (xs != 0 && xstream_aligned(d_y, d_x, mode) && (xs == 1 || xstream_applies(m, n, mode)))
+  if (xs != 0 && xstream_aligned(d_y, d_x, mode) && (xs == 1 || xstream_applies(m, n)))
     return launch_xstream(d_y, d_x, d_packed, d_bias, m, k, n, channels, mode, st);
   const size_t splitk_need = ring_splitk_bytes(m, k, n);
   const bool splitk_ok = ring_splitk_mode() != 0 && splitk_need && d_workspace && workspace_bytes >= splitk_need &&
